@@ -1,0 +1,325 @@
+"""Benchmark of the torchwarp alignment hot path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--config cfg2] [--all] [--no-cpu]
+
+A "step" is one forward + loss + backward of the configured alignment loss on
+synthetic inputs already resident in HBM (inputs are
+drawn from a CPU ``torch.Generator().manual_seed(0)`` in config order, then
+moved to the GPU). The headline workload is configs[1]: uDTW fp32 fwd+bwd,
+B=256, N=M=140, D=1 -- metric "DP cells/s" (N*M*B per step / step time).
+
+One JSON line is printed with ``roofline`` for the dominant kernel (algorithmic
+bytes per launch / its mean duration, timed with HIP events on the stream the
+kernel runs on) and ``cpu_baseline`` (the CPU oracle, the clean-room
+restatement of the reference's vectorised PyTorch backend, timed on this
+host on a bounded sample). ``--all`` adds one line per config to stderr.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0
+CONFIGS = ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5a", "cfg5b")
+
+
+# ------------------------------------------------------------------ inputs
+
+def _walk(g, B, L):
+    x = torch.cumsum(0.1 * torch.randn(B, L, 1, generator=g), 1)
+    return (x - x.mean(1, keepdim=True)) / x.std(1, keepdim=True)
+
+
+def make_inputs(name, device="cpu", dtype=torch.float32):
+    """Synthetic inputs of one BASELINE config (seed 0, drawn in config order)."""
+    g = torch.Generator().manual_seed(0)
+    if name == "cfg1":
+        t = (torch.randn(32, 64, 1, generator=g), torch.randn(32, 64, 1, generator=g))
+    elif name == "cfg2":
+        X, Y = _walk(g, 256, 140), _walk(g, 256, 140)
+        sx, sy = 0.5 + torch.rand(256, 140, 1, generator=g), 0.5 + torch.rand(256, 140, 1, generator=g)
+        t = (X, Y, sx, sy)
+    elif name == "cfg3":
+        X, Y = torch.randn(64, 1024, 16, generator=g), torch.randn(64, 1024, 16, generator=g)
+        sx, sy = 0.5 + torch.rand(64, 1024, 1, generator=g), 0.5 + torch.rand(64, 1024, 1, generator=g)
+        t = (X, Y, sx, sy)
+    elif name == "cfg4":
+        q = torch.nn.functional.normalize(torch.randn(400, 9, 8, 256, generator=g), dim=-1)
+        s = torch.nn.functional.normalize(torch.randn(400, 8, 256, generator=g), dim=-1)
+        t = (q, s)
+    elif name in ("cfg5a", "cfg5b"):
+        t = (4.0 * torch.rand(1024, 25, 16, 16, generator=g),)
+    else:
+        raise ValueError(name)
+    return tuple(x.to(device=device, dtype=dtype) for x in t)
+
+
+# Work units and algorithmic HBM bytes per fwd+bwd (fp32), BASELINE.md table:
+# inputs read once per pass, outputs written once, carried tensors (R, P)
+# written once and read once.
+def work(name):
+    return {
+        "cfg1": dict(cells=32 * 64 * 64, pairs=32),
+        "cfg2": dict(cells=256 * 140 * 140, pairs=256),
+        "cfg3": dict(cells=64 * 1024 * 1024, pairs=64),
+        "cfg4": dict(cells=400 * 9 * 8 * 8, pairs=400),
+        "cfg5a": dict(cells=1024 * 25 * 16 * 16, pairs=1024),
+        "cfg5b": dict(cells=1024 * 16 * 16, pairs=1024),
+    }[name]
+
+
+def step_fn(name, inputs):
+    """One forward + loss + backward through the public API."""
+    import torchwarp_amd as tw
+    import torchwarp_amd.functional as TF
+
+    if name == "cfg1":
+        m = tw.SoftDTW(gamma=1.0)
+        X, Y = inputs
+
+        def f():
+            x = X.detach().requires_grad_(True)
+            m(x, Y).mean().backward()
+        return f
+    if name in ("cfg2", "cfg3"):
+        gamma = 1.0 if name == "cfg2" else 0.1
+        m = tw.UDTW(gamma=gamma, beta=1.0)
+        X, Y, sx, sy = inputs
+
+        def f():
+            xs = [t.detach().requires_grad_(True) for t in (X, Y, sx, sy)]
+            d, p = m(*xs)
+            (d + p).mean().backward()
+        return f
+    if name == "cfg4":
+        q, s = inputs
+
+        def f():
+            qq, ss = q.detach().requires_grad_(True), s.detach().requires_grad_(True)
+            TF.jeanie(qq, ss, gamma=0.1, max_shift=1).mean().backward()
+        return f
+    (c,) = inputs
+    if name == "cfg5a":
+        def f():
+            cc = c.detach().view(1024, 5, 5, 16, 16).requires_grad_(True)
+            TF.jeanie_from_cost(cc, gamma=0.1, max_shift=1).mean().backward()
+        return f
+
+    def f():
+        cc = c.detach().requires_grad_(True)
+        TF.fvm_from_cost(cc, gamma=0.1).mean().backward()
+    return f
+
+
+# ------------------------------------------------------------- kernel timing
+
+def _hip_call_times(name, inputs, iters):
+    """Mean durations (ms) of the forward and backward DP launches of one config,
+    called through the C ABI and bracketed by HIP events on the same stream.
+    Returns (label, mean_ms, algorithmic_bytes_per_launch) for the dominant one."""
+    from torchwarp_amd import _hip
+    dev = inputs[0].device
+    stream = torch.cuda.current_stream(dev)
+    f32 = torch.float32
+    calls = []
+    if name in ("cfg1", "cfg2", "cfg3"):
+        if name == "cfg1":
+            X, Y = inputs
+            vx = torch.ones(X.shape[:2], device=dev)
+            vy = torch.ones(Y.shape[:2], device=dev)
+            beta, gamma = 0.0, 1.0
+        else:
+            X, Y, sx, sy = inputs
+            vx, vy = sx.squeeze(-1) ** 2, sy.squeeze(-1) ** 2
+            beta, gamma = 1.0, (1.0 if name == "cfg2" else 0.1)
+        B, N, D = X.shape
+        M = Y.shape[1]
+        pen = beta != 0
+        R = X.new_empty(B, N * M)
+        P = X.new_empty(B, N * M) if pen else None
+        o1, o2 = X.new_empty(B), X.new_empty(B)
+        nws = _hip.udtw_workspace_elems(B, N, M, D)
+        ws = X.new_empty(nws) if nws else None
+        wsb = 0 if ws is None else nws * 4
+        g = torch.full((B,), 1.0 / B, device=dev)
+        dX, dY, dvx, dvy = [torch.empty_like(t) for t in (X, Y, vx, vy)]
+        io = 4 * (X.numel() + Y.numel() + vx.numel() + vy.numel())
+        carried = 4 * B * N * M * (2 if pen else 1)
+        calls.append(("udtw_fwd", lambda: _hip.call(
+            "tw_udtw_feat_fwd", f32, X, Y, vx, vy, B, N, M, D, gamma, beta, 1e-8, 0.0, R, P, o1,
+            o2, ws, wsb), io + carried))
+        calls.append(("udtw_bwd", lambda: _hip.call(
+            "tw_udtw_feat_bwd", f32, X, Y, vx, vy, R, P, g, g if pen else None, B, N, M, D, gamma,
+            beta, 1e-8, dX, dY, dvx, dvy, ws, wsb), 2 * io + carried))
+    elif name == "cfg5a":
+        (c,) = inputs
+        B = c.shape[0]
+        R, out = torch.empty_like(c), c.new_empty(B)
+        dC = torch.empty_like(c)
+        g = torch.full((B,), 1.0 / B, device=dev)
+        nb = 4 * c.numel()
+        calls.append(("jeanie_fwd", lambda: _hip.call(
+            "tw_jeanie_cost_fwd", f32, c, B, 5, 5, 16, 16, 0, 1, 1, 0.1, R, out), 2 * nb))
+        calls.append(("jeanie_bwd", lambda: _hip.call(
+            "tw_jeanie_cost_bwd", f32, c, R, g, None, B, 5, 5, 16, 16, 0, 1, 1, 0.1, dC), 3 * nb))
+    else:
+        return None
+    best = None
+    for label, fn, nbytes in calls:
+        fn()
+        torch.cuda.synchronize(dev)
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record(stream)
+        for _ in range(iters):
+            fn()
+        ev1.record(stream)
+        torch.cuda.synchronize(dev)
+        ms = ev0.elapsed_time(ev1) / iters
+        if best is None or ms > best[1]:
+            best = (label, ms, nbytes)
+    return best
+
+
+def _traffic(label, name):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as fh:
+            return json.load(fh).get("{}/{}".format(label, name))
+    except (OSError, ValueError):
+        return None
+
+
+# --------------------------------------------------------------- CPU oracle
+
+def cpu_baseline(name, budget_s=10.0):
+    """The CPU oracle (restatement of the reference's vectorised PyTorch
+    backend) timed on this host, fp32, on the full config batch repeated
+    until ~budget_s of work; returns cells/s."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import jeanie as OJ, udtw as OU
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    inp = make_inputs(name)
+    w = work(name)
+
+    def once():
+        if name in ("cfg1", "cfg2", "cfg3"):
+            if name == "cfg1":
+                X, Y = inp
+                vx = torch.ones(X.shape[:2])
+                vy = torch.ones(Y.shape[:2])
+                beta, gamma = 0.0, 1.0
+            else:
+                X, Y, sx, sy = inp
+                vx, vy = sx.squeeze(-1) ** 2, sy.squeeze(-1) ** 2
+                beta, gamma = 1.0, (1.0 if name == "cfg2" else 0.1)
+            B = X.shape[0]
+            r, p, R, P = OU.features_forward(X, Y, vx, vy, gamma, beta, 1e-8)
+            g = torch.full((B,), 1.0 / B)
+            OU.features_backward(X, Y, vx, vy, R, P, g, g, gamma, beta, 1e-8)
+        elif name == "cfg5a":
+            c = inp[0].view(1024, 5, 5, 16, 16)
+            out, R = OJ.forward(c, 1, 1, 0.1)
+            OJ.backward(c, R, torch.full((1024,), 1 / 1024), 1, 1, 0.1)
+        elif name == "cfg5b":
+            OJ.fvm_backward(inp[0], torch.full((1024,), 1 / 1024), 0.1)
+        else:
+            q, s = inp
+            c = OJ.euclidean_cost(q.requires_grad_(True), s.requires_grad_(True))
+            OJ.jeanie_from_cost(c, gamma=0.1, max_shift=1).mean().backward()
+
+    once()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        once()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 50:
+            break
+    return {"value": w["cells"] * n / el, "unit": "DP cells/s", "cores": cores,
+            "kind": "port",
+            "sample": "{}: full batch fwd+bwd x{} in {:.1f} s, fp32, oracle/ on {} threads"
+                      .format(name, n, el, cores)}
+
+
+# -------------------------------------------------------------------- main
+
+def run_config(name, steps, warmup):
+    dev = torch.device("cuda", 0)
+    inputs = make_inputs(name, dev)
+    f = step_fn(name, inputs)
+    for _ in range(warmup):
+        f()
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        f()
+    torch.cuda.synchronize(dev)
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    w = work(name)
+    return inputs, ms, w["cells"] / (ms * 1e-3), w["pairs"] / (ms * 1e-3)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="cfg2", choices=CONFIGS)
+    ap.add_argument("--all", action="store_true", help="also time every config (stderr)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU; pairs are independent, so N GPUs would "
+              "each run this same per-GPU workload on B/N pairs (no collective inside the op). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    name = args.config
+    inputs, ms, cells_s, pairs_s = run_config(name, args.steps, args.warmup)
+    kt = _hip_call_times(name, inputs, max(args.steps, 10))
+    roof = None
+    if kt is not None:
+        label, kms, nbytes = kt
+        gbs = nbytes / (kms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 5), "traffic": _traffic(label, name),
+                "kernel": label, "kernel_ms": round(kms, 5), "algorithmic_bytes": nbytes}
+    line = {
+        "metric": "DP cells/s fwd+bwd (uDTW B=256 N=M=140)",
+        "value": round(cells_s, 1),
+        "unit": "cells/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": name, "pairs_per_s": round(pairs_s, 1), "cells": work(name)["cells"],
+                   "pairs": work(name)["pairs"]},
+        "roofline": roof,
+        "cpu_baseline": None if args.no_cpu else cpu_baseline(name),
+    }
+    print(json.dumps(line), flush=True)
+    if args.all:
+        for other in CONFIGS:
+            inp, oms, oc, op = run_config(other, max(5, args.steps // 3), 2)
+            kt = _hip_call_times(other, inp, 10)
+            rec = {"config": other, "ms_per_step": round(oms, 4), "cells_per_s": round(oc, 1),
+                   "pairs_per_s": round(op, 1)}
+            if kt is not None:
+                rec.update(kernel=kt[0], kernel_ms=round(kt[1], 5),
+                           hbm_frac=round(kt[2] / (kt[1] * 1e-3) / 1e9 / HBM_PEAK_GBS, 5))
+            print(json.dumps(rec), file=sys.stderr, flush=True)
+
+
+if __name__ == "__main__":
+    main()

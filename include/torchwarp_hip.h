@@ -1,0 +1,181 @@
+/*
+ * torchwarp_hip.h -- C ABI of the gfx950 (MI355X) backend for torchwarp's
+ * alignment hot path: soft-DTW, uncertainty-DTW (uDTW), JEANIE and FVM,
+ * forward and backward, plus the pairwise cost builders.
+ *
+ * Conventions
+ *  - Every pointer is a device pointer; the caller allocates every output and
+ *    workspace buffer (the library never allocates). All tensors are dense
+ *    and row-major in the layout stated for each argument.
+ *  - Launches are asynchronous on `stream`; no host synchronisation.
+ *  - Returns TW_OK (0) or an error code; the message is in tw_last_error()
+ *    (thread-local). B = 0 is a no-op returning TW_OK.
+ *  - _f32 and _f64 variants compute in float / double.
+ *  - "R" and "P" buffers of the uDTW functions are internal tensors carried
+ *    from a forward call to the matching backward call ([B, N*M], opaque
+ *    layout). The JEANIE "R" is the accumulator in the cost's own layout.
+ *
+ * Citations (file:line) are into the reference torchwarp sources
+ * (src/torchwarp/...): each entry point replaces the named pybind function
+ * of the reference CUDA extension and the Python op that wraps it.
+ */
+#ifndef TORCHWARP_HIP_H
+#define TORCHWARP_HIP_H
+
+#include <stddef.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TW_ABI_VERSION 1
+
+#define TW_OK 0
+#define TW_EINVAL 1  /* bad argument */
+#define TW_ELAUNCH 2 /* kernel launch failed */
+#define TW_ESIZE 3   /* problem larger than this build handles / workspace too small */
+
+/* Pairwise metrics (tw_pair_cost_*, tw_jeanie_feat_*). */
+#define TW_METRIC_RAW 0   /* |a|^2 + |b|^2 - 2 a.b, unclamped */
+#define TW_METRIC_SQEUC 1 /* max(., 0)                        */
+#define TW_METRIC_EUC 2   /* sqrt(max(., 0)), zero gradient at 0 */
+
+int tw_version(void);
+const char* tw_last_error(void);
+
+/* ---------------------------------------------------------------- uDTW --
+ * DP on precomputed matrices, N <= M (callers transpose).
+ * Replaces udtw_cuda.cu:624-657 (forward) / :659-690 (backward) and the ops
+ * torchwarp_udtw::dp / dp_backward (udtw/_ops.py:100-138).
+ * cost, pen: [B,N,M]; pen may be NULL (zero penalty, P unused).
+ * R, P: [B, N*M] internal; out_dist, out_pen: [B].
+ * Backward: grad_dist, grad_pen [B] (grad_pen may be NULL iff pen is NULL);
+ * d_cost, d_pen [B,N,M] (d_pen may be NULL). */
+int tw_udtw_cost_fwd_f32(const float* cost, const float* pen, int B, int N, int M, float gamma,
+                         float bandwidth, float* R, float* P, float* out_dist, float* out_pen,
+                         hipStream_t stream);
+int tw_udtw_cost_fwd_f64(const double* cost, const double* pen, int B, int N, int M,
+                         double gamma, double bandwidth, double* R, double* P, double* out_dist,
+                         double* out_pen, hipStream_t stream);
+int tw_udtw_cost_bwd_f32(const float* cost, const float* pen, const float* R, const float* P,
+                         const float* grad_dist, const float* grad_pen, int B, int N, int M,
+                         float gamma, float* d_cost, float* d_pen, hipStream_t stream);
+int tw_udtw_cost_bwd_f64(const double* cost, const double* pen, const double* R,
+                         const double* P, const double* grad_dist, const double* grad_pen, int B,
+                         int N, int M, double gamma, double* d_cost, double* d_pen,
+                         hipStream_t stream);
+
+/* uDTW straight from the features, N <= M. Replaces udtw_cuda.cu:738-775
+ * (fused_forward) / :777-814 (fused_backward) together with the bmm / vecdot /
+ * diagonal permutations of the ops torchwarp_udtw::fused / fused_backward
+ * (udtw/_ops.py:157-211). X [B,N,D], Y [B,M,D], vx [B,N], vy [B,M] (sigma^2).
+ * beta == 0 (soft-DTW) skips the penalty: P may be NULL, out_pen gets 0.
+ * D == 1 runs fully fused; D > 1 needs workspace of
+ * tw_udtw_feat_workspace_bytes(...) bytes. Backward writes dX [B,N,D],
+ * dY [B,M,D] and, unless both are NULL, dvx [B,N], dvy [B,M]. */
+size_t tw_udtw_feat_workspace_bytes(int B, int N, int M, int D, int elem_size);
+int tw_udtw_feat_fwd_f32(const float* X, const float* Y, const float* vx, const float* vy, int B,
+                         int N, int M, int D, float gamma, float beta, float eps,
+                         float bandwidth, float* R, float* P, float* out_dist, float* out_pen,
+                         float* workspace, size_t workspace_bytes, hipStream_t stream);
+int tw_udtw_feat_fwd_f64(const double* X, const double* Y, const double* vx, const double* vy,
+                         int B, int N, int M, int D, double gamma, double beta, double eps,
+                         double bandwidth, double* R, double* P, double* out_dist,
+                         double* out_pen, double* workspace, size_t workspace_bytes,
+                         hipStream_t stream);
+int tw_udtw_feat_bwd_f32(const float* X, const float* Y, const float* vx, const float* vy,
+                         const float* R, const float* P, const float* grad_dist,
+                         const float* grad_pen, int B, int N, int M, int D, float gamma,
+                         float beta, float eps, float* dX, float* dY, float* dvx, float* dvy,
+                         float* workspace, size_t workspace_bytes, hipStream_t stream);
+int tw_udtw_feat_bwd_f64(const double* X, const double* Y, const double* vx, const double* vy,
+                         const double* R, const double* P, const double* grad_dist,
+                         const double* grad_pen, int B, int N, int M, int D, double gamma,
+                         double beta, double eps, double* dX, double* dY, double* dvx,
+                         double* dvy, double* workspace, size_t workspace_bytes,
+                         hipStream_t stream);
+
+/* -------------------------------------------------------------- JEANIE --
+ * 3-D DP on a cost [B, K1*K2, T, U] (swap_tu = 0) or [B, K1*K2, U, T]
+ * (swap_tu = 1: the DP runs on the transposed grid, T <= U required).
+ * Shifts are clamped to K-1. R: accumulator, same layout as cost; out: [B].
+ * Replaces jeanie_cuda.cu:564-587 (forward) / :589-619 (backward) and the
+ * ops torchwarp_jeanie::dp / dp_backward (jeanie/_ops.py:110-139).
+ * grad_R (dL/dR, same layout) may be NULL. */
+int tw_jeanie_cost_fwd_f32(const float* cost, int B, int K1, int K2, int T, int U, int swap_tu,
+                           int s1, int s2, float gamma, float* R, float* out, hipStream_t stream);
+int tw_jeanie_cost_fwd_f64(const double* cost, int B, int K1, int K2, int T, int U, int swap_tu,
+                           int s1, int s2, double gamma, double* R, double* out,
+                           hipStream_t stream);
+int tw_jeanie_cost_bwd_f32(const float* cost, const float* R, const float* grad_out,
+                           const float* grad_R, int B, int K1, int K2, int T, int U, int swap_tu,
+                           int s1, int s2, float gamma, float* d_cost, hipStream_t stream);
+int tw_jeanie_cost_bwd_f64(const double* cost, const double* R, const double* grad_out,
+                           const double* grad_R, int B, int K1, int K2, int T, int U,
+                           int swap_tu, int s1, int s2, double gamma, double* d_cost,
+                           hipStream_t stream);
+
+/* JEANIE from features: query [B, K1*K2, T, D], support [B, U, D],
+ * metric TW_METRIC_SQEUC or TW_METRIC_EUC. Writes the cost [B, K1*K2, T, U]
+ * (saved for the backward), the accumulator R (same layout) and out [B].
+ * Replaces jeanie_cuda.cu:621-648 / :650-683 with the ops
+ * torchwarp_jeanie::features / features_backward (jeanie/_ops.py:155-230).
+ * Backward workspace: B*K1*K2*T*U elements. */
+int tw_jeanie_feat_fwd_f32(const float* query, const float* support, int B, int K1, int K2, int T,
+                           int U, int D, int s1, int s2, float gamma, int metric, float* cost,
+                           float* R, float* out, hipStream_t stream);
+int tw_jeanie_feat_fwd_f64(const double* query, const double* support, int B, int K1, int K2,
+                           int T, int U, int D, int s1, int s2, double gamma, int metric,
+                           double* cost, double* R, double* out, hipStream_t stream);
+int tw_jeanie_feat_bwd_f32(const float* query, const float* support, const float* cost,
+                           const float* R, const float* grad_out, const float* grad_R, int B,
+                           int K1, int K2, int T, int U, int D, int s1, int s2, float gamma,
+                           int metric, float* d_query, float* d_support, float* workspace,
+                           hipStream_t stream);
+int tw_jeanie_feat_bwd_f64(const double* query, const double* support, const double* cost,
+                           const double* R, const double* grad_out, const double* grad_R, int B,
+                           int K1, int K2, int T, int U, int D, int s1, int s2, double gamma,
+                           int metric, double* d_query, double* d_support, double* workspace,
+                           hipStream_t stream);
+
+/* ----------------------------------------------------------------- FVM --
+ * fvm_from_cost (jeanie/fvm.py:15-38: logsumexp over the viewpoints, then
+ * soft_dtw_from_cost, sdtw.py:29-47) on cost [B, K, T, U], K = product of
+ * the viewpoint dims. temporal: [B, T*U] (saved), R: [B, T*U] internal,
+ * out [B], scratch [B]. Backward workspace: B*T*U elements. */
+int tw_fvm_cost_fwd_f32(const float* cost, int B, int K, int T, int U, float gamma,
+                        float* temporal, float* R, float* out, float* scratch,
+                        hipStream_t stream);
+int tw_fvm_cost_fwd_f64(const double* cost, int B, int K, int T, int U, double gamma,
+                        double* temporal, double* R, double* out, double* scratch,
+                        hipStream_t stream);
+int tw_fvm_cost_bwd_f32(const float* cost, const float* temporal, const float* R,
+                        const float* grad_out, int B, int K, int T, int U, float gamma,
+                        float* d_cost, float* workspace, hipStream_t stream);
+int tw_fvm_cost_bwd_f64(const double* cost, const double* temporal, const double* R,
+                        const double* grad_out, int B, int K, int T, int U, double gamma,
+                        double* d_cost, double* workspace, hipStream_t stream);
+
+/* ------------------------------------------------------- pairwise cost --
+ * A [P, R, D] against Bm [P, C, D] -> cost [P, R, C] with a TW_METRIC_*.
+ * Replaces euclidean_cost / squared_euclidean_cost (jeanie/distances.py:15-38)
+ * and the Gram + norm construction of udtw/_ops.py:164-165,
+ * jeanie/_ops.py:162-167. Backward: d_cost -> dA [P,R,D], dB [P,C,D]
+ * (cost is needed for the SQEUC / EUC masks; NULL allowed for RAW). */
+int tw_pair_cost_fwd_f32(const float* A, const float* Bm, int P, int R, int C, int D, int metric,
+                         float* cost, hipStream_t stream);
+int tw_pair_cost_fwd_f64(const double* A, const double* Bm, int P, int R, int C, int D,
+                         int metric, double* cost, hipStream_t stream);
+int tw_pair_cost_bwd_f32(const float* A, const float* Bm, const float* cost, const float* d_cost,
+                         int P, int R, int C, int D, int metric, float* dA, float* dB,
+                         hipStream_t stream);
+int tw_pair_cost_bwd_f64(const double* A, const double* Bm, const double* cost,
+                         const double* d_cost, int P, int R, int C, int D, int metric,
+                         double* dA, double* dB, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TORCHWARP_HIP_H */

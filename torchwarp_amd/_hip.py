@@ -1,0 +1,135 @@
+"""ctypes binding of ``libtorchwarp_hip.so`` (C ABI in ``include/torchwarp_hip.h``).
+
+Replaces the reference's JIT loader (``src/torchwarp/_cuda.py:29-73``): the
+library is built ahead of time (``torchwarp_amd/build.py``) and loaded from
+this package directory. There is no fallback: when the library or a ROCm
+device is missing, every entry point raises. PyTorch provides device memory
+and the current stream; the library launches its own kernels on that stream.
+"""
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "libtorchwarp_hip.so"
+
+# argument codes: p pointer, i int, f real (float or double by suffix),
+# z size_t, s stream
+SIGNATURES = {
+    "tw_udtw_cost_fwd": "ppiiiffpppps",
+    "tw_udtw_cost_bwd": "ppppppiiifpps",
+    "tw_udtw_feat_fwd": "ppppiiiiffffpppppzs",
+    "tw_udtw_feat_bwd": "ppppppppiiiifffpppppzs",
+    "tw_jeanie_cost_fwd": "piiiiiiiifpps",
+    "tw_jeanie_cost_bwd": "ppppiiiiiiiifps",
+    "tw_jeanie_feat_fwd": "ppiiiiiiiifippps",
+    "tw_jeanie_feat_bwd": "ppppppiiiiiiiifippps",
+    "tw_fvm_cost_fwd": "piiiifpppps",
+    "tw_fvm_cost_bwd": "ppppiiiifpps",
+    "tw_pair_cost_fwd": "ppiiiiips",
+    "tw_pair_cost_bwd": "ppppiiiiipps",
+}
+
+METRIC_RAW, METRIC_SQEUC, METRIC_EUC = 0, 1, 2
+
+_lib = None
+_error = None
+
+
+def _ctype(code, real):
+    return {"p": ctypes.c_void_p, "i": ctypes.c_int, "f": real, "z": ctypes.c_size_t,
+            "s": ctypes.c_void_p}[code]
+
+
+def _load():
+    global _lib, _error
+    if _lib is not None or _error is not None:
+        return _lib
+    if os.environ.get("TORCHWARP_NO_CUDA") == "1":
+        _error = RuntimeError("disabled by TORCHWARP_NO_CUDA=1")
+        return None
+    try:
+        lib = ctypes.CDLL(str(LIB_PATH))
+    except OSError as exc:
+        _error = RuntimeError("cannot load {} ({}); build it with "
+                              "`python -m torchwarp_amd.build`".format(LIB_PATH, exc))
+        return None
+    lib.tw_last_error.restype = ctypes.c_char_p
+    lib.tw_version.restype = ctypes.c_int
+    lib.tw_udtw_feat_workspace_bytes.restype = ctypes.c_size_t
+    lib.tw_udtw_feat_workspace_bytes.argtypes = [ctypes.c_int] * 5
+    for base, sig in SIGNATURES.items():
+        for suffix, real in (("_f32", ctypes.c_float), ("_f64", ctypes.c_double)):
+            fn = getattr(lib, base + suffix)
+            fn.restype = ctypes.c_int
+            fn.argtypes = [_ctype(c, real) for c in sig]
+    _lib = lib
+    return lib
+
+
+def library():
+    """The loaded library; raises RuntimeError if it cannot be loaded."""
+    lib = _load()
+    if lib is None:
+        raise _error
+    return lib
+
+
+def build_error():
+    _load()
+    return _error
+
+
+def available():
+    """True when the HIP library loads and a ROCm device is present."""
+    return _load() is not None and torch.cuda.is_available()
+
+
+def _arg(x):
+    if x is None:
+        return None
+    if isinstance(x, torch.Tensor):
+        return ctypes.c_void_p(x.data_ptr()) if x.numel() else None
+    return x
+
+
+def call(base, dtype, *args):
+    """Call ``base``_f32/_f64 on the current stream of the first tensor's device."""
+    lib = library()
+    suffix = {torch.float32: "_f32", torch.float64: "_f64"}.get(dtype)
+    if suffix is None:
+        raise TypeError("torchwarp_amd computes in float32 or float64, got {}".format(dtype))
+    dev = next(a.device for a in args if isinstance(a, torch.Tensor))
+    with torch.cuda.device(dev):
+        stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+        rc = getattr(lib, base + suffix)(*[_arg(a) for a in args], stream)
+    if rc != 0:
+        raise RuntimeError("torchwarp_amd: " + lib.tw_last_error().decode())
+
+
+def udtw_workspace_elems(B, N, M, D):
+    return library().tw_udtw_feat_workspace_bytes(B, N, M, D, 1)
+
+
+def check_backend(backend):
+    if backend not in ("auto", "cuda", "torch"):
+        raise ValueError("backend must be 'auto', 'cuda' or 'torch'")
+
+
+def require(t, backend, what):
+    """Every computation runs on the HIP kernels; say so loudly otherwise."""
+    check_backend(backend)
+    if backend == "torch":
+        raise ValueError(
+            "{}: backend='torch' (the reference's portable PyTorch dynamic program) is not part "
+            "of torchwarp_amd, which runs the HIP kernels only; use backend='auto' or "
+            "'cuda'".format(what))
+    if not t.is_cuda:
+        raise RuntimeError(
+            "{}: torchwarp_amd runs on ROCm GPUs only; move the inputs to a 'cuda' device "
+            "(got a {} tensor)".format(what, t.device.type))
+    if t.dtype not in (torch.float32, torch.float64):
+        raise TypeError("{}: expected float32 or float64, got {}".format(what, t.dtype))
+    library()

@@ -1,0 +1,69 @@
+"""Shared plumbing of the custom operators: vmap rules, autocast, derivative helpers.
+
+Same operator contract as the reference (``udtw/_ops.py:60-95``,
+``jeanie/_ops.py:67-105``): each op folds a vmapped dimension into its batch
+dimension, runs in float32 under autocast, and the ``autograd.Function``
+wrappers route first-order reverse mode to the HIP backward op while forward
+mode and derivatives of a backward go through ``torch.func`` on the
+autograd-native restatement.
+"""
+
+import torch
+from torch import Tensor
+
+
+def register_vmap(op, n_tensors):
+    """vmap rule: fold the vmapped dimension into the leading batch dimension."""
+    def rule(info, in_dims, *args):
+        V = info.batch_size
+        folded = []
+        for k, (a, d) in enumerate(zip(args, in_dims)):
+            if k < n_tensors and isinstance(a, Tensor):
+                a = a.unsqueeze(0).expand(V, *a.shape) if d is None else a.movedim(d, 0)
+                a = a.reshape(V * a.shape[1], *a.shape[2:]).contiguous()
+            folded.append(a)
+        outs = op(*folded)
+        single = not isinstance(outs, tuple)
+        outs = (outs,) if single else outs
+        outs = tuple(o.reshape(V, o.shape[0] // V, *o.shape[1:]) if o.numel() else o.new_empty(V, 0)
+                     for o in outs)
+        if single:
+            return outs[0], 0
+        return outs, tuple(0 for _ in outs)
+    op.register_vmap(rule)
+
+
+def register_autocast(op):
+    for device in ("cuda", "cpu"):
+        torch.library.register_autocast(op, device, torch.float32)
+
+
+def zeros_if_none(g, like):
+    return torch.zeros_like(like) if g is None else g
+
+
+def jvp_of(f, primals, tangents):
+    """J t of f at primals (inputs made dense: jacrev hands over expanded tensors)."""
+    primals = tuple(p.contiguous() for p in primals)
+    tangents = tuple(t.contiguous() for t in tangents)
+    return torch.func.jvp(f, primals, tangents)[1]
+
+
+def vjp_of(f, primals, cotangents):
+    """J^T v of f at primals, itself differentiable."""
+    _, pullback = torch.func.vjp(f, *primals)
+    return pullback(tuple(cotangents))
+
+
+def without_jvp(cls):
+    """Twin of an autograd.Function without ``jvp`` (dynamo cannot trace one that has it)."""
+    ns = {k: v for k, v in vars(cls).items() if k not in ("jvp", "__dict__", "__weakref__")}
+    return type(cls.__name__ + "Compiled", (torch.autograd.Function,), ns)
+
+
+def pick(cls, compiled):
+    def apply(*args):
+        if torch.compiler.is_compiling():
+            return compiled.apply(*args)
+        return cls.apply(*args)
+    return apply

@@ -1,0 +1,477 @@
+// JEANIE temporal-viewpoint DP for gfx950 (cost path), forward and backward.
+//
+// Reference: jeanie_cuda.cu:144-295 (kernels), jeanie/_torch_dp.py:14-75,
+// jeanie/functional.py:28-61. For a pair b, viewpoints n = (n1, n2) on a
+// K1 x K2 grid and temporal cells (t, u):
+//   R[n,0,0] = C[n,0,0]
+//   R[n,t,u] = C[n,t,u] + softmin_g{ R[n',t',u'] : |n1'-n1| <= s1, |n2'-n2| <= s2,
+//                                   (t',u') in {(t-1,u), (t,u-1), (t-1,u-1)} }
+//   out      = softmin_g{ R[n,T-1,U-1] }
+// Backward: Rbar_k = sum_s 2^((E_s - R_k) log2(e)/g) Rbar_s (+ dL/dR_k),
+// E_s = R_s - C_s, seeded with grad_out * softmax_n(-R[n,T-1,U-1]/g); dC = Rbar.
+//
+// Layout: C, R, dL/dR and dC share one natural layout [B, K1*K2, T, U]; with
+// `swap` set, the (t, u) plane is stored transposed ([U, T]) -- the DP runs on
+// the T <= U orientation without copying the caller's tensor. R is the true
+// (unscaled) accumulator, since callers may request it.
+//
+// One workgroup per pair; each diagonal's cells (t, n) are spread over the
+// threads. The two previous diagonals live in LDS (3 rolling slabs of T*K);
+// when they do not fit, the kernel reads them back from the R output in
+// global memory (full-fence barrier per diagonal).
+
+#include "tw_capi.hpp"
+#include "tw_common.hpp"
+#include "../../include/torchwarp_hip.h"
+
+namespace tw {
+
+template <typename T>
+struct JeanieArgs {
+  const T* C;
+  const T* R;   // backward input
+  T* Rw;        // forward output
+  T* out;
+  const T* gout;
+  const T* gR;
+  T* dC;
+  int K1, K2, K, Tn, Un, s1, s2;
+  int swap;
+  T k;       // log2(e) / gamma
+  T inv_k;   // gamma ln 2
+};
+
+template <typename T>
+__device__ __forceinline__ size_t jidx(const JeanieArgs<T>& a, int n, int t, int u) {
+  const size_t plane = (size_t)a.Tn * a.Un;
+  return (size_t)n * plane + (a.swap ? (size_t)u * a.Tn + t : (size_t)t * a.Un + u);
+}
+
+template <typename T, bool LDSBUF>
+__global__ void __launch_bounds__(1024) jeanie_fwd_kernel(JeanieArgs<T> a) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* buf = reinterpret_cast<T*>(smem_raw);   // [3][T*K] (LDSBUF)
+  const int K = a.K, Tn = a.Tn, Un = a.Un, K2 = a.K2;
+  const int b = blockIdx.x;
+  const size_t pair = (size_t)K * Tn * Un;
+  const T* Cb = a.C + b * pair;
+  T* Rb = a.Rw + b * pair;
+  const int slab = Tn * K;
+  const T INF = inf_v<T>();
+  const int Dn = Tn + Un - 1;
+
+  // R of a cell on a previous diagonal
+  auto Rget = [&](int d, int t, int n) -> T {
+    if (LDSBUF) return buf[(d % 3) * slab + t * K + n];
+    return Rb[jidx(a, n, t, d - t)];
+  };
+
+  for (int d = 0; d < Dn; ++d) {
+    const int lo = max(0, d - Un + 1), hi = min(Tn - 1, d);
+    const int cells = (hi - lo + 1) * K;
+    for (int idx = threadIdx.x; idx < cells; idx += blockDim.x) {
+      const int t = lo + idx / K, n = idx - (idx / K) * K, u = d - t;
+      const size_t o = jidx(a, n, t, u);
+      T rv = Cb[o];
+      if (d > 0) {
+        const int n1 = n / K2, n2 = n - n1 * K2;
+        const int a1lo = max(0, n1 - a.s1), a1hi = min(a.K1 - 1, n1 + a.s1);
+        const int a2lo = max(0, n2 - a.s2), a2hi = min(K2 - 1, n2 + a.s2);
+        T m = INF;
+        for (int a1 = a1lo; a1 <= a1hi; ++a1)
+          for (int a2 = a2lo; a2 <= a2hi; ++a2) {
+            const int pn = a1 * K2 + a2;
+            if (t > 0) m = fmin(m, Rget(d - 1, t - 1, pn));
+            if (u > 0) m = fmin(m, Rget(d - 1, t, pn));
+            if (t > 0 && u > 0) m = fmin(m, Rget(d - 2, t - 1, pn));
+          }
+        T s = 0;
+        for (int a1 = a1lo; a1 <= a1hi; ++a1)
+          for (int a2 = a2lo; a2 <= a2hi; ++a2) {
+            const int pn = a1 * K2 + a2;
+            if (t > 0) s += ex2((m - Rget(d - 1, t - 1, pn)) * a.k);
+            if (u > 0) s += ex2((m - Rget(d - 1, t, pn)) * a.k);
+            if (t > 0 && u > 0) s += ex2((m - Rget(d - 2, t - 1, pn)) * a.k);
+          }
+        rv += m - a.inv_k * lg2(s);
+      }
+      if (LDSBUF) buf[(d % 3) * slab + t * K + n] = rv;
+      Rb[o] = rv;
+    }
+    if (LDSBUF)
+      lds_barrier();
+    else
+      __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    T m = INF;
+    for (int n = 0; n < K; ++n) m = fmin(m, Rget(Dn - 1, Tn - 1, n));
+    T s = 0;
+    for (int n = 0; n < K; ++n) s += ex2((m - Rget(Dn - 1, Tn - 1, n)) * a.k);
+    a.out[b] = m - a.inv_k * lg2(s);
+  }
+}
+
+template <typename T, bool LDSBUF>
+__global__ void __launch_bounds__(1024) jeanie_bwd_kernel(JeanieArgs<T> a) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* Gb = reinterpret_cast<T*>(smem_raw);    // Rbar  [3][T*K] (LDSBUF)
+  const int K = a.K, Tn = a.Tn, Un = a.Un, K2 = a.K2;
+  const int slab = Tn * K;
+  T* Eb = Gb + 3 * slab;                     // R - C [3][T*K] (LDSBUF)
+  __shared__ T fin_s;
+  const int b = blockIdx.x;
+  const size_t pair = (size_t)K * Tn * Un;
+  const T* Cb = a.C + b * pair;
+  const T* Rb = a.R + b * pair;
+  const T* gRb = a.gR ? a.gR + b * pair : nullptr;
+  T* dCb = a.dC + b * pair;
+  const T INF = inf_v<T>();
+  const int Dn = Tn + Un - 1;
+  const T gout = a.gout[b];
+
+  auto Gget = [&](int d, int t, int n) -> T {
+    if (LDSBUF) return Gb[(d % 3) * slab + t * K + n];
+    return dCb[jidx(a, n, t, d - t)];
+  };
+  auto Eget = [&](int d, int t, int n) -> T {
+    if (LDSBUF) return Eb[(d % 3) * slab + t * K + n];
+    const size_t o = jidx(a, n, t, d - t);
+    return Rb[o] - Cb[o];
+  };
+
+  if (threadIdx.x == 0) {
+    T m = INF;
+    for (int n = 0; n < K; ++n) m = fmin(m, Rb[jidx(a, n, Tn - 1, Un - 1)]);
+    T s = 0;
+    for (int n = 0; n < K; ++n) s += ex2((m - Rb[jidx(a, n, Tn - 1, Un - 1)]) * a.k);
+    fin_s = m - a.inv_k * lg2(s);
+  }
+  __syncthreads();
+  const T fin = fin_s;
+
+  for (int d = Dn - 1; d >= 0; --d) {
+    const int lo = max(0, d - Un + 1), hi = min(Tn - 1, d);
+    const int cells = (hi - lo + 1) * K;
+    for (int idx = threadIdx.x; idx < cells; idx += blockDim.x) {
+      const int t = lo + idx / K, n = idx - (idx / K) * K, u = d - t;
+      const size_t o = jidx(a, n, t, u);
+      const T rk = Rb[o];
+      T acc;
+      if (d == Dn - 1) {
+        acc = gout * ex2((fin - rk) * a.k);
+      } else {
+        const int n1 = n / K2, n2 = n - n1 * K2;
+        const int a1lo = max(0, n1 - a.s1), a1hi = min(a.K1 - 1, n1 + a.s1);
+        const int a2lo = max(0, n2 - a.s2), a2hi = min(K2 - 1, n2 + a.s2);
+        acc = 0;
+        for (int a1 = a1lo; a1 <= a1hi; ++a1)
+          for (int a2 = a2lo; a2 <= a2hi; ++a2) {
+            const int sn = a1 * K2 + a2;
+            if (t + 1 < Tn) acc += ex2((Eget(d + 1, t + 1, sn) - rk) * a.k) * Gget(d + 1, t + 1, sn);
+            if (u + 1 < Un) acc += ex2((Eget(d + 1, t, sn) - rk) * a.k) * Gget(d + 1, t, sn);
+            if (t + 1 < Tn && u + 1 < Un)
+              acc += ex2((Eget(d + 2, t + 1, sn) - rk) * a.k) * Gget(d + 2, t + 1, sn);
+          }
+      }
+      if (gRb) acc += gRb[o];
+      if (LDSBUF) {
+        Gb[(d % 3) * slab + t * K + n] = acc;
+        Eb[(d % 3) * slab + t * K + n] = rk - Cb[o];
+      }
+      dCb[o] = acc;
+    }
+    if (LDSBUF)
+      lds_barrier();
+    else
+      __syncthreads();
+  }
+}
+
+static int jeanie_threads(int cells) {
+  int t = ((cells + 63) / 64) * 64;
+  return t < 64 ? 64 : (t > 1024 ? 1024 : t);
+}
+
+template <typename T>
+static int jeanie_check(const char* what, int B, int K1, int K2, int Tn, int Un, int s1, int s2,
+                        double gamma) {
+  if (B < 0 || K1 <= 0 || K2 <= 0 || Tn <= 0 || Un <= 0)
+    return fail(TW_EINVAL, "%s: bad sizes", what);
+  if (s1 < 0 || s2 < 0) return fail(TW_EINVAL, "%s: shifts must be >= 0", what);
+  if (!(gamma > 0)) return fail(TW_EINVAL, "%s: gamma must be > 0", what);
+  if (Tn > Un) return fail(TW_EINVAL, "%s: expected T <= U after orientation", what);
+  return TW_OK;
+}
+
+template <typename T>
+static void jeanie_fill(JeanieArgs<T>& a, int K1, int K2, int Tn, int Un, int s1, int s2,
+                        int swap, double gamma) {
+  a.K1 = K1;
+  a.K2 = K2;
+  a.K = K1 * K2;
+  a.Tn = Tn;
+  a.Un = Un;
+  a.s1 = s1 < K1 - 1 ? s1 : K1 - 1;
+  a.s2 = s2 < K2 - 1 ? s2 : K2 - 1;
+  a.swap = swap;
+  a.k = (T)(1.4426950408889634 / gamma);
+  a.inv_k = (T)(gamma * 0.6931471805599453);
+}
+
+template <typename T>
+int jeanie_cost_fwd(const T* C, int B, int K1, int K2, int Tn, int Un, int swap, int s1, int s2,
+                    double gamma, T* R, T* out, hipStream_t s, const char* what) {
+  if (int e = jeanie_check<T>(what, B, K1, K2, Tn, Un, s1, s2, gamma)) return e;
+  if (!C || !R || !out) return fail(TW_EINVAL, "%s: null pointer", what);
+  if (B == 0) return TW_OK;
+  JeanieArgs<T> a = {};
+  a.C = C;
+  a.Rw = R;
+  a.out = out;
+  jeanie_fill(a, K1, K2, Tn, Un, s1, s2, swap, gamma);
+  const int threads = jeanie_threads(Tn * a.K);
+  const size_t lds = (size_t)3 * Tn * a.K * sizeof(T);
+  if (lds <= (size_t)max_lds_bytes())
+    hipLaunchKernelGGL((jeanie_fwd_kernel<T, true>), dim3(B), dim3(threads), lds, s, a);
+  else
+    hipLaunchKernelGGL((jeanie_fwd_kernel<T, false>), dim3(B), dim3(threads), 0, s, a);
+  return check_launch(what);
+}
+
+template <typename T>
+int jeanie_cost_bwd(const T* C, const T* R, const T* gout, const T* gR, int B, int K1, int K2,
+                    int Tn, int Un, int swap, int s1, int s2, double gamma, T* dC, hipStream_t s,
+                    const char* what) {
+  if (int e = jeanie_check<T>(what, B, K1, K2, Tn, Un, s1, s2, gamma)) return e;
+  if (!C || !R || !gout || !dC) return fail(TW_EINVAL, "%s: null pointer", what);
+  if (B == 0) return TW_OK;
+  JeanieArgs<T> a = {};
+  a.C = C;
+  a.R = R;
+  a.gout = gout;
+  a.gR = gR;
+  a.dC = dC;
+  jeanie_fill(a, K1, K2, Tn, Un, s1, s2, swap, gamma);
+  const int threads = jeanie_threads(Tn * a.K);
+  const size_t lds = (size_t)6 * Tn * a.K * sizeof(T);
+  if (lds + sizeof(T) <= (size_t)max_lds_bytes())
+    hipLaunchKernelGGL((jeanie_bwd_kernel<T, true>), dim3(B), dim3(threads), lds, s, a);
+  else
+    hipLaunchKernelGGL((jeanie_bwd_kernel<T, false>), dim3(B), dim3(threads), 0, s, a);
+  return check_launch(what);
+}
+
+// ----------------------------------------------------------------- FVM
+// Viewpoint softmin at every temporal cell (jeanie/fvm.py:36-37):
+//   temporal[t,u] = -g ln sum_n exp(-C[n,t,u]/g)
+// written in the DP orientation ([U,T] when `swap`), and its adjoint
+//   dC[n,t,u] = exp((temporal[t,u] - C[n,t,u])/g) * dtemporal[t,u].
+
+template <typename T>
+__global__ void __launch_bounds__(256) fvm_softmin_fwd(const T* __restrict__ C, T* __restrict__ tmp,
+                                                       int K, int Tn, int Un, int swap, T k,
+                                                       T inv_k) {
+  const int b = blockIdx.y;
+  const int cell = blockIdx.x * blockDim.x + threadIdx.x;
+  const int plane = Tn * Un;
+  if (cell >= plane) return;
+  const T* c = C + (size_t)b * K * plane + cell;
+  T m = inf_v<T>();
+  for (int n = 0; n < K; ++n) m = fmin(m, c[(size_t)n * plane]);
+  T s = 0;
+  for (int n = 0; n < K; ++n) s += ex2((m - c[(size_t)n * plane]) * k);
+  const int t = cell / Un, u = cell - t * Un;
+  const int o = swap ? u * Tn + t : cell;
+  tmp[(size_t)b * plane + o] = m - inv_k * lg2(s);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) fvm_softmin_bwd(const T* __restrict__ C,
+                                                       const T* __restrict__ tmp,
+                                                       const T* __restrict__ dtmp,
+                                                       T* __restrict__ dC, int K, int Tn, int Un,
+                                                       int swap, T k) {
+  const int b = blockIdx.y;
+  const int cell = blockIdx.x * blockDim.x + threadIdx.x;
+  const int plane = Tn * Un;
+  if (cell >= plane) return;
+  const int t = cell / Un, u = cell - t * Un;
+  const int o = swap ? u * Tn + t : cell;
+  const T tv = tmp[(size_t)b * plane + o], g = dtmp[(size_t)b * plane + o];
+  const T* c = C + (size_t)b * K * plane + cell;
+  T* dc = dC + (size_t)b * K * plane + cell;
+  for (int n = 0; n < K; ++n) dc[(size_t)n * plane] = ex2((tv - c[(size_t)n * plane]) * k) * g;
+}
+
+template <typename T>
+int udtw_cost_fwd_any(const T* C, const T* Q, int B, int N, int M, double gamma, double band,
+                      T* R, T* P, T* out_r, T* out_p, hipStream_t s, const char* what);
+template <typename T>
+int udtw_cost_bwd_any(const T* C, const T* Q, const T* R, const T* P, const T* gr, const T* gp,
+                      int B, int N, int M, double gamma, T* dC, T* dQ, hipStream_t s,
+                      const char* what);
+
+template <typename T>
+int fvm_fwd(const T* C, int B, int K, int Tn, int Un, double gamma, T* tmp, T* R, T* out,
+            T* pen_scratch, hipStream_t s, const char* what) {
+  if (B < 0 || K <= 0 || Tn <= 0 || Un <= 0 || !(gamma > 0))
+    return fail(TW_EINVAL, "%s: bad arguments", what);
+  if (!C || !tmp || !R || !out || !pen_scratch) return fail(TW_EINVAL, "%s: null pointer", what);
+  if (B == 0) return TW_OK;
+  const int swap = Tn > Un;
+  const T k = (T)(1.4426950408889634 / gamma), inv_k = (T)(gamma * 0.6931471805599453);
+  dim3 grid((Tn * Un + 255) / 256, B);
+  hipLaunchKernelGGL((fvm_softmin_fwd<T>), grid, dim3(256), 0, s, C, tmp, K, Tn, Un, swap, k,
+                     inv_k);
+  if (int e = check_launch(what)) return e;
+  const int N = swap ? Un : Tn, M = swap ? Tn : Un;
+  return udtw_cost_fwd_any<T>(tmp, nullptr, B, N, M, gamma, 0.0, R, nullptr, out, pen_scratch,
+                              s, what);
+}
+
+template <typename T>
+int fvm_bwd(const T* C, const T* tmp, const T* R, const T* gout, int B, int K, int Tn, int Un,
+            double gamma, T* dC, T* ws, hipStream_t s, const char* what) {
+  if (B < 0 || K <= 0 || Tn <= 0 || Un <= 0 || !(gamma > 0))
+    return fail(TW_EINVAL, "%s: bad arguments", what);
+  if (!C || !tmp || !R || !gout || !dC || !ws) return fail(TW_EINVAL, "%s: null pointer", what);
+  if (B == 0) return TW_OK;
+  const int swap = Tn > Un;
+  const int N = swap ? Un : Tn, M = swap ? Tn : Un;
+  if (int e = udtw_cost_bwd_any<T>(tmp, nullptr, R, nullptr, gout, nullptr, B, N, M, gamma, ws,
+                                   nullptr, s, what))
+    return e;
+  const T k = (T)(1.4426950408889634 / gamma);
+  dim3 grid((Tn * Un + 255) / 256, B);
+  hipLaunchKernelGGL((fvm_softmin_bwd<T>), grid, dim3(256), 0, s, C, tmp, ws, dC, K, Tn, Un,
+                     swap, k);
+  return check_launch(what);
+}
+
+// ------------------------------------------------------ JEANIE from features
+
+template <typename T>
+int pair_cost_fwd(const T* A, const T* Bm, int P, int R, int C, int D, int metric, T* out,
+                  hipStream_t s, const char* what);
+template <typename T>
+int pair_cost_bwd(const T* A, const T* Bm, const T* cost, const T* dcost, int P, int R, int C,
+                  int D, int metric, T* dA, T* dB, hipStream_t s, const char* what);
+
+template <typename T>
+int jeanie_feat_fwd(const T* q, const T* sup, int B, int K1, int K2, int Tq, int Us, int D,
+                    int s1, int s2, double gamma, int metric, T* cost, T* R, T* out,
+                    hipStream_t s, const char* what) {
+  if (metric != 1 && metric != 2)
+    return fail(TW_EINVAL, "%s: metric must be 1 (squared) or 2 (Euclidean)", what);
+  if (B == 0) return TW_OK;
+  if (int e = pair_cost_fwd<T>(q, sup, B, K1 * K2 * Tq, Us, D, metric, cost, s, what)) return e;
+  const int swap = Tq > Us;
+  return jeanie_cost_fwd<T>(cost, B, K1, K2, swap ? Us : Tq, swap ? Tq : Us, swap, s1, s2, gamma,
+                            R, out, s, what);
+}
+
+template <typename T>
+int jeanie_feat_bwd(const T* q, const T* sup, const T* cost, const T* R, const T* gout,
+                    const T* gR, int B, int K1, int K2, int Tq, int Us, int D, int s1, int s2,
+                    double gamma, int metric, T* dq, T* dsup, T* ws, hipStream_t s,
+                    const char* what) {
+  if (metric != 1 && metric != 2)
+    return fail(TW_EINVAL, "%s: metric must be 1 (squared) or 2 (Euclidean)", what);
+  if (!ws) return fail(TW_EINVAL, "%s: workspace needed", what);
+  if (B == 0) return TW_OK;
+  const int swap = Tq > Us;
+  if (int e = jeanie_cost_bwd<T>(cost, R, gout, gR, B, K1, K2, swap ? Us : Tq, swap ? Tq : Us,
+                                 swap, s1, s2, gamma, ws, s, what))
+    return e;
+  return pair_cost_bwd<T>(q, sup, cost, ws, B, K1 * K2 * Tq, Us, D, metric, dq, dsup, s, what);
+}
+
+}  // namespace tw
+
+using namespace tw;
+
+extern "C" {
+
+int tw_jeanie_cost_fwd_f32(const float* cost, int B, int K1, int K2, int T, int U, int swap_tu,
+                           int s1, int s2, float gamma, float* R, float* out, hipStream_t stream) {
+  return jeanie_cost_fwd<float>(cost, B, K1, K2, T, U, swap_tu, s1, s2, gamma, R, out, stream,
+                                "tw_jeanie_cost_fwd_f32");
+}
+int tw_jeanie_cost_fwd_f64(const double* cost, int B, int K1, int K2, int T, int U, int swap_tu,
+                           int s1, int s2, double gamma, double* R, double* out,
+                           hipStream_t stream) {
+  return jeanie_cost_fwd<double>(cost, B, K1, K2, T, U, swap_tu, s1, s2, gamma, R, out, stream,
+                                 "tw_jeanie_cost_fwd_f64");
+}
+int tw_jeanie_cost_bwd_f32(const float* cost, const float* R, const float* grad_out,
+                           const float* grad_R, int B, int K1, int K2, int T, int U, int swap_tu,
+                           int s1, int s2, float gamma, float* d_cost, hipStream_t stream) {
+  return jeanie_cost_bwd<float>(cost, R, grad_out, grad_R, B, K1, K2, T, U, swap_tu, s1, s2,
+                                gamma, d_cost, stream, "tw_jeanie_cost_bwd_f32");
+}
+int tw_jeanie_cost_bwd_f64(const double* cost, const double* R, const double* grad_out,
+                           const double* grad_R, int B, int K1, int K2, int T, int U,
+                           int swap_tu, int s1, int s2, double gamma, double* d_cost,
+                           hipStream_t stream) {
+  return jeanie_cost_bwd<double>(cost, R, grad_out, grad_R, B, K1, K2, T, U, swap_tu, s1, s2,
+                                 gamma, d_cost, stream, "tw_jeanie_cost_bwd_f64");
+}
+
+int tw_jeanie_feat_fwd_f32(const float* query, const float* support, int B, int K1, int K2, int T,
+                           int U, int D, int s1, int s2, float gamma, int metric, float* cost,
+                           float* R, float* out, hipStream_t stream) {
+  return jeanie_feat_fwd<float>(query, support, B, K1, K2, T, U, D, s1, s2, gamma, metric, cost,
+                                R, out, stream, "tw_jeanie_feat_fwd_f32");
+}
+int tw_jeanie_feat_fwd_f64(const double* query, const double* support, int B, int K1, int K2,
+                           int T, int U, int D, int s1, int s2, double gamma, int metric,
+                           double* cost, double* R, double* out, hipStream_t stream) {
+  return jeanie_feat_fwd<double>(query, support, B, K1, K2, T, U, D, s1, s2, gamma, metric, cost,
+                                 R, out, stream, "tw_jeanie_feat_fwd_f64");
+}
+int tw_jeanie_feat_bwd_f32(const float* query, const float* support, const float* cost,
+                           const float* R, const float* grad_out, const float* grad_R, int B,
+                           int K1, int K2, int T, int U, int D, int s1, int s2, float gamma,
+                           int metric, float* d_query, float* d_support, float* workspace,
+                           hipStream_t stream) {
+  return jeanie_feat_bwd<float>(query, support, cost, R, grad_out, grad_R, B, K1, K2, T, U, D, s1,
+                                s2, gamma, metric, d_query, d_support, workspace, stream,
+                                "tw_jeanie_feat_bwd_f32");
+}
+int tw_jeanie_feat_bwd_f64(const double* query, const double* support, const double* cost,
+                           const double* R, const double* grad_out, const double* grad_R, int B,
+                           int K1, int K2, int T, int U, int D, int s1, int s2, double gamma,
+                           int metric, double* d_query, double* d_support, double* workspace,
+                           hipStream_t stream) {
+  return jeanie_feat_bwd<double>(query, support, cost, R, grad_out, grad_R, B, K1, K2, T, U, D,
+                                 s1, s2, gamma, metric, d_query, d_support, workspace, stream,
+                                 "tw_jeanie_feat_bwd_f64");
+}
+
+int tw_fvm_cost_fwd_f32(const float* cost, int B, int K, int T, int U, float gamma,
+                        float* temporal, float* R, float* out, float* scratch,
+                        hipStream_t stream) {
+  return fvm_fwd<float>(cost, B, K, T, U, gamma, temporal, R, out, scratch, stream,
+                        "tw_fvm_cost_fwd_f32");
+}
+int tw_fvm_cost_fwd_f64(const double* cost, int B, int K, int T, int U, double gamma,
+                        double* temporal, double* R, double* out, double* scratch,
+                        hipStream_t stream) {
+  return fvm_fwd<double>(cost, B, K, T, U, gamma, temporal, R, out, scratch, stream,
+                         "tw_fvm_cost_fwd_f64");
+}
+int tw_fvm_cost_bwd_f32(const float* cost, const float* temporal, const float* R,
+                        const float* grad_out, int B, int K, int T, int U, float gamma,
+                        float* d_cost, float* workspace, hipStream_t stream) {
+  return fvm_bwd<float>(cost, temporal, R, grad_out, B, K, T, U, gamma, d_cost, workspace,
+                        stream, "tw_fvm_cost_bwd_f32");
+}
+int tw_fvm_cost_bwd_f64(const double* cost, const double* temporal, const double* R,
+                        const double* grad_out, int B, int K, int T, int U, double gamma,
+                        double* d_cost, double* workspace, hipStream_t stream) {
+  return fvm_bwd<double>(cost, temporal, R, grad_out, B, K, T, U, gamma, d_cost, workspace,
+                         stream, "tw_fvm_cost_bwd_f64");
+}
+
+}  // extern "C"

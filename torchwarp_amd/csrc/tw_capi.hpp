@@ -1,0 +1,23 @@
+// Host-side helpers shared by the C-ABI entry points: error reporting and
+// launch checks. The library never allocates device memory; callers pass
+// every output and workspace buffer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+#define TW_OK 0
+#define TW_EINVAL 1
+#define TW_ELAUNCH 2
+#define TW_ESIZE 3
+
+namespace tw {
+
+// Formats the thread-local last-error message and returns `code`.
+int fail(int code, const char* fmt, ...);
+// Checks hipGetLastError after a launch; returns TW_OK or TW_ELAUNCH.
+int check_launch(const char* what);
+// Device limits of the current device, queried once per device.
+int max_lds_bytes();
+
+}  // namespace tw

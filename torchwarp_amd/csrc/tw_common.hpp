@@ -1,0 +1,95 @@
+// Shared device helpers for the torchwarp gfx950 kernels.
+//
+// Conventions used by every DP kernel in this library:
+//  * Values are carried in the base-2 "scaled" domain: Rh = R * log2(e) / gamma.
+//    softmin_g(a, b, c) = gamma * ln2 * (mh - log2(2^(mh-ah) + 2^(mh-bh) + 2^(mh-ch)))
+//    with mh = min(ah, bh, ch); every exponent is an exact difference of two
+//    neighbouring scaled values, so one v_exp_f32 / v_log_f32 per term and no
+//    extra multiply on the dependency chain.
+//  * One row of the DP grid per (thread, k) slot; neighbouring rows of
+//    neighbouring threads exchange their boundary value with a DPP wave shift,
+//    and neighbouring waves through a small LDS mailbox behind an LDS-only
+//    barrier (never a wait on outstanding global stores).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace tw {
+
+template <typename T> __device__ __forceinline__ T inf_v();
+template <> __device__ __forceinline__ float inf_v<float>() { return __builtin_inff(); }
+template <> __device__ __forceinline__ double inf_v<double>() { return __builtin_inf(); }
+
+// 2^x, log2(x), 1/x. float uses the hardware transcendental unit (1 ulp);
+// double uses the device library.
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ double ex2(double x) { return exp2(x); }
+__device__ __forceinline__ float lg2(float x) { return __builtin_amdgcn_logf(x); }
+__device__ __forceinline__ double lg2(double x) { return log2(x); }
+__device__ __forceinline__ float rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ double rcp(double x) { return 1.0 / x; }
+__device__ __forceinline__ float sqrt_v(float x) { return __builtin_sqrtf(x); }
+__device__ __forceinline__ double sqrt_v(double x) { return __builtin_sqrt(x); }
+
+template <typename T>
+__device__ __forceinline__ T min3(T a, T b, T c) {
+  return fmin(a, fmin(b, c));
+}
+
+// ---- cross-lane moves (DPP wave shifts; a 64-bit value moves as two dwords)
+// lane l receives lane l-1's value; lane 0 receives `edge`.
+__device__ __forceinline__ float from_prev_lane(float v, float edge) {
+  int r = __builtin_amdgcn_update_dpp(__float_as_int(edge), __float_as_int(v), 0x138, 0xf, 0xf,
+                                      false);
+  return __int_as_float(r);
+}
+__device__ __forceinline__ double from_prev_lane(double v, double edge) {
+  long long b = __double_as_longlong(v), e = __double_as_longlong(edge);
+  int lo = __builtin_amdgcn_update_dpp((int)e, (int)b, 0x138, 0xf, 0xf, false);
+  int hi = __builtin_amdgcn_update_dpp((int)(e >> 32), (int)(b >> 32), 0x138, 0xf, 0xf, false);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+// lane l receives lane l+1's value; lane 63 receives `edge`.
+__device__ __forceinline__ float from_next_lane(float v, float edge) {
+  int r = __builtin_amdgcn_update_dpp(__float_as_int(edge), __float_as_int(v), 0x130, 0xf, 0xf,
+                                      false);
+  return __int_as_float(r);
+}
+__device__ __forceinline__ double from_next_lane(double v, double edge) {
+  long long b = __double_as_longlong(v), e = __double_as_longlong(edge);
+  int lo = __builtin_amdgcn_update_dpp((int)e, (int)b, 0x130, 0xf, 0xf, false);
+  int hi = __builtin_amdgcn_update_dpp((int)(e >> 32), (int)(b >> 32), 0x130, 0xf, 0xf, false);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+// Workgroup barrier that orders LDS only: outstanding global stores are not
+// waited for (the DP stores its R/P history every diagonal).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Number of cells on anti-diagonals 0..d-1 of an N x M grid (N <= M not required).
+__host__ __device__ __forceinline__ long long diag_offset(int d, int N, int M) {
+  // cells (i, d' - i) with max(0, d'-M+1) <= i <= min(N-1, d'), summed over d' < d
+  long long s = 0;
+  const int a = N < M ? N : M;   // length of the plateau
+  const int b = N < M ? M : N;
+  // ramp up: diagonals 0..a-2 have lengths 1..a-1
+  int ramp = d < a - 1 ? d : a - 1;
+  s += (long long)ramp * (ramp + 1) / 2;
+  if (d <= a - 1) return s;
+  // plateau: diagonals a-1 .. b-1 have length a
+  int plat = (d < b ? d : b) - (a - 1);
+  s += (long long)plat * a;
+  if (d <= b) return s;
+  // ramp down: diagonals b .. d-1 have lengths a-1, a-2, ...
+  int down = d - b;
+  s += (long long)down * (a - 1) - (long long)down * (down - 1) / 2;
+  return s;
+}
+
+}  // namespace tw
