@@ -50,8 +50,8 @@ const char* tw_last_error(void);
  * torchwarp_udtw::dp / dp_backward (udtw/_ops.py:100-138).
  * cost, pen: [B,N,M]; pen may be NULL (zero penalty, P unused).
  * R, P: [B, N*M] internal; out_dist, out_pen: [B].
- * Backward: grad_dist, grad_pen [B] (grad_pen may be NULL iff pen is NULL);
- * d_cost, d_pen [B,N,M] (d_pen may be NULL). */
+ * Backward: the forward's bandwidth; grad_dist, grad_pen [B] (grad_pen may be
+ * NULL iff pen is NULL); d_cost, d_pen [B,N,M] (d_pen may be NULL). */
 int tw_udtw_cost_fwd_f32(const float* cost, const float* pen, int B, int N, int M, float gamma,
                          float bandwidth, float* R, float* P, float* out_dist, float* out_pen,
                          hipStream_t stream);
@@ -60,11 +60,12 @@ int tw_udtw_cost_fwd_f64(const double* cost, const double* pen, int B, int N, in
                          double* out_pen, hipStream_t stream);
 int tw_udtw_cost_bwd_f32(const float* cost, const float* pen, const float* R, const float* P,
                          const float* grad_dist, const float* grad_pen, int B, int N, int M,
-                         float gamma, float* d_cost, float* d_pen, hipStream_t stream);
+                         float gamma, float bandwidth, float* d_cost, float* d_pen,
+                         hipStream_t stream);
 int tw_udtw_cost_bwd_f64(const double* cost, const double* pen, const double* R,
                          const double* P, const double* grad_dist, const double* grad_pen, int B,
-                         int N, int M, double gamma, double* d_cost, double* d_pen,
-                         hipStream_t stream);
+                         int N, int M, double gamma, double bandwidth, double* d_cost,
+                         double* d_pen, hipStream_t stream);
 
 /* uDTW straight from the features, N <= M. Replaces udtw_cuda.cu:738-775
  * (fused_forward) / :777-814 (fused_backward) together with the bmm / vecdot /
@@ -87,13 +88,14 @@ int tw_udtw_feat_fwd_f64(const double* X, const double* Y, const double* vx, con
 int tw_udtw_feat_bwd_f32(const float* X, const float* Y, const float* vx, const float* vy,
                          const float* R, const float* P, const float* grad_dist,
                          const float* grad_pen, int B, int N, int M, int D, float gamma,
-                         float beta, float eps, float* dX, float* dY, float* dvx, float* dvy,
-                         float* workspace, size_t workspace_bytes, hipStream_t stream);
+                         float beta, float eps, float bandwidth, float* dX, float* dY,
+                         float* dvx, float* dvy, float* workspace, size_t workspace_bytes,
+                         hipStream_t stream);
 int tw_udtw_feat_bwd_f64(const double* X, const double* Y, const double* vx, const double* vy,
                          const double* R, const double* P, const double* grad_dist,
                          const double* grad_pen, int B, int N, int M, int D, double gamma,
-                         double beta, double eps, double* dX, double* dY, double* dvx,
-                         double* dvy, double* workspace, size_t workspace_bytes,
+                         double beta, double eps, double bandwidth, double* dX, double* dY,
+                         double* dvx, double* dvy, double* workspace, size_t workspace_bytes,
                          hipStream_t stream);
 
 /* -------------------------------------------------------------- JEANIE --

@@ -19,9 +19,9 @@ LIB_PATH = Path(__file__).resolve().parent / "libtorchwarp_hip.so"
 # z size_t, s stream
 SIGNATURES = {
     "tw_udtw_cost_fwd": "ppiiiffpppps",
-    "tw_udtw_cost_bwd": "ppppppiiifpps",
+    "tw_udtw_cost_bwd": "ppppppiiiffpps",
     "tw_udtw_feat_fwd": "ppppiiiiffffpppppzs",
-    "tw_udtw_feat_bwd": "ppppppppiiiifffpppppzs",
+    "tw_udtw_feat_bwd": "ppppppppiiiiffffpppppzs",
     "tw_jeanie_cost_fwd": "piiiiiiiifpps",
     "tw_jeanie_cost_bwd": "ppppiiiiiiiifps",
     "tw_jeanie_feat_fwd": "ppiiiiiiiifippps",

@@ -64,6 +64,79 @@ __device__ __forceinline__ double from_next_lane(double v, double edge) {
   return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 
+// DPP wave shift with an explicit value for the lane that has no source:
+// lane l takes lane l-1 (prev) / l+1 (next); lane 0 (prev) / 63 (next) keeps `edge`.
+__device__ __forceinline__ int dpp_prev_i(int v, int edge) {
+  return __builtin_amdgcn_update_dpp(edge, v, 0x138, 0xf, 0xf, false);
+}
+__device__ __forceinline__ int dpp_next_i(int v, int edge) {
+  return __builtin_amdgcn_update_dpp(edge, v, 0x130, 0xf, 0xf, false);
+}
+
+// Raw buffer access with a 32-bit byte offset split in a per-lane part
+// (voffset) and a wave-uniform part (soffset). A voffset of kOob is out of
+// range: loads return 0 and stores are dropped by the hardware range check.
+constexpr int kOob = 0x80000000;
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9-family raw buffer, dword format
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+struct Buf {
+  __amdgpu_buffer_rsrc_t r;
+  template <typename T>
+  __device__ __forceinline__ void init(const T* p, long long n) {
+    r = __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)(n * (long long)sizeof(T)),
+                                          kRsrcWord3);
+  }
+  __device__ __forceinline__ float ldf(int v, int s) const {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, v, s, 0));
+  }
+  __device__ __forceinline__ double ldd(int v, int s) const {
+    const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(r, v, s, 0);
+    return __longlong_as_double((long long)(((unsigned long long)w.y << 32) | w.x));
+  }
+  __device__ __forceinline__ void st(float x, int v, int s) const {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), r, v, s, 0);
+  }
+  __device__ __forceinline__ void st(double x, int v, int s) const {
+    const unsigned long long u = (unsigned long long)__double_as_longlong(x);
+    u32x2 w;
+    w.x = (unsigned int)u;
+    w.y = (unsigned int)(u >> 32);
+    __builtin_amdgcn_raw_buffer_store_b64(w, r, v, s, 0);
+  }
+  template <typename T>
+  __device__ __forceinline__ T ld(int v, int s) const;
+};
+template <> __device__ __forceinline__ float Buf::ld<float>(int v, int s) const { return ldf(v, s); }
+template <> __device__ __forceinline__ double Buf::ld<double>(int v, int s) const { return ldd(v, s); }
+
+template <typename T>
+__device__ __forceinline__ T shift_prev(T v, T edge);
+template <>
+__device__ __forceinline__ float shift_prev<float>(float v, float edge) {
+  return __int_as_float(dpp_prev_i(__float_as_int(v), __float_as_int(edge)));
+}
+template <>
+__device__ __forceinline__ double shift_prev<double>(double v, double edge) {
+  long long b = __double_as_longlong(v), e = __double_as_longlong(edge);
+  int lo = dpp_prev_i((int)b, (int)e);
+  int hi = dpp_prev_i((int)(b >> 32), (int)(e >> 32));
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+template <typename T>
+__device__ __forceinline__ T shift_next(T v, T edge);
+template <>
+__device__ __forceinline__ float shift_next<float>(float v, float edge) {
+  return __int_as_float(dpp_next_i(__float_as_int(v), __float_as_int(edge)));
+}
+template <>
+__device__ __forceinline__ double shift_next<double>(double v, double edge) {
+  long long b = __double_as_longlong(v), e = __double_as_longlong(edge);
+  int lo = dpp_next_i((int)b, (int)e);
+  int hi = dpp_next_i((int)(b >> 32), (int)(e >> 32));
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
 // Workgroup barrier that orders LDS only: outstanding global stores are not
 // waited for (the DP stores its R/P history every diagonal).
 __device__ __forceinline__ void lds_barrier() {

@@ -115,158 +115,198 @@ __device__ __forceinline__ CellCost<T> cell_cost(const UdtwArgs<T>& a, T cin, T 
   return o;
 }
 
-template <typename T, int ROWS, int SRC, bool PEN>
+// Column values (y, vy) travel with the wavefront: the cell of row i on
+// diagonal d uses column j = d - i, which row i-1 used on diagonal d-1, so a
+// row takes its column operands from the row above (forward) or below
+// (backward) with the same DPP shift that moves R. Only the row where a
+// column enters the sweep (row 0 forward, row N-1 backward) reads it from LDS.
+// The backward's column gradient sums ride along the same way and are
+// written out when the column leaves the sweep, in a fixed row order.
+//
+// Global accesses are raw buffer operations with a lane-constant voffset and
+// a wave-uniform soffset; lanes outside the grid use an out-of-range voffset,
+// so their stores are dropped without branching. Loads of the cost source
+// (and, in the backward, of R/P) run PF diagonals ahead through a register ring.
+
+template <typename T, int ROWS, int SRC, bool PEN, bool BAND, int PF>
 __global__ void __launch_bounds__(1024) udtw_fwd_kernel(UdtwArgs<T> a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T* sm = reinterpret_cast<T*>(smem_raw);
+  constexpr int ES = sizeof(T);
   const int N = a.N, M = a.M;
   const int b = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const T INF = inf_v<T>();
-  const size_t NM = (size_t)N * M;
+  const long long NM = (long long)N * M;
 
-  T* mbr = sm;                 // mailbox R [2][nw]
-  T* mbp = sm + 2 * nw;        // mailbox P [2][nw]
-  T* ys = sm + 4 * nw;         // y  [M]  (SRC_FEAT1)
-  T* vys = ys + (SRC == SRC_FEAT1 ? M : 0);  // vy [M] (SRC_SQ, SRC_FEAT1)
-
+  T* mb = sm;                                  // mailbox [2][nw][4]: R, P, y, vy
+  T* ys = sm + 8 * nw;                         // y  [M] (FEAT1)
+  T* vys = ys + (SRC == SRC_FEAT1 ? M : 0);    // vy [M] (SQ, FEAT1)
   if (SRC == SRC_FEAT1)
     for (int t = tid; t < M; t += blockDim.x) ys[t] = a.Y[(size_t)b * M + t];
   if (SRC != SRC_COST)
     for (int t = tid; t < M; t += blockDim.x) vys[t] = a.VY[(size_t)b * M + t];
   for (int t = tid; t < 2 * nw; t += blockDim.x) {
-    mbr[t] = INF;
-    mbp[t] = (T)0;
+    mb[4 * t + 0] = INF;
+    mb[4 * t + 1] = (T)0;
+    mb[4 * t + 2] = (T)0;
+    mb[4 * t + 3] = (T)1;
   }
 
+  Buf bR, bP, bC, bQ;
+  bR.init(a.R + b * NM, NM);
+  if (PEN) bP.init(a.P + b * NM, NM);
+  if (SRC != SRC_FEAT1) bC.init(a.C + b * NM, NM);
+  if (SRC == SRC_COST && PEN) bQ.init(a.Q + b * NM, NM);
+
   const int row0 = tid * ROWS;
-  T xr[ROWS], vxr[ROWS];
+  T xr[ROWS], vxr[ROWS], r1[ROWS], r2[ROWS], p1[ROWS], p2[ROWS], yc[ROWS], vyc[ROWS];
 #pragma unroll
   for (int k = 0; k < ROWS; ++k) {
     const int i = row0 + k;
     xr[k] = (SRC == SRC_FEAT1 && i < N) ? a.X[(size_t)b * N + i] : (T)0;
     vxr[k] = (SRC != SRC_COST && i < N) ? a.VX[(size_t)b * N + i] : (T)1;
+    r1[k] = r2[k] = INF;
+    p1[k] = p2[k] = (T)0;
+    yc[k] = (T)0;
+    vyc[k] = (T)1;
   }
-  T r1[ROWS], r2[ROWS], p1[ROWS], p2[ROWS];
-#pragma unroll
-  for (int k = 0; k < ROWS; ++k) {
-    r1[k] = INF;
-    r2[k] = INF;
-    p1[k] = (T)0;
-    p2[k] = (T)0;
-  }
-  // Neighbour row (previous thread's last row) at diagonals d-1 and d-2.
-  // Thread 0's "neighbour" is the border; its value 0 at the origin makes
-  // the generic update give R[0,0] = C[0,0], P[0,0] = Q[0,0].
+  // Previous thread's last row on diagonals d-1 / d-2. For thread 0 this is
+  // the border; its 0 at the origin makes the update give R[0,0] = C[0,0].
   T nr1 = (tid == 0) ? (T)0 : INF, nr2 = INF, np1 = (T)0, np2 = (T)0;
 
-  const T* Cb = a.C ? a.C + b * NM : nullptr;
-  const T* Qb = a.Q ? a.Q + b * NM : nullptr;
-  T* Rb = a.R + b * NM;
-  T* Pb = PEN ? a.P + b * NM : nullptr;
-
-  T pc[ROWS], pq[ROWS];
-#pragma unroll
-  for (int k = 0; k < ROWS; ++k) {
-    pc[k] = (T)0;
-    pq[k] = (T)0;
-  }
-  auto fetch = [&](int d) {
-    if (SRC == SRC_FEAT1) return;
+  // cost-source prefetch ring (natural [N, M] layout: cell (i, d-i) sits at
+  // element i*(M-1) + d)
+  T rc[PF][ROWS], rq[PF][ROWS];
+  auto fetch = [&](int d, T* c, T* q) {
 #pragma unroll
     for (int k = 0; k < ROWS; ++k) {
       const int i = row0 + k, j = d - i;
-      if (i < N && j >= 0 && j < M) {
-        const size_t o = (size_t)i * M + j;
-        pc[k] = Cb[o];
-        if (SRC == SRC_COST && PEN) pq[k] = Qb[o];
-      }
+      const int vo = (i < N && j >= 0 && j < M) ? i * (M - 1) * ES : kOob;
+      c[k] = bC.ld<T>(vo, d * ES);
+      if (SRC == SRC_COST && PEN) q[k] = bQ.ld<T>(vo, d * ES);
     }
   };
-  fetch(0);
+  const int Dn = N + M - 1;
+  if (SRC != SRC_FEAT1) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) fetch(u, rc[u], rq[u]);
+  }
   __syncthreads();
 
-  const int Dn = N + M - 1;
-  long long off = 0;
-  for (int d = 0; d < Dn; ++d) {
-    const int lo = max(0, d - M + 1), hi = min(N - 1, d);
-    T cc[ROWS], cq[ROWS];
+  T ycol_next = SRC == SRC_FEAT1 ? ys[0] : (T)0;
+  T vycol_next = SRC != SRC_COST ? vys[0] : (T)1;
+  long long off = 0;  // first element of diagonal d in the diagonal-major layout
+  for (int d0 = 0; d0 < Dn; d0 += PF) {
 #pragma unroll
-    for (int k = 0; k < ROWS; ++k) {
-      cc[k] = pc[k];
-      cq[k] = pq[k];
-    }
-    if (d + 1 < Dn) fetch(d + 1);
-
-    nr2 = nr1;
-    np2 = np1;
-    {
-      T sr = from_prev_lane(r1[ROWS - 1], INF);
-      T sp = PEN ? from_prev_lane(p1[ROWS - 1], (T)0) : (T)0;
-      if (lane == 0) {
-        if (wave == 0) {
-          sr = INF;
-          sp = (T)0;
-        } else {
-          const int par = (d - 1) & 1;
-          sr = mbr[par * nw + wave - 1];
-          if (PEN) sp = mbp[par * nw + wave - 1];
-        }
+    for (int u = 0; u < PF; ++u) {
+      const int d = d0 + u;
+      if (d >= Dn) break;
+      const int lo = max(0, d - M + 1), hi = min(N - 1, d);
+      T cc[ROWS], cq[ROWS];
+#pragma unroll
+      for (int k = 0; k < ROWS; ++k) {
+        cc[k] = rc[u][k];
+        cq[k] = rq[u][k];
       }
-      nr1 = sr;
-      np1 = sp;
-    }
+      if (SRC != SRC_FEAT1) fetch(d + PF, rc[u], rq[u]);
 
-    T nr[ROWS], np[ROWS];
-#pragma unroll
-    for (int k = 0; k < ROWS; ++k) {
-      const int i = row0 + k, j = d - i;
-      const bool valid = (i < N) & (j >= 0) & (j < M);
-      const int jc = j < 0 ? 0 : (j >= M ? M - 1 : j);
-      const T up = k ? r1[k - 1] : nr1;
-      const T dg = k ? r2[k - 1] : nr2;
-      const T lf = r1[k];
-      T y = (T)0, vy = (T)1;
-      if (SRC == SRC_FEAT1) y = ys[jc];
-      if (SRC != SRC_COST) vy = vys[jc];
-      const CellCost<T> cv = cell_cost<T, SRC, PEN>(a, cc[k], cq[k], xr[k], vxr[k], y, vy);
-      const T m = min3(dg, up, lf);
-      const T ed = ex2(m - dg), eu = ex2(m - up), el = ex2(m - lf);
-      const T s = ed + eu + el;
-      const T rv = cv.ch + m - lg2(s);
-      bool ok = valid && (m < INF);
-      if (a.band > (T)0) ok = ok && (fabs((T)(i - j)) <= a.band);
-      nr[k] = ok ? rv : INF;
-      if (PEN) {
-        const T pup = k ? p1[k - 1] : np1;
-        const T pdg = k ? p2[k - 1] : np2;
-        const T pv = cv.q + (ed * pdg + eu * pup + el * p1[k]) * rcp(s);
-        np[k] = ok ? pv : (T)0;
+      // operands arriving at this thread's first row
+      T er, ep, ey, evy;
+      if (wave == 0) {
+        er = INF;
+        ep = (T)0;
+        ey = ycol_next;
+        evy = vycol_next;
+        const int dn = d + 1 < M ? d + 1 : M - 1;   // column entering on the next diagonal
+        if (SRC == SRC_FEAT1) ycol_next = ys[dn];
+        if (SRC != SRC_COST) vycol_next = vys[dn];
       } else {
-        np[k] = (T)0;
+        const T* box = mb + 4 * (((d - 1) & 1) * nw + wave - 1);
+        er = box[0];
+        ep = box[1];
+        ey = box[2];
+        evy = box[3];
       }
-      if (valid) {
-        const long long o = off + (i - lo);
-        Rb[o] = nr[k];
-        if (PEN) Pb[o] = np[k];
-      }
-    }
+      nr2 = nr1;
+      np2 = np1;
+      nr1 = shift_prev(r1[ROWS - 1], er);
+      if (PEN) np1 = shift_prev(p1[ROWS - 1], ep);
+      const T ny = SRC == SRC_FEAT1 ? shift_prev(yc[ROWS - 1], ey) : (T)0;
+      const T nvy = SRC != SRC_COST ? shift_prev(vyc[ROWS - 1], evy) : (T)1;
 #pragma unroll
-    for (int k = 0; k < ROWS; ++k) {
-      r2[k] = r1[k];
-      r1[k] = nr[k];
-      p2[k] = p1[k];
-      p1[k] = np[k];
-    }
-    if (nw > 1) {
-      const int par = d & 1;
-      if (lane == 63) {
-        mbr[par * nw + wave] = r1[ROWS - 1];
-        if (PEN) mbp[par * nw + wave] = p1[ROWS - 1];
+      for (int k = ROWS - 1; k > 0; --k) {
+        yc[k] = yc[k - 1];
+        vyc[k] = vyc[k - 1];
       }
-      lds_barrier();
+      yc[0] = ny;
+      vyc[0] = nvy;
+
+      const int soff = (int)(off - lo) * ES;
+      T nr[ROWS], np[ROWS];
+#pragma unroll
+      for (int k = 0; k < ROWS; ++k) {
+        const int i = row0 + k, j = d - i;
+        const bool valid = (i < N) & ((unsigned)j < (unsigned)M);
+        const T up = k ? r1[k - 1] : nr1;
+        const T dg = k ? r2[k - 1] : nr2;
+        const T lf = r1[k];
+        T ch, q = (T)0;
+        if (SRC == SRC_COST) {
+          ch = cc[k] * a.k;
+          if (PEN) q = cq[k];
+        } else {
+          T sq;
+          if (SRC == SRC_FEAT1) {
+            const T df = xr[k] - yc[k];
+            sq = df * df;
+          } else {
+            sq = cc[k] > (T)0 ? cc[k] : (T)0;
+          }
+          const T var_raw = (T)0.5 * (vxr[k] + vyc[k]);
+          const T var = var_raw > a.eps ? var_raw : a.eps;
+          ch = sq * (rcp(var) * a.k);
+          if (PEN) q = a.beta_ln2 * lg2(var);
+        }
+        const T m = min3(dg, up, lf);
+        const T ed = ex2(m - dg), eu = ex2(m - up), el = ex2(m - lf);
+        const T s = ed + eu + el;
+        const T rv = ch + m - lg2(s);
+        bool ok = valid;
+        if (BAND) ok = ok && (m < INF) && (fabs((T)(i - j)) <= a.band);
+        nr[k] = ok ? rv : INF;
+        if (PEN) {
+          const T pup = k ? p1[k - 1] : np1;
+          const T pdg = k ? p2[k - 1] : np2;
+          const T pv = q + (ed * pdg + eu * pup + el * p1[k]) * rcp(s);
+          np[k] = ok ? pv : (T)0;
+        } else {
+          np[k] = (T)0;
+        }
+        const int vo = valid ? i * ES : kOob;
+        bR.st(nr[k], vo, soff);
+        if (PEN) bP.st(np[k], vo, soff);
+      }
+#pragma unroll
+      for (int k = 0; k < ROWS; ++k) {
+        r2[k] = r1[k];
+        r1[k] = nr[k];
+        p2[k] = p1[k];
+        p1[k] = np[k];
+      }
+      if (nw > 1) {
+        if (lane == 63) {
+          T* box = mb + 4 * ((d & 1) * nw + wave);
+          box[0] = r1[ROWS - 1];
+          box[1] = p1[ROWS - 1];
+          box[2] = yc[ROWS - 1];
+          box[3] = vyc[ROWS - 1];
+        }
+        lds_barrier();
+      }
+      off += hi - lo + 1;
     }
-    off += hi - lo + 1;
   }
 #pragma unroll
   for (int k = 0; k < ROWS; ++k) {
@@ -277,255 +317,292 @@ __global__ void __launch_bounds__(1024) udtw_fwd_kernel(UdtwArgs<T> a) {
   }
 }
 
-template <typename T, int ROWS, int SRC, bool PEN>
+template <typename T, int ROWS, int SRC, bool PEN, bool BAND, int PF>
 __global__ void __launch_bounds__(1024) udtw_bwd_kernel(UdtwArgs<T> a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T* sm = reinterpret_cast<T*>(smem_raw);
+  constexpr int ES = sizeof(T);
   const int N = a.N, M = a.M;
   const int b = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = blockDim.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const T INF = inf_v<T>();
-  const size_t NM = (size_t)N * M;
+  const long long NM = (long long)N * M;
   const bool vgrad = SRC != SRC_COST && a.dVX != nullptr;
 
-  T* mbe = sm;                 // mailboxes [2][nw] each: E, G(Rbar), H(Pbar), A
-  T* mbg = sm + 2 * nw;
-  T* mbh = sm + 4 * nw;
-  T* mba = sm + 6 * nw;
-  T* ys = sm + 8 * nw;                              // y   [M] (FEAT1)
-  T* vys = ys + (SRC == SRC_FEAT1 ? M : 0);         // vy  [M] (SQ, FEAT1)
-  T* dys = vys + (SRC != SRC_COST ? M : 0);         // dy  [M] (FEAT1)
-  T* dvys = dys + (SRC == SRC_FEAT1 ? M : 0);       // dvy [M] (SQ, FEAT1)
-
-  for (int t = tid; t < M; t += blockDim.x) {
-    if (SRC == SRC_FEAT1) {
-      ys[t] = a.Y[(size_t)b * M + t];
-      dys[t] = (T)0;
-    }
-    if (SRC != SRC_COST) {
-      vys[t] = a.VY[(size_t)b * M + t];
-      dvys[t] = (T)0;
-    }
-  }
+  // mailbox [2][nw][8]: E, G (Rbar), H (Pbar), A, y, vy, column sums dy, dvy
+  T* mb = sm;
+  T* ys = sm + 16 * nw;                        // y  [M] (FEAT1)
+  T* vys = ys + (SRC == SRC_FEAT1 ? M : 0);    // vy [M] (SQ, FEAT1)
+  if (SRC == SRC_FEAT1)
+    for (int t = tid; t < M; t += blockDim.x) ys[t] = a.Y[(size_t)b * M + t];
+  if (SRC != SRC_COST)
+    for (int t = tid; t < M; t += blockDim.x) vys[t] = a.VY[(size_t)b * M + t];
   for (int t = tid; t < 2 * nw; t += blockDim.x) {
-    mbe[t] = -INF;
-    mbg[t] = (T)0;
-    mbh[t] = (T)0;
-    mba[t] = (T)0;
+    mb[8 * t + 0] = -INF;
+#pragma unroll
+    for (int q = 1; q < 8; ++q) mb[8 * t + q] = (T)0;
   }
+
+  Buf bR, bP, bC, bQ, bdC, bdQ, bdY, bdVY;
+  bR.init(a.R + b * NM, NM);
+  if (PEN) bP.init(a.P + b * NM, NM);
+  if (SRC != SRC_FEAT1) {
+    bC.init(a.C + b * NM, NM);
+    bdC.init(a.dC + b * NM, NM);
+  }
+  if (SRC == SRC_COST && PEN) {
+    bQ.init(a.Q + b * NM, NM);
+    if (a.dQ) bdQ.init(a.dQ + b * NM, NM);
+  }
+  if (SRC == SRC_FEAT1) bdY.init(a.dY + (size_t)b * M, M);
+  if (vgrad) bdVY.init(a.dVY + (size_t)b * M, M);
+  const bool want_dq = SRC == SRC_COST && PEN && a.dQ != nullptr;
 
   const int row0 = tid * ROWS;
   T xr[ROWS], vxr[ROWS], dxr[ROWS], dvr[ROWS];
+  T e1[ROWS], e2[ROWS], g1[ROWS], g2[ROWS], h1[ROWS], h2[ROWS], a1[ROWS], a2[ROWS];
+  T yc[ROWS], vyc[ROWS], cy[ROWS], cvy[ROWS];
 #pragma unroll
   for (int k = 0; k < ROWS; ++k) {
     const int i = row0 + k;
     xr[k] = (SRC == SRC_FEAT1 && i < N) ? a.X[(size_t)b * N + i] : (T)0;
     vxr[k] = (SRC != SRC_COST && i < N) ? a.VX[(size_t)b * N + i] : (T)1;
-    dxr[k] = (T)0;
-    dvr[k] = (T)0;
-  }
-  // Own rows at diagonals d+1 (…1) and d+2 (…2).
-  T e1[ROWS], e2[ROWS], g1[ROWS], g2[ROWS], h1[ROWS], h2[ROWS], a1[ROWS], a2[ROWS];
-#pragma unroll
-  for (int k = 0; k < ROWS; ++k) {
+    dxr[k] = dvr[k] = (T)0;
     e1[k] = e2[k] = -INF;
     g1[k] = g2[k] = h1[k] = h2[k] = a1[k] = a2[k] = (T)0;
+    yc[k] = cy[k] = cvy[k] = (T)0;
+    vyc[k] = (T)1;
   }
-  // Next thread's first row at d+1 / d+2.
+  // next thread's first row on diagonals d+1 / d+2
   T ne1 = -INF, ne2 = -INF, ng1 = 0, ng2 = 0, nh1 = 0, nh2 = 0, na1 = 0, na2 = 0;
-
-  const T* Cb = a.C ? a.C + b * NM : nullptr;
-  const T* Qb = a.Q ? a.Q + b * NM : nullptr;
-  const T* Rb = a.R + b * NM;
-  const T* Pb = PEN ? a.P + b * NM : nullptr;
-  T* dCb = a.dC ? a.dC + b * NM : nullptr;
-  T* dQb = a.dQ ? a.dQ + b * NM : nullptr;
   const T gr = a.gr[b];
   const T gp = PEN ? a.gp[b] : (T)0;
-
   const int Dn = N + M - 1;
-  T pr[ROWS], pp[ROWS], pc[ROWS], pq[ROWS];
-#pragma unroll
-  for (int k = 0; k < ROWS; ++k) {
-    pr[k] = INF;
-    pp[k] = pc[k] = pq[k] = (T)0;
-  }
-  auto fetch = [&](int d, long long off) {
+
+  // prefetch ring: R, P (diagonal-major) and the cost source (natural layout)
+  T rr[PF][ROWS], rp[PF][ROWS], rc[PF][ROWS], rq[PF][ROWS];
+  auto fetch = [&](int d, T* r, T* p, T* c, T* q) {
     const int lo = max(0, d - M + 1);
+    const int soff_d = d >= 0 ? (int)(diag_offset(d, N, M) - lo) * ES : 0;
 #pragma unroll
     for (int k = 0; k < ROWS; ++k) {
       const int i = row0 + k, j = d - i;
-      if (i < N && j >= 0 && j < M) {
-        const long long od = off + (i - lo);
-        pr[k] = Rb[od];
-        if (PEN) pp[k] = Pb[od];
-        if (SRC != SRC_FEAT1) {
-          const size_t o = (size_t)i * M + j;
-          pc[k] = Cb[o];
-          if (SRC == SRC_COST && PEN) pq[k] = Qb[o];
-        }
+      const bool v = d >= 0 && i < N && j >= 0 && j < M;
+      r[k] = bR.ld<T>(v ? i * ES : kOob, soff_d);
+      if (PEN) p[k] = bP.ld<T>(v ? i * ES : kOob, soff_d);
+      if (SRC != SRC_FEAT1) {
+        const int vn = v ? i * (M - 1) * ES : kOob;
+        c[k] = bC.ld<T>(vn, d >= 0 ? d * ES : 0);
+        if (SRC == SRC_COST && PEN) q[k] = bQ.ld<T>(vn, d >= 0 ? d * ES : 0);
       }
     }
   };
-  long long off = (long long)NM - 1;
-  fetch(Dn - 1, off);
-  __syncthreads();
-
-  for (int d = Dn - 1; d >= 0; --d) {
-    const int lo = max(0, d - M + 1);
-    T cr[ROWS], cp[ROWS], cc[ROWS], cq[ROWS];
 #pragma unroll
-    for (int k = 0; k < ROWS; ++k) {
-      cr[k] = pr[k];
-      cp[k] = pp[k];
-      cc[k] = pc[k];
-      cq[k] = pq[k];
-    }
-    long long off1 = off;
-    if (d > 0) {
-      const int lo1 = max(0, d - 1 - M + 1), hi1 = min(N - 1, d - 1);
-      off1 = off - (hi1 - lo1 + 1);
-      fetch(d - 1, off1);
-    }
+  for (int u = 0; u < PF; ++u) fetch(Dn - 1 - u, rr[u], rp[u], rc[u], rq[u]);
+  __syncthreads();
+  T ycol_next = SRC == SRC_FEAT1 ? ys[M - 1] : (T)0;   // column M-1 enters first
+  T vycol_next = SRC != SRC_COST ? vys[M - 1] : (T)1;
 
-    ne2 = ne1;
-    ng2 = ng1;
-    nh2 = nh1;
-    na2 = na1;
-    {
-      T se = from_next_lane(e1[0], -INF);
-      T sg = from_next_lane(g1[0], (T)0);
-      T sh = PEN ? from_next_lane(h1[0], (T)0) : (T)0;
-      T sa = PEN ? from_next_lane(a1[0], (T)0) : (T)0;
-      if (lane == 63) {
-        if (wave == nw - 1) {
-          se = -INF;
-          sg = sh = sa = (T)0;
-        } else {
-          const int par = (d + 1) & 1;
-          se = mbe[par * nw + wave + 1];
-          sg = mbg[par * nw + wave + 1];
-          if (PEN) {
-            sh = mbh[par * nw + wave + 1];
-            sa = mba[par * nw + wave + 1];
+  for (int d0 = Dn - 1; d0 >= 0; d0 -= PF) {
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+      const int d = d0 - u;
+      if (d < 0) break;
+      T cr[ROWS], cp[ROWS], cc[ROWS], cq[ROWS];
+#pragma unroll
+      for (int k = 0; k < ROWS; ++k) {
+        cr[k] = rr[u][k];
+        cp[k] = rp[u][k];
+        cc[k] = rc[u][k];
+        cq[k] = rq[u][k];
+      }
+      fetch(d - PF, rr[u], rp[u], rc[u], rq[u]);
+
+      // operands arriving at this thread's last row from the next thread (step d+1)
+      T ed_, eg_, eh_, ea_, ey_, evy_, ecy_, ecvy_;
+      if (wave == nw - 1) {
+        ed_ = -INF;
+        eg_ = eh_ = ea_ = ey_ = ecy_ = ecvy_ = (T)0;
+        evy_ = (T)1;
+      } else {
+        const T* box = mb + 8 * (((d + 1) & 1) * nw + wave + 1);
+        ed_ = box[0];
+        eg_ = box[1];
+        eh_ = box[2];
+        ea_ = box[3];
+        ey_ = box[4];
+        evy_ = box[5];
+        ecy_ = box[6];
+        ecvy_ = box[7];
+      }
+      ne2 = ne1;
+      ng2 = ng1;
+      nh2 = nh1;
+      na2 = na1;
+      ne1 = shift_next(e1[0], ed_);
+      ng1 = shift_next(g1[0], eg_);
+      if (PEN) {
+        nh1 = shift_next(h1[0], eh_);
+        na1 = shift_next(a1[0], ea_);
+      }
+      // columns move up one row; a new column enters at row N-1
+      {
+        const T fy = SRC == SRC_FEAT1 ? shift_next(yc[0], ey_) : (T)0;
+        const T fvy = SRC != SRC_COST ? shift_next(vyc[0], evy_) : (T)1;
+        const T fcy = SRC == SRC_FEAT1 ? shift_next(cy[0], ecy_) : (T)0;
+        const T fcvy = SRC != SRC_COST ? shift_next(cvy[0], ecvy_) : (T)0;
+#pragma unroll
+        for (int k = 0; k + 1 < ROWS; ++k) {
+          yc[k] = yc[k + 1];
+          vyc[k] = vyc[k + 1];
+          cy[k] = cy[k + 1];
+          cvy[k] = cvy[k + 1];
+        }
+        yc[ROWS - 1] = fy;
+        vyc[ROWS - 1] = fvy;
+        cy[ROWS - 1] = fcy;
+        cvy[ROWS - 1] = fcvy;
+        if (SRC != SRC_COST) {
+          const T ny = ycol_next, nvy = vycol_next;
+          const int jn = d - 1 - (N - 1);                 // column entering on diagonal d-1
+          const int jc = jn < 0 ? 0 : (jn >= M ? M - 1 : jn);
+          if (SRC == SRC_FEAT1) ycol_next = ys[jc];
+          vycol_next = vys[jc];
+#pragma unroll
+          for (int k = 0; k < ROWS; ++k) {
+            if (row0 + k == N - 1) {
+              yc[k] = ny;
+              vyc[k] = nvy;
+              cy[k] = (T)0;
+              cvy[k] = (T)0;
+            }
           }
         }
       }
-      ne1 = se;
-      ng1 = sg;
-      nh1 = sh;
-      na1 = sa;
-    }
 
-    T xe[ROWS], xg[ROWS], xh[ROWS], xa[ROWS];
+      T xe[ROWS], xg[ROWS], xh[ROWS], xa[ROWS];
 #pragma unroll
-    for (int k = 0; k < ROWS; ++k) {
-      const int i = row0 + k, j = d - i;
-      const bool valid = (i < N) & (j >= 0) & (j < M);
-      const int jc = j < 0 ? 0 : (j >= M ? M - 1 : j);
-      const T rk = valid ? cr[k] : INF;
-      const T pk = cp[k];
-      T y = (T)0, vy = (T)1;
-      if (SRC == SRC_FEAT1) y = ys[jc];
-      if (SRC != SRC_COST) vy = vys[jc];
-      const CellCost<T> cv = cell_cost<T, SRC, PEN>(a, cc[k], cq[k], xr[k], vxr[k], y, vy);
-      // successors: down (i+1, j) and right (i, j+1) on d+1, diagonal (i+1, j+1) on d+2
-      const T edn = (k + 1 < ROWS) ? e1[k + 1] : ne1;
-      const T gdn = (k + 1 < ROWS) ? g1[k + 1] : ng1;
-      const T edg = (k + 1 < ROWS) ? e2[k + 1] : ne2;
-      const T gdg = (k + 1 < ROWS) ? g2[k + 1] : ng2;
-      const T ert = e1[k], grt = g1[k];
-      T g, h = (T)0;
-      if (d == Dn - 1) {
-        g = gr;
-        h = gp;
-      } else {
-        const T wdn = ex2(edn - rk), wrt = ex2(ert - rk), wdg = ex2(edg - rk);
-        g = wdn * gdn + wrt * grt + wdg * gdg;
-        if (PEN) {
-          const T hdn = (k + 1 < ROWS) ? h1[k + 1] : nh1;
-          const T adn = (k + 1 < ROWS) ? a1[k + 1] : na1;
-          const T hdg = (k + 1 < ROWS) ? h2[k + 1] : nh2;
-          const T adg = (k + 1 < ROWS) ? a2[k + 1] : na2;
-          const T hrt = h1[k], art = a1[k];
-          const T wh_dn = wdn * hdn, wh_rt = wrt * hrt, wh_dg = wdg * hdg;
-          g -= (wh_dn * (pk - adn) + wh_rt * (pk - art) + wh_dg * (pk - adg)) * a.inv_gamma;
-          h = wh_dn + wh_rt + wh_dg;
+      for (int k = 0; k < ROWS; ++k) {
+        const int i = row0 + k, j = d - i;
+        const bool valid = (i < N) & ((unsigned)j < (unsigned)M);
+        const T rk = valid ? cr[k] : INF;
+        const T pk = cp[k];
+        T ch, q = (T)0, c = (T)0, rv = (T)1, sq_raw = (T)0, var_raw = (T)1;
+        if (SRC == SRC_COST) {
+          ch = cc[k] * a.k;
+          if (PEN) q = cq[k];
+        } else {
+          if (SRC == SRC_FEAT1) {
+            const T df = xr[k] - yc[k];
+            sq_raw = df * df;
+          } else {
+            sq_raw = cc[k];
+          }
+          const T sq = sq_raw > (T)0 ? sq_raw : (T)0;
+          var_raw = (T)0.5 * (vxr[k] + vyc[k]);
+          const T var = var_raw > a.eps ? var_raw : a.eps;
+          rv = rcp(var);
+          c = sq * rv;
+          ch = c * a.k;
+          if (PEN) q = a.beta_ln2 * lg2(var);
         }
-        if (!(rk < INF)) {
+        // successors: down (i+1, j) and right (i, j+1) on d+1, diagonal (i+1, j+1) on d+2
+        const T edn = (k + 1 < ROWS) ? e1[k + 1] : ne1;
+        const T gdn = (k + 1 < ROWS) ? g1[k + 1] : ng1;
+        const T edg = (k + 1 < ROWS) ? e2[k + 1] : ne2;
+        const T gdg = (k + 1 < ROWS) ? g2[k + 1] : ng2;
+        T g, h = (T)0;
+        if (d == Dn - 1) {
+          g = gr;
+          h = gp;
+        } else {
+          const T wdn = ex2(edn - rk), wrt = ex2(e1[k] - rk), wdg = ex2(edg - rk);
+          g = wdn * gdn + wrt * g1[k] + wdg * gdg;
+          if (PEN) {
+            const T hdn = (k + 1 < ROWS) ? h1[k + 1] : nh1;
+            const T adn = (k + 1 < ROWS) ? a1[k + 1] : na1;
+            const T hdg = (k + 1 < ROWS) ? h2[k + 1] : nh2;
+            const T adg = (k + 1 < ROWS) ? a2[k + 1] : na2;
+            const T wh_dn = wdn * hdn, wh_rt = wrt * h1[k], wh_dg = wdg * hdg;
+            g -= (wh_dn * (pk - adn) + wh_rt * (pk - a1[k]) + wh_dg * (pk - adg)) * a.inv_gamma;
+            h = wh_dn + wh_rt + wh_dg;
+          }
+          if (BAND) {
+            if (!(rk < INF)) {
+              g = (T)0;
+              h = (T)0;
+            }
+          }
+        }
+        if (!valid) {
           g = (T)0;
           h = (T)0;
         }
-      }
-      if (!valid) {
-        g = (T)0;
-        h = (T)0;
-      }
-      xe[k] = (valid && rk < INF) ? rk - cv.ch : -INF;
-      xg[k] = g;
-      xh[k] = h;
-      xa[k] = valid ? pk - cv.q : (T)0;
+        xe[k] = (valid && (!BAND || rk < INF)) ? rk - ch : -INF;
+        xg[k] = g;
+        xh[k] = h;
+        xa[k] = valid ? pk - q : (T)0;
 
-      if (valid) {
+        const int vn = valid ? i * (M - 1) * ES : kOob;
         if (SRC == SRC_COST) {
-          const size_t o = (size_t)i * M + j;
-          dCb[o] = g;
-          if (dQb) dQb[o] = h;
+          bdC.st(g, vn, d * ES);
+          if (want_dq) bdQ.st(h, vn, d * ES);
         } else {
-          const T dsq = cv.sq_raw > (T)0 ? g * cv.rv : (T)0;
-          if (SRC == SRC_SQ) dCb[(size_t)i * M + j] = dsq;
+          const T dsq = sq_raw > (T)0 ? g * rv : (T)0;
+          if (SRC == SRC_SQ) bdC.st(dsq, vn, d * ES);
           if (SRC == SRC_FEAT1) {
-            const T df = (T)2 * dsq * (xr[k] - y);
+            const T df = valid ? (T)2 * dsq * (xr[k] - yc[k]) : (T)0;
             dxr[k] += df;
-            atomicAdd(&dys[j], -df);
+            cy[k] -= df;
           }
           if (vgrad) {
-            const T dvar = cv.var_raw > a.eps ? (a.beta * h - g * cv.c) * cv.rv : (T)0;
-            dvr[k] += (T)0.5 * dvar;
-            atomicAdd(&dvys[j], (T)0.5 * dvar);
+            T dvar = var_raw > a.eps ? (T)0.5 * (a.beta * h - g * c) * rv : (T)0;
+            dvar = valid ? dvar : (T)0;
+            dvr[k] += dvar;
+            cvy[k] += dvar;
           }
         }
       }
-    }
-#pragma unroll
-    for (int k = 0; k < ROWS; ++k) {
-      e2[k] = e1[k];
-      e1[k] = xe[k];
-      g2[k] = g1[k];
-      g1[k] = xg[k];
-      h2[k] = h1[k];
-      h1[k] = xh[k];
-      a2[k] = a1[k];
-      a1[k] = xa[k];
-    }
-    if (nw > 1) {
-      const int par = d & 1;
-      if (lane == 0) {
-        mbe[par * nw + wave] = e1[0];
-        mbg[par * nw + wave] = g1[0];
-        if (PEN) {
-          mbh[par * nw + wave] = h1[0];
-          mba[par * nw + wave] = a1[0];
-        }
+      // the column of global row 0 is complete: write its sums
+      if (SRC != SRC_COST) {
+        const int vo = (tid == 0 && d < M) ? 0 : kOob;
+        if (SRC == SRC_FEAT1) bdY.st(cy[0], vo, d * ES);
+        if (vgrad) bdVY.st(cvy[0], vo, d * ES);
       }
-      lds_barrier();
+#pragma unroll
+      for (int k = 0; k < ROWS; ++k) {
+        e2[k] = e1[k];
+        e1[k] = xe[k];
+        g2[k] = g1[k];
+        g1[k] = xg[k];
+        h2[k] = h1[k];
+        h1[k] = xh[k];
+        a2[k] = a1[k];
+        a1[k] = xa[k];
+      }
+      if (nw > 1) {
+        if (lane == 0) {
+          T* box = mb + 8 * ((d & 1) * nw + wave);
+          box[0] = e1[0];
+          box[1] = g1[0];
+          box[2] = h1[0];
+          box[3] = a1[0];
+          box[4] = yc[0];
+          box[5] = vyc[0];
+          box[6] = cy[0];
+          box[7] = cvy[0];
+        }
+        lds_barrier();
+      }
     }
-    off = off1;
   }
-
 #pragma unroll
   for (int k = 0; k < ROWS; ++k) {
     const int i = row0 + k;
     if (i < N) {
       if (SRC == SRC_FEAT1) a.dX[(size_t)b * N + i] = dxr[k];
       if (vgrad) a.dVX[(size_t)b * N + i] = dvr[k];
-    }
-  }
-  if (SRC != SRC_COST) {
-    __syncthreads();
-    for (int t = tid; t < M; t += blockDim.x) {
-      if (SRC == SRC_FEAT1) a.dY[(size_t)b * M + t] = dys[t];
-      if (vgrad) a.dVY[(size_t)b * M + t] = dvys[t];
     }
   }
 }
@@ -548,23 +625,18 @@ static Shape pick_shape(int N) {
   return {rows, threads};
 }
 
-template <typename T, int SRC, bool PEN>
-static size_t fwd_lds(int nw, int M) {
-  size_t n = 4 * (size_t)nw;
-  if (SRC == SRC_FEAT1) n += 2 * (size_t)M;
-  if (SRC == SRC_SQ) n += (size_t)M;
-  return n * sizeof(T);
+template <typename T, int SRC>
+static size_t col_lds(int M) {
+  return (SRC == SRC_FEAT1 ? 2 : SRC == SRC_SQ ? 1 : 0) * (size_t)M * sizeof(T);
 }
 
-template <typename T, int SRC, bool PEN>
-static size_t bwd_lds(int nw, int M) {
-  size_t n = 8 * (size_t)nw;
-  if (SRC == SRC_FEAT1) n += 4 * (size_t)M;
-  if (SRC == SRC_SQ) n += 2 * (size_t)M;
-  return n * sizeof(T);
-}
+// Prefetch depth (diagonals) of the register ring for a row count.
+template <int ROWS>
+struct PrefetchDepth {
+  static constexpr int value = ROWS == 1 ? 4 : (ROWS == 2 ? 2 : 1);
+};
 
-template <typename T, int SRC, bool PEN>
+template <typename T, int SRC, bool PEN, bool BAND>
 static int launch_udtw(bool backward, const UdtwArgs<T>& a, int B, hipStream_t stream,
                        const char* what) {
   if (B == 0) return TW_OK;
@@ -573,19 +645,26 @@ static int launch_udtw(bool backward, const UdtwArgs<T>& a, int B, hipStream_t s
     return fail(TW_ESIZE, "%s: the shorter sequence has %d steps; this build handles up to 16384",
                 what, a.N);
   }
+  if ((long long)a.N * a.M * (long long)sizeof(T) >= (1LL << 31)) {
+    return fail(TW_ESIZE, "%s: one pair's N*M matrix must stay below 2 GiB", what);
+  }
   const int nw = sh.threads / 64;
-  const size_t lds = backward ? bwd_lds<T, SRC, PEN>(nw, a.M) : fwd_lds<T, SRC, PEN>(nw, a.M);
+  const size_t lds = (backward ? 16 : 8) * (size_t)nw * sizeof(T) + col_lds<T, SRC>(a.M);
   if (lds > (size_t)max_lds_bytes()) {
     return fail(TW_ESIZE, "%s: %zu bytes of LDS needed (M = %d), %d available", what, lds, a.M,
                 max_lds_bytes());
   }
   dim3 grid(B), block(sh.threads);
-#define TW_UDTW_CASE(R_)                                                                   \
-  case R_:                                                                                 \
-    if (backward)                                                                          \
-      hipLaunchKernelGGL((udtw_bwd_kernel<T, R_, SRC, PEN>), grid, block, lds, stream, a); \
-    else                                                                                   \
-      hipLaunchKernelGGL((udtw_fwd_kernel<T, R_, SRC, PEN>), grid, block, lds, stream, a); \
+#define TW_UDTW_CASE(R_)                                                                     \
+  case R_:                                                                                   \
+    if (backward)                                                                            \
+      hipLaunchKernelGGL(                                                                    \
+          (udtw_bwd_kernel<T, R_, SRC, PEN, BAND, PrefetchDepth<R_>::value>), grid, block,   \
+          lds, stream, a);                                                                   \
+    else                                                                                     \
+      hipLaunchKernelGGL(                                                                    \
+          (udtw_fwd_kernel<T, R_, SRC, PEN, BAND, PrefetchDepth<R_>::value>), grid, block,   \
+          lds, stream, a);                                                                   \
     break;
   switch (sh.rows) {
     TW_UDTW_CASE(1)
@@ -603,8 +682,12 @@ static int launch_udtw(bool backward, const UdtwArgs<T>& a, int B, hipStream_t s
 template <typename T, int SRC>
 static int launch_pen(bool pen, bool backward, const UdtwArgs<T>& a, int B, hipStream_t s,
                       const char* what) {
-  return pen ? launch_udtw<T, SRC, true>(backward, a, B, s, what)
-             : launch_udtw<T, SRC, false>(backward, a, B, s, what);
+  const bool band = a.band > (T)0;
+  if (pen)
+    return band ? launch_udtw<T, SRC, true, true>(backward, a, B, s, what)
+                : launch_udtw<T, SRC, true, false>(backward, a, B, s, what);
+  return band ? launch_udtw<T, SRC, false, true>(backward, a, B, s, what)
+              : launch_udtw<T, SRC, false, false>(backward, a, B, s, what);
 }
 
 template <typename T>
@@ -646,7 +729,7 @@ static int cost_fwd(const T* C, const T* Q, int B, int N, int M, double gamma, d
 
 template <typename T>
 static int cost_bwd(const T* C, const T* Q, const T* R, const T* P, const T* gr, const T* gp,
-                    int B, int N, int M, double gamma, T* dC, T* dQ, hipStream_t s,
+                    int B, int N, int M, double gamma, double band, T* dC, T* dQ, hipStream_t s,
                     const char* what) {
   if (int e = check_dims(what, B, N, M, gamma)) return e;
   if (!C || !R || !gr || !dC) return fail(TW_EINVAL, "%s: null pointer", what);
@@ -663,7 +746,7 @@ static int cost_bwd(const T* C, const T* Q, const T* R, const T* P, const T* gr,
   a.dQ = pen ? dQ : nullptr;
   a.N = N;
   a.M = M;
-  set_hyper(a, gamma, 0.0, 1.0, 0.0);
+  set_hyper(a, gamma, 0.0, 1.0, band);
   return launch_pen<T, SRC_COST>(pen, true, a, B, s, what);
 }
 
@@ -676,7 +759,7 @@ template <typename T>
 int udtw_cost_bwd_any(const T* C, const T* Q, const T* R, const T* P, const T* gr, const T* gp,
                       int B, int N, int M, double gamma, T* dC, T* dQ, hipStream_t s,
                       const char* what) {
-  return cost_bwd<T>(C, Q, R, P, gr, gp, B, N, M, gamma, dC, dQ, s, what);
+  return cost_bwd<T>(C, Q, R, P, gr, gp, B, N, M, gamma, 0.0, dC, dQ, s, what);
 }
 template int udtw_cost_fwd_any<float>(const float*, const float*, int, int, int, double, double,
                                       float*, float*, float*, float*, hipStream_t, const char*);
@@ -714,17 +797,18 @@ int tw_udtw_cost_fwd_f64(const double* cost, const double* pen, int B, int N, in
 
 int tw_udtw_cost_bwd_f32(const float* cost, const float* pen, const float* R, const float* P,
                          const float* grad_dist, const float* grad_pen, int B, int N, int M,
-                         float gamma, float* d_cost, float* d_pen, hipStream_t stream) {
-  return cost_bwd<float>(cost, pen, R, P, grad_dist, grad_pen, B, N, M, gamma, d_cost, d_pen,
-                         stream, "tw_udtw_cost_bwd_f32");
+                         float gamma, float bandwidth, float* d_cost, float* d_pen,
+                         hipStream_t stream) {
+  return cost_bwd<float>(cost, pen, R, P, grad_dist, grad_pen, B, N, M, gamma, bandwidth, d_cost,
+                         d_pen, stream, "tw_udtw_cost_bwd_f32");
 }
 
 int tw_udtw_cost_bwd_f64(const double* cost, const double* pen, const double* R,
                          const double* P, const double* grad_dist, const double* grad_pen, int B,
-                         int N, int M, double gamma, double* d_cost, double* d_pen,
-                         hipStream_t stream) {
-  return cost_bwd<double>(cost, pen, R, P, grad_dist, grad_pen, B, N, M, gamma, d_cost, d_pen,
-                          stream, "tw_udtw_cost_bwd_f64");
+                         int N, int M, double gamma, double bandwidth, double* d_cost,
+                         double* d_pen, hipStream_t stream) {
+  return cost_bwd<double>(cost, pen, R, P, grad_dist, grad_pen, B, N, M, gamma, bandwidth,
+                          d_cost, d_pen, stream, "tw_udtw_cost_bwd_f64");
 }
 
 }  // extern "C"
@@ -775,7 +859,7 @@ static int feat_fwd(const T* X, const T* Y, const T* vx, const T* vy, int B, int
 template <typename T>
 static int feat_bwd(const T* X, const T* Y, const T* vx, const T* vy, const T* R, const T* P,
                     const T* gr, const T* gp, int B, int N, int M, int D, double gamma,
-                    double beta, double eps, T* dX, T* dY, T* dvx, T* dvy, T* ws,
+                    double beta, double eps, double band, T* dX, T* dY, T* dvx, T* dvy, T* ws,
                     size_t ws_bytes, hipStream_t s, const char* what) {
   if (int e = check_dims(what, B, N, M, gamma)) return e;
   if (D <= 0) return fail(TW_EINVAL, "%s: D must be > 0", what);
@@ -796,7 +880,7 @@ static int feat_bwd(const T* X, const T* Y, const T* vx, const T* vy, const T* R
   a.dVY = dvy;
   a.N = N;
   a.M = M;
-  set_hyper(a, gamma, beta, eps, 0.0);
+  set_hyper(a, gamma, beta, eps, band);
   if (D == 1) {
     a.X = X;
     a.Y = Y;
@@ -845,21 +929,22 @@ int tw_udtw_feat_fwd_f64(const double* X, const double* Y, const double* vx, con
 int tw_udtw_feat_bwd_f32(const float* X, const float* Y, const float* vx, const float* vy,
                          const float* R, const float* P, const float* grad_dist,
                          const float* grad_pen, int B, int N, int M, int D, float gamma,
-                         float beta, float eps, float* dX, float* dY, float* dvx, float* dvy,
-                         float* workspace, size_t workspace_bytes, hipStream_t stream) {
+                         float beta, float eps, float bandwidth, float* dX, float* dY,
+                         float* dvx, float* dvy, float* workspace, size_t workspace_bytes,
+                         hipStream_t stream) {
   return feat_bwd<float>(X, Y, vx, vy, R, P, grad_dist, grad_pen, B, N, M, D, gamma, beta, eps,
-                         dX, dY, dvx, dvy, workspace, workspace_bytes, stream,
+                         bandwidth, dX, dY, dvx, dvy, workspace, workspace_bytes, stream,
                          "tw_udtw_feat_bwd_f32");
 }
 
 int tw_udtw_feat_bwd_f64(const double* X, const double* Y, const double* vx, const double* vy,
                          const double* R, const double* P, const double* grad_dist,
                          const double* grad_pen, int B, int N, int M, int D, double gamma,
-                         double beta, double eps, double* dX, double* dY, double* dvx,
-                         double* dvy, double* workspace, size_t workspace_bytes,
+                         double beta, double eps, double bandwidth, double* dX, double* dY,
+                         double* dvx, double* dvy, double* workspace, size_t workspace_bytes,
                          hipStream_t stream) {
   return feat_bwd<double>(X, Y, vx, vy, R, P, grad_dist, grad_pen, B, N, M, D, gamma, beta, eps,
-                          dX, dY, dvx, dvy, workspace, workspace_bytes, stream,
+                          bandwidth, dX, dY, dvx, dvy, workspace, workspace_bytes, stream,
                           "tw_udtw_feat_bwd_f64");
 }
 

@@ -66,7 +66,8 @@ def dp_backward(cost: Tensor, penalty: Tensor, R: Tensor, P: Tensor, grad_r: Ten
     d_cost = torch.empty_like(c)
     d_pen = torch.empty_like(c) if pen else c.new_empty(0)
     _hip.call("tw_udtw_cost_bwd", c.dtype, c, q, R, P, grad_r.to(c.dtype).contiguous(),
-              grad_p.to(c.dtype).contiguous() if pen else None, B, N, M, gamma, d_cost, d_pen)
+              grad_p.to(c.dtype).contiguous() if pen else None, B, N, M, gamma, bandwidth, d_cost,
+              d_pen)
     return d_cost, d_pen
 
 
@@ -129,7 +130,7 @@ def fused_backward(X: Tensor, Y: Tensor, vx: Tensor, vy: Tensor, R: Tensor, P: T
     ws = _feat_ws(X, N, M)
     _hip.call("tw_udtw_feat_bwd", X.dtype, X, Y, vx, vy, R, P if pen else None,
               grad_r.to(X.dtype).contiguous(), grad_p.to(X.dtype).contiguous() if pen else None,
-              B, N, M, D, gamma, beta, eps, dX, dY, dvx, dvy, ws,
+              B, N, M, D, gamma, beta, eps, bandwidth, dX, dY, dvx, dvy, ws,
               0 if ws is None else ws.numel() * ws.element_size())
     return dX, dY, dvx, dvy
 
