@@ -145,6 +145,18 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Barrier for lagged wavefront pipelines: waits for every LDS operation of
+// this wave except the most recent one (the mailbox store just issued), then
+// joins the workgroup barrier. A mailbox record stored before barrier k is
+// therefore complete at barrier k+1; readers only touch it after that
+// barrier. LDS operations of a wave complete in order, so lgkmcnt <= 1
+// leaves at most the newest LDS operation pending even when scalar-memory
+// loads share the counter. The asm's memory clobber keeps the compiler from
+// moving memory operations across it.
+__device__ __forceinline__ void lag_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(1)\n\ts_barrier" ::: "memory");
+}
+
 // Number of cells on anti-diagonals 0..d-1 of an N x M grid (N <= M not required).
 __host__ __device__ __forceinline__ long long diag_offset(int d, int N, int M) {
   // cells (i, d' - i) with max(0, d'-M+1) <= i <= min(N-1, d'), summed over d' < d

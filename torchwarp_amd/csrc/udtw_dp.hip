@@ -34,6 +34,8 @@
 // touched by exactly one cell, so the adds never collide and their order is
 // fixed by the diagonal index (bitwise deterministic).
 
+#include <stdlib.h>
+
 #include "tw_capi.hpp"
 #include "tw_common.hpp"
 #include "../../include/torchwarp_hip.h"
@@ -115,24 +117,39 @@ __device__ __forceinline__ CellCost<T> cell_cost(const UdtwArgs<T>& a, T cin, T 
   return o;
 }
 
-// Column values (y, vy) travel with the wavefront: the cell of row i on
-// diagonal d uses column j = d - i, which row i-1 used on diagonal d-1, so a
-// row takes its column operands from the row above (forward) or below
-// (backward) with the same DPP shift that moves R. Only the row where a
-// column enters the sweep (row 0 forward, row N-1 backward) reads it from LDS.
-// The backward's column gradient sums ride along the same way and are
-// written out when the column leaves the sweep, in a fixed row order.
+// ------------------------------------------------------------- pipeline
 //
-// Global accesses are raw buffer operations with a lane-constant voffset and
-// a wave-uniform soffset; lanes outside the grid use an out-of-range voffset,
-// so their stores are dropped without branching. Loads of the cost source
-// (and, in the backward, of R/P) run PF diagonals ahead through a register ring.
+// Wavefront w of a workgroup runs LAG = 2 diagonals behind wavefront w-1
+// (forward; behind w+1 in the backward). The value a wavefront needs from its
+// neighbour at diagonal d was therefore stored two barriers earlier: it is
+// read from the LDS mailbox one step ahead and never waited for, and the
+// barrier itself only waits for LDS operations older than the mailbox store
+// just issued (lag_barrier). The edge wavefront feeds itself the same way:
+// it stores the border row and the column entering the sweep into its own
+// mailbox, so every wavefront runs one branch-free instruction stream.
+//
+// Column values (y, and half the column variance hy) travel with the sweep:
+// the cell of row i on diagonal d uses column j = d - i, which row i-1 used
+// on diagonal d-1, so a row takes its column operands from the row above
+// (forward) or below (backward) with the same DPP shift that moves R. The
+// backward's column-gradient sums ride along and are written out when their
+// column leaves the sweep at row 0, summed over rows in a fixed order.
+//
+// Global accesses are raw buffer operations with a lane-constant voffset
+// and a wave-uniform soffset; lanes outside the grid use an out-of-range
+// voffset, so their stores are dropped without branching. Loads of the cost
+// source (and, in the backward, of R/P) run PF diagonals ahead in a
+// register ring.
+
+constexpr int kLag = 2;
+constexpr int kSlots = 4;   // mailbox ring depth (> kLag + 1)
 
 template <typename T, int ROWS, int SRC, bool PEN, bool BAND, int PF>
 __global__ void __launch_bounds__(1024) udtw_fwd_kernel(UdtwArgs<T> a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T* sm = reinterpret_cast<T*>(smem_raw);
   constexpr int ES = sizeof(T);
+  constexpr bool COLS = SRC != SRC_COST;
   const int N = a.N, M = a.M;
   const int b = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
@@ -140,19 +157,30 @@ __global__ void __launch_bounds__(1024) udtw_fwd_kernel(UdtwArgs<T> a) {
   const T INF = inf_v<T>();
   const long long NM = (long long)N * M;
 
-  T* mb = sm;                                  // mailbox [2][nw][4]: R, P, y, vy
-  T* ys = sm + 8 * nw;                         // y  [M] (FEAT1)
-  T* vys = ys + (SRC == SRC_FEAT1 ? M : 0);    // vy [M] (SQ, FEAT1)
-  if (SRC == SRC_FEAT1)
-    for (int t = tid; t < M; t += blockDim.x) ys[t] = a.Y[(size_t)b * M + t];
-  if (SRC != SRC_COST)
-    for (int t = tid; t < M; t += blockDim.x) vys[t] = a.VY[(size_t)b * M + t];
-  for (int t = tid; t < 2 * nw; t += blockDim.x) {
-    mb[4 * t + 0] = INF;
-    mb[4 * t + 1] = (T)0;
-    mb[4 * t + 2] = (T)0;
-    mb[4 * t + 3] = (T)1;
+  // inbox[w][slot][4]: the row above wavefront w's first row on diagonal e
+  // (slot e & 3): R, P, y, hy.
+  T* inbox = sm;
+  T* cols = sm + 4 * kSlots * nw;   // (y, hy) per column
+  if (COLS) {
+    for (int t = tid; t < M; t += blockDim.x) {
+      cols[2 * t] = SRC == SRC_FEAT1 ? a.Y[(size_t)b * M + t] : (T)0;
+      cols[2 * t + 1] = (T)0.5 * a.VY[(size_t)b * M + t];
+    }
   }
+  for (int t = tid; t < kSlots * nw; t += blockDim.x) {
+    inbox[4 * t + 0] = INF;
+    inbox[4 * t + 1] = (T)0;
+    inbox[4 * t + 2] = (T)0;
+    inbox[4 * t + 3] = (T)0.5;
+  }
+  __syncthreads();
+  // border record of diagonal -1 for wavefront 0: column 0 enters row 0 on diagonal 0
+  if (COLS && tid == 0) {
+    T* r = inbox + 4 * (3 & (kSlots - 1));
+    r[2] = cols[0];
+    r[3] = cols[1];
+  }
+  __syncthreads();
 
   Buf bR, bP, bC, bQ;
   bR.init(a.R + b * NM, NM);
@@ -161,49 +189,58 @@ __global__ void __launch_bounds__(1024) udtw_fwd_kernel(UdtwArgs<T> a) {
   if (SRC == SRC_COST && PEN) bQ.init(a.Q + b * NM, NM);
 
   const int row0 = tid * ROWS;
-  T xr[ROWS], vxr[ROWS], r1[ROWS], r2[ROWS], p1[ROWS], p2[ROWS], yc[ROWS], vyc[ROWS];
+  T xr[ROWS], hxr[ROWS], r1[ROWS], r2[ROWS], p1[ROWS], p2[ROWS], yc[ROWS], hyc[ROWS];
 #pragma unroll
   for (int k = 0; k < ROWS; ++k) {
     const int i = row0 + k;
     xr[k] = (SRC == SRC_FEAT1 && i < N) ? a.X[(size_t)b * N + i] : (T)0;
-    vxr[k] = (SRC != SRC_COST && i < N) ? a.VX[(size_t)b * N + i] : (T)1;
+    hxr[k] = (COLS && i < N) ? (T)0.5 * a.VX[(size_t)b * N + i] : (T)0.5;
     r1[k] = r2[k] = INF;
     p1[k] = p2[k] = (T)0;
     yc[k] = (T)0;
-    vyc[k] = (T)1;
+    hyc[k] = (T)0.5;
   }
-  // Previous thread's last row on diagonals d-1 / d-2. For thread 0 this is
-  // the border; its 0 at the origin makes the update give R[0,0] = C[0,0].
+  // the row above this thread's first row on diagonals d-1 / d-2; for thread 0
+  // the border, whose 0 at the origin makes the update give R[0,0] = C[0,0]
   T nr1 = (tid == 0) ? (T)0 : INF, nr2 = INF, np1 = (T)0, np2 = (T)0;
 
-  // cost-source prefetch ring (natural [N, M] layout: cell (i, d-i) sits at
-  // element i*(M-1) + d)
+  const int d_first = -kLag * wave;
+  const int steps = N + M - 1 + kLag * (nw - 1);
+  T* my_inbox = inbox + 4 * kSlots * wave;
+  T* next_inbox = inbox + 4 * kSlots * (wave + 1);
+  const T* rec_src = my_inbox + 4 * ((d_first - 1) & (kSlots - 1));
+  T rec0 = rec_src[0], rec1 = rec_src[1], rec2 = rec_src[2], rec3 = rec_src[3];
+  // columns wavefront 0 writes into its own mailbox (one step ahead)
+  T self_y = (T)0, self_hy = (T)0.5;
+  if (COLS && wave == 0) {
+    const int c = 1 < M ? 1 : M - 1;
+    self_y = cols[2 * c];
+    self_hy = cols[2 * c + 1];
+  }
+
   T rc[PF][ROWS], rq[PF][ROWS];
   auto fetch = [&](int d, T* c, T* q) {
 #pragma unroll
     for (int k = 0; k < ROWS; ++k) {
       const int i = row0 + k, j = d - i;
       const int vo = (i < N && j >= 0 && j < M) ? i * (M - 1) * ES : kOob;
-      c[k] = bC.ld<T>(vo, d * ES);
-      if (SRC == SRC_COST && PEN) q[k] = bQ.ld<T>(vo, d * ES);
+      const int so = d > 0 ? d * ES : 0;
+      c[k] = bC.ld<T>(vo, so);
+      if (SRC == SRC_COST && PEN) q[k] = bQ.ld<T>(vo, so);
     }
   };
-  const int Dn = N + M - 1;
   if (SRC != SRC_FEAT1) {
 #pragma unroll
-    for (int u = 0; u < PF; ++u) fetch(u, rc[u], rq[u]);
+    for (int u = 0; u < PF; ++u) fetch(d_first + u, rc[u], rq[u]);
   }
-  __syncthreads();
 
-  T ycol_next = SRC == SRC_FEAT1 ? ys[0] : (T)0;
-  T vycol_next = SRC != SRC_COST ? vys[0] : (T)1;
-  long long off = 0;  // first element of diagonal d in the diagonal-major layout
-  for (int d0 = 0; d0 < Dn; d0 += PF) {
+  long long off = 0;   // first element of diagonal d (diagonal-major layout)
+  for (int t0 = 0; t0 < steps; t0 += PF) {
 #pragma unroll
     for (int u = 0; u < PF; ++u) {
-      const int d = d0 + u;
-      if (d >= Dn) break;
-      const int lo = max(0, d - M + 1), hi = min(N - 1, d);
+      const int tau = t0 + u;
+      if (tau >= steps) break;
+      const int d = d_first + tau;
       T cc[ROWS], cq[ROWS];
 #pragma unroll
       for (int k = 0; k < ROWS; ++k) {
@@ -212,38 +249,46 @@ __global__ void __launch_bounds__(1024) udtw_fwd_kernel(UdtwArgs<T> a) {
       }
       if (SRC != SRC_FEAT1) fetch(d + PF, rc[u], rq[u]);
 
-      // operands arriving at this thread's first row
-      T er, ep, ey, evy;
-      if (wave == 0) {
-        er = INF;
-        ep = (T)0;
-        ey = ycol_next;
-        evy = vycol_next;
-        const int dn = d + 1 < M ? d + 1 : M - 1;   // column entering on the next diagonal
-        if (SRC == SRC_FEAT1) ycol_next = ys[dn];
-        if (SRC != SRC_COST) vycol_next = vys[dn];
-      } else {
-        const T* box = mb + 4 * (((d - 1) & 1) * nw + wave - 1);
-        er = box[0];
-        ep = box[1];
-        ey = box[2];
-        evy = box[3];
+      // wavefront 0: border record of diagonal d (column d+1 enters next)
+      if (COLS && wave == 0 && lane == 0) {
+        T* r = my_inbox + 4 * (d & (kSlots - 1));
+        r[2] = self_y;
+        r[3] = self_hy;
       }
+      if (COLS && wave == 0) {
+        const int c = d + 2 < M ? d + 2 : M - 1;
+        self_y = cols[2 * c];
+        self_hy = cols[2 * c + 1];
+      }
+      // the record for diagonal d is what the next step needs
+      const T e0 = rec0, e1v = rec1, e2 = rec2, e3 = rec3;
+      {
+        const T* r = my_inbox + 4 * (d & (kSlots - 1));
+        rec0 = r[0];
+        rec1 = r[1];
+        rec2 = r[2];
+        rec3 = r[3];
+      }
+
       nr2 = nr1;
       np2 = np1;
-      nr1 = shift_prev(r1[ROWS - 1], er);
-      if (PEN) np1 = shift_prev(p1[ROWS - 1], ep);
-      const T ny = SRC == SRC_FEAT1 ? shift_prev(yc[ROWS - 1], ey) : (T)0;
-      const T nvy = SRC != SRC_COST ? shift_prev(vyc[ROWS - 1], evy) : (T)1;
+      nr1 = shift_prev(r1[ROWS - 1], e0);
+      if (PEN) np1 = shift_prev(p1[ROWS - 1], e1v);
+      {
+        const T ny = SRC == SRC_FEAT1 ? shift_prev(yc[ROWS - 1], e2) : (T)0;
+        const T nhy = COLS ? shift_prev(hyc[ROWS - 1], e3) : (T)0.5;
 #pragma unroll
-      for (int k = ROWS - 1; k > 0; --k) {
-        yc[k] = yc[k - 1];
-        vyc[k] = vyc[k - 1];
+        for (int k = ROWS - 1; k > 0; --k) {
+          yc[k] = yc[k - 1];
+          hyc[k] = hyc[k - 1];
+        }
+        yc[0] = ny;
+        hyc[0] = nhy;
       }
-      yc[0] = ny;
-      vyc[0] = nvy;
 
-      const int soff = (int)(off - lo) * ES;
+      const bool live = d >= 0 && d < N + M - 1;
+      const int lo = max(0, d - M + 1);
+      const int soff = live ? (int)(off - lo) * ES : 0;
       T nr[ROWS], np[ROWS];
 #pragma unroll
       for (int k = 0; k < ROWS; ++k) {
@@ -264,7 +309,7 @@ __global__ void __launch_bounds__(1024) udtw_fwd_kernel(UdtwArgs<T> a) {
           } else {
             sq = cc[k] > (T)0 ? cc[k] : (T)0;
           }
-          const T var_raw = (T)0.5 * (vxr[k] + vyc[k]);
+          const T var_raw = hxr[k] + hyc[k];   // (vx + vy) / 2, exactly
           const T var = var_raw > a.eps ? var_raw : a.eps;
           ch = sq * (rcp(var) * a.k);
           if (PEN) q = a.beta_ln2 * lg2(var);
@@ -295,24 +340,26 @@ __global__ void __launch_bounds__(1024) udtw_fwd_kernel(UdtwArgs<T> a) {
         p2[k] = p1[k];
         p1[k] = np[k];
       }
-      if (nw > 1) {
-        if (lane == 63) {
-          T* box = mb + 4 * ((d & 1) * nw + wave);
-          box[0] = r1[ROWS - 1];
-          box[1] = p1[ROWS - 1];
-          box[2] = yc[ROWS - 1];
-          box[3] = vyc[ROWS - 1];
-        }
-        lds_barrier();
-      }
-      off += hi - lo + 1;
-    }
-  }
+      if (d == N + M - 2) {
 #pragma unroll
-  for (int k = 0; k < ROWS; ++k) {
-    if (row0 + k == N - 1) {
-      a.out_r[b] = r1[k] < INF ? r1[k] * a.inv_k : INF;
-      a.out_p[b] = PEN ? p1[k] : (T)0;
+        for (int k = 0; k < ROWS; ++k) {
+          if (row0 + k == N - 1) {
+            a.out_r[b] = r1[k] < INF ? r1[k] * a.inv_k : INF;
+            a.out_p[b] = PEN ? p1[k] : (T)0;
+          }
+        }
+      }
+      if (live) off += min(N - 1, d) - lo + 1;
+      if (nw > 1) {
+        if (wave + 1 < nw && lane == 63) {
+          T* r = next_inbox + 4 * (d & (kSlots - 1));
+          r[0] = r1[ROWS - 1];
+          r[1] = p1[ROWS - 1];
+          r[2] = yc[ROWS - 1];
+          r[3] = hyc[ROWS - 1];
+        }
+        lag_barrier();
+      }
     }
   }
 }
@@ -322,27 +369,38 @@ __global__ void __launch_bounds__(1024) udtw_bwd_kernel(UdtwArgs<T> a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   T* sm = reinterpret_cast<T*>(smem_raw);
   constexpr int ES = sizeof(T);
+  constexpr bool COLS = SRC != SRC_COST;
   const int N = a.N, M = a.M;
   const int b = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const T INF = inf_v<T>();
   const long long NM = (long long)N * M;
-  const bool vgrad = SRC != SRC_COST && a.dVX != nullptr;
+  const bool vgrad = COLS && a.dVX != nullptr;
+  const int Dn = N + M - 1;
 
-  // mailbox [2][nw][8]: E, G (Rbar), H (Pbar), A, y, vy, column sums dy, dvy
-  T* mb = sm;
-  T* ys = sm + 16 * nw;                        // y  [M] (FEAT1)
-  T* vys = ys + (SRC == SRC_FEAT1 ? M : 0);    // vy [M] (SQ, FEAT1)
-  if (SRC == SRC_FEAT1)
-    for (int t = tid; t < M; t += blockDim.x) ys[t] = a.Y[(size_t)b * M + t];
-  if (SRC != SRC_COST)
-    for (int t = tid; t < M; t += blockDim.x) vys[t] = a.VY[(size_t)b * M + t];
-  for (int t = tid; t < 2 * nw; t += blockDim.x) {
-    mb[8 * t + 0] = -INF;
-#pragma unroll
-    for (int q = 1; q < 8; ++q) mb[8 * t + q] = (T)0;
+  // Rows are bottom-aligned: row N-1 is the last lane of the last wavefront,
+  // where every column enters the backward sweep.
+  const int shift = blockDim.x * ROWS - N;
+  const int row0 = tid * ROWS - shift;
+
+  // inbox[w][slot][8]: the row below wavefront w's last row on diagonal e:
+  // E, G (Rbar), H (Pbar), A, y, hy, column sums dy, dvy.
+  T* inbox = sm;
+  T* cols = sm + 8 * kSlots * nw;
+  if (COLS) {
+    for (int t = tid; t < M; t += blockDim.x) {
+      cols[2 * t] = SRC == SRC_FEAT1 ? a.Y[(size_t)b * M + t] : (T)0;
+      cols[2 * t + 1] = (T)0.5 * a.VY[(size_t)b * M + t];
+    }
   }
+  for (int t = tid; t < kSlots * nw; t += blockDim.x) {
+    inbox[8 * t + 0] = -INF;
+#pragma unroll
+    for (int q = 1; q < 8; ++q) inbox[8 * t + q] = (T)0;
+    inbox[8 * t + 5] = (T)0.5;
+  }
+  __syncthreads();
 
   Buf bR, bP, bC, bQ, bdC, bdQ, bdY, bdVY;
   bR.init(a.R + b * NM, NM);
@@ -359,56 +417,81 @@ __global__ void __launch_bounds__(1024) udtw_bwd_kernel(UdtwArgs<T> a) {
   if (vgrad) bdVY.init(a.dVY + (size_t)b * M, M);
   const bool want_dq = SRC == SRC_COST && PEN && a.dQ != nullptr;
 
-  const int row0 = tid * ROWS;
-  T xr[ROWS], vxr[ROWS], dxr[ROWS], dvr[ROWS];
+  T xr[ROWS], hxr[ROWS], dxr[ROWS], dvr[ROWS];
   T e1[ROWS], e2[ROWS], g1[ROWS], g2[ROWS], h1[ROWS], h2[ROWS], a1[ROWS], a2[ROWS];
-  T yc[ROWS], vyc[ROWS], cy[ROWS], cvy[ROWS];
+  T yc[ROWS], hyc[ROWS], cy[ROWS], cvy[ROWS];
 #pragma unroll
   for (int k = 0; k < ROWS; ++k) {
     const int i = row0 + k;
-    xr[k] = (SRC == SRC_FEAT1 && i < N) ? a.X[(size_t)b * N + i] : (T)0;
-    vxr[k] = (SRC != SRC_COST && i < N) ? a.VX[(size_t)b * N + i] : (T)1;
+    const bool in = i >= 0 && i < N;
+    xr[k] = (SRC == SRC_FEAT1 && in) ? a.X[(size_t)b * N + i] : (T)0;
+    hxr[k] = (COLS && in) ? (T)0.5 * a.VX[(size_t)b * N + i] : (T)0.5;
     dxr[k] = dvr[k] = (T)0;
     e1[k] = e2[k] = -INF;
     g1[k] = g2[k] = h1[k] = h2[k] = a1[k] = a2[k] = (T)0;
     yc[k] = cy[k] = cvy[k] = (T)0;
-    vyc[k] = (T)1;
+    hyc[k] = (T)0.5;
   }
-  // next thread's first row on diagonals d+1 / d+2
+  // the row below this thread's last row on diagonals d+1 / d+2
   T ne1 = -INF, ne2 = -INF, ng1 = 0, ng2 = 0, nh1 = 0, nh2 = 0, na1 = 0, na2 = 0;
   const T gr = a.gr[b];
   const T gp = PEN ? a.gp[b] : (T)0;
-  const int Dn = N + M - 1;
 
-  // prefetch ring: R, P (diagonal-major) and the cost source (natural layout)
+  const int d_first = Dn - 1 + kLag * (nw - 1 - wave);
+  const int steps = Dn + kLag * (nw - 1);
+  T* my_inbox = inbox + 8 * kSlots * wave;
+  T* prev_inbox = inbox + 8 * kSlots * (wave - 1);
+  const bool last_wave = wave == nw - 1;
+  // the virtual row N on diagonal Dn: column M-1 enters row N-1 on diagonal Dn-1
+  if (COLS && last_wave && lane == 0) {
+    T* r = my_inbox + 8 * (Dn & (kSlots - 1));
+    r[4] = cols[2 * (M - 1)];
+    r[5] = cols[2 * (M - 1) + 1];
+  }
+  __syncthreads();
+  T rec[8];
+  {
+    const T* r = my_inbox + 8 * ((d_first + 1) & (kSlots - 1));
+#pragma unroll
+    for (int q = 0; q < 8; ++q) rec[q] = r[q];
+  }
+  // column the last wavefront stores for the virtual row N on diagonal d
+  // (column d - N), one step ahead
+  T self_y = (T)0, self_hy = (T)0.5;
+  if (COLS && last_wave) {
+    const int c = min(max(Dn - 1 - N, 0), M - 1);
+    self_y = cols[2 * c];
+    self_hy = cols[2 * c + 1];
+  }
+
   T rr[PF][ROWS], rp[PF][ROWS], rc[PF][ROWS], rq[PF][ROWS];
   auto fetch = [&](int d, T* r, T* p, T* c, T* q) {
+    const bool live = d >= 0 && d < Dn;
     const int lo = max(0, d - M + 1);
-    const int soff_d = d >= 0 ? (int)(diag_offset(d, N, M) - lo) * ES : 0;
+    const int soff_d = live ? (int)(diag_offset(d, N, M) - lo) * ES : 0;
 #pragma unroll
     for (int k = 0; k < ROWS; ++k) {
       const int i = row0 + k, j = d - i;
-      const bool v = d >= 0 && i < N && j >= 0 && j < M;
+      const bool v = live && i >= 0 && i < N && j >= 0 && j < M;
       r[k] = bR.ld<T>(v ? i * ES : kOob, soff_d);
       if (PEN) p[k] = bP.ld<T>(v ? i * ES : kOob, soff_d);
       if (SRC != SRC_FEAT1) {
         const int vn = v ? i * (M - 1) * ES : kOob;
-        c[k] = bC.ld<T>(vn, d >= 0 ? d * ES : 0);
-        if (SRC == SRC_COST && PEN) q[k] = bQ.ld<T>(vn, d >= 0 ? d * ES : 0);
+        const int so = live ? d * ES : 0;
+        c[k] = bC.ld<T>(vn, so);
+        if (SRC == SRC_COST && PEN) q[k] = bQ.ld<T>(vn, so);
       }
     }
   };
 #pragma unroll
-  for (int u = 0; u < PF; ++u) fetch(Dn - 1 - u, rr[u], rp[u], rc[u], rq[u]);
-  __syncthreads();
-  T ycol_next = SRC == SRC_FEAT1 ? ys[M - 1] : (T)0;   // column M-1 enters first
-  T vycol_next = SRC != SRC_COST ? vys[M - 1] : (T)1;
+  for (int u = 0; u < PF; ++u) fetch(d_first - u, rr[u], rp[u], rc[u], rq[u]);
 
-  for (int d0 = Dn - 1; d0 >= 0; d0 -= PF) {
+  for (int t0 = 0; t0 < steps; t0 += PF) {
 #pragma unroll
     for (int u = 0; u < PF; ++u) {
-      const int d = d0 - u;
-      if (d < 0) break;
+      const int tau = t0 + u;
+      if (tau >= steps) break;
+      const int d = d_first - tau;
       T cr[ROWS], cp[ROWS], cc[ROWS], cq[ROWS];
 #pragma unroll
       for (int k = 0; k < ROWS; ++k) {
@@ -419,73 +502,60 @@ __global__ void __launch_bounds__(1024) udtw_bwd_kernel(UdtwArgs<T> a) {
       }
       fetch(d - PF, rr[u], rp[u], rc[u], rq[u]);
 
-      // operands arriving at this thread's last row from the next thread (step d+1)
-      T ed_, eg_, eh_, ea_, ey_, evy_, ecy_, ecvy_;
-      if (wave == nw - 1) {
-        ed_ = -INF;
-        eg_ = eh_ = ea_ = ey_ = ecy_ = ecvy_ = (T)0;
-        evy_ = (T)1;
-      } else {
-        const T* box = mb + 8 * (((d + 1) & 1) * nw + wave + 1);
-        ed_ = box[0];
-        eg_ = box[1];
-        eh_ = box[2];
-        ea_ = box[3];
-        ey_ = box[4];
-        evy_ = box[5];
-        ecy_ = box[6];
-        ecvy_ = box[7];
+      // last wavefront: virtual row N on diagonal d (column d - N enters row N-1 on d-1)
+      if (COLS && last_wave && lane == 0) {
+        T* r = my_inbox + 8 * (d & (kSlots - 1));
+        r[4] = self_y;
+        r[5] = self_hy;
       }
+      if (COLS && last_wave) {
+        const int c = min(max(d - 1 - N, 0), M - 1);
+        self_y = cols[2 * c];
+        self_hy = cols[2 * c + 1];
+      }
+      T er[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) er[q] = rec[q];
+      {
+        const T* r = my_inbox + 8 * (d & (kSlots - 1));
+#pragma unroll
+        for (int q = 0; q < 8; ++q) rec[q] = r[q];
+      }
+
       ne2 = ne1;
       ng2 = ng1;
       nh2 = nh1;
       na2 = na1;
-      ne1 = shift_next(e1[0], ed_);
-      ng1 = shift_next(g1[0], eg_);
+      ne1 = shift_next(e1[0], er[0]);
+      ng1 = shift_next(g1[0], er[1]);
       if (PEN) {
-        nh1 = shift_next(h1[0], eh_);
-        na1 = shift_next(a1[0], ea_);
+        nh1 = shift_next(h1[0], er[2]);
+        na1 = shift_next(a1[0], er[3]);
       }
-      // columns move up one row; a new column enters at row N-1
-      {
-        const T fy = SRC == SRC_FEAT1 ? shift_next(yc[0], ey_) : (T)0;
-        const T fvy = SRC != SRC_COST ? shift_next(vyc[0], evy_) : (T)1;
-        const T fcy = SRC == SRC_FEAT1 ? shift_next(cy[0], ecy_) : (T)0;
-        const T fcvy = SRC != SRC_COST ? shift_next(cvy[0], ecvy_) : (T)0;
+      if (COLS) {
+        const T fy = SRC == SRC_FEAT1 ? shift_next(yc[0], er[4]) : (T)0;
+        const T fhy = shift_next(hyc[0], er[5]);
+        const T fcy = SRC == SRC_FEAT1 ? shift_next(cy[0], er[6]) : (T)0;
+        const T fcvy = vgrad ? shift_next(cvy[0], er[7]) : (T)0;
 #pragma unroll
         for (int k = 0; k + 1 < ROWS; ++k) {
           yc[k] = yc[k + 1];
-          vyc[k] = vyc[k + 1];
+          hyc[k] = hyc[k + 1];
           cy[k] = cy[k + 1];
           cvy[k] = cvy[k + 1];
         }
         yc[ROWS - 1] = fy;
-        vyc[ROWS - 1] = fvy;
+        hyc[ROWS - 1] = fhy;
         cy[ROWS - 1] = fcy;
         cvy[ROWS - 1] = fcvy;
-        if (SRC != SRC_COST) {
-          const T ny = ycol_next, nvy = vycol_next;
-          const int jn = d - 1 - (N - 1);                 // column entering on diagonal d-1
-          const int jc = jn < 0 ? 0 : (jn >= M ? M - 1 : jn);
-          if (SRC == SRC_FEAT1) ycol_next = ys[jc];
-          vycol_next = vys[jc];
-#pragma unroll
-          for (int k = 0; k < ROWS; ++k) {
-            if (row0 + k == N - 1) {
-              yc[k] = ny;
-              vyc[k] = nvy;
-              cy[k] = (T)0;
-              cvy[k] = (T)0;
-            }
-          }
-        }
       }
 
+      const bool live = d >= 0 && d < Dn;
       T xe[ROWS], xg[ROWS], xh[ROWS], xa[ROWS];
 #pragma unroll
       for (int k = 0; k < ROWS; ++k) {
         const int i = row0 + k, j = d - i;
-        const bool valid = (i < N) & ((unsigned)j < (unsigned)M);
+        const bool valid = (i >= 0) & (i < N) & ((unsigned)j < (unsigned)M);
         const T rk = valid ? cr[k] : INF;
         const T pk = cp[k];
         T ch, q = (T)0, c = (T)0, rv = (T)1, sq_raw = (T)0, var_raw = (T)1;
@@ -500,7 +570,7 @@ __global__ void __launch_bounds__(1024) udtw_bwd_kernel(UdtwArgs<T> a) {
             sq_raw = cc[k];
           }
           const T sq = sq_raw > (T)0 ? sq_raw : (T)0;
-          var_raw = (T)0.5 * (vxr[k] + vyc[k]);
+          var_raw = hxr[k] + hyc[k];
           const T var = var_raw > a.eps ? var_raw : a.eps;
           rv = rcp(var);
           c = sq * rv;
@@ -545,12 +615,13 @@ __global__ void __launch_bounds__(1024) udtw_bwd_kernel(UdtwArgs<T> a) {
         xa[k] = valid ? pk - q : (T)0;
 
         const int vn = valid ? i * (M - 1) * ES : kOob;
+        const int so = live ? d * ES : 0;
         if (SRC == SRC_COST) {
-          bdC.st(g, vn, d * ES);
-          if (want_dq) bdQ.st(h, vn, d * ES);
+          bdC.st(g, vn, so);
+          if (want_dq) bdQ.st(h, vn, so);
         } else {
           const T dsq = sq_raw > (T)0 ? g * rv : (T)0;
-          if (SRC == SRC_SQ) bdC.st(dsq, vn, d * ES);
+          if (SRC == SRC_SQ) bdC.st(dsq, vn, so);
           if (SRC == SRC_FEAT1) {
             const T df = valid ? (T)2 * dsq * (xr[k] - yc[k]) : (T)0;
             dxr[k] += df;
@@ -562,13 +633,11 @@ __global__ void __launch_bounds__(1024) udtw_bwd_kernel(UdtwArgs<T> a) {
             dvr[k] += dvar;
             cvy[k] += dvar;
           }
+          // column d leaves the sweep at row 0: store its sums
+          const int vc = (row0 + k == 0 && d >= 0 && d < M) ? 0 : kOob;
+          if (SRC == SRC_FEAT1) bdY.st(cy[k], vc, so);
+          if (vgrad) bdVY.st(cvy[k], vc, so);
         }
-      }
-      // the column of global row 0 is complete: write its sums
-      if (SRC != SRC_COST) {
-        const int vo = (tid == 0 && d < M) ? 0 : kOob;
-        if (SRC == SRC_FEAT1) bdY.st(cy[0], vo, d * ES);
-        if (vgrad) bdVY.st(cvy[0], vo, d * ES);
       }
 #pragma unroll
       for (int k = 0; k < ROWS; ++k) {
@@ -582,25 +651,25 @@ __global__ void __launch_bounds__(1024) udtw_bwd_kernel(UdtwArgs<T> a) {
         a1[k] = xa[k];
       }
       if (nw > 1) {
-        if (lane == 0) {
-          T* box = mb + 8 * ((d & 1) * nw + wave);
-          box[0] = e1[0];
-          box[1] = g1[0];
-          box[2] = h1[0];
-          box[3] = a1[0];
-          box[4] = yc[0];
-          box[5] = vyc[0];
-          box[6] = cy[0];
-          box[7] = cvy[0];
+        if (wave > 0 && lane == 0) {
+          T* r = prev_inbox + 8 * (d & (kSlots - 1));
+          r[0] = e1[0];
+          r[1] = g1[0];
+          r[2] = h1[0];
+          r[3] = a1[0];
+          r[4] = yc[0];
+          r[5] = hyc[0];
+          r[6] = cy[0];
+          r[7] = cvy[0];
         }
-        lds_barrier();
+        lag_barrier();
       }
     }
   }
 #pragma unroll
   for (int k = 0; k < ROWS; ++k) {
     const int i = row0 + k;
-    if (i < N) {
+    if (i >= 0 && i < N) {
       if (SRC == SRC_FEAT1) a.dX[(size_t)b * N + i] = dxr[k];
       if (vgrad) a.dVX[(size_t)b * N + i] = dvr[k];
     }
@@ -619,15 +688,23 @@ struct Shape {
 static Shape pick_shape(int N) {
   int rows = 1;
   while (rows < 16 && (N + rows - 1) / rows > 256) rows *= 2;
+  // tuning override: TORCHWARP_UDTW_ROWS = 1, 2, 4, 8 or 16 rows per thread
+  static const int forced = [] {
+    const char* e = getenv("TORCHWARP_UDTW_ROWS");
+    return e ? atoi(e) : 0;
+  }();
+  if (forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16) rows = forced;
   int threads = (N + rows - 1) / rows;
   if (threads > 1024) return {0, 0};
   threads = ((threads + 63) / 64) * 64;
   return {rows, threads};
 }
 
+// LDS of one workgroup: mailbox rings plus the (y, hy) table of the columns.
 template <typename T, int SRC>
-static size_t col_lds(int M) {
-  return (SRC == SRC_FEAT1 ? 2 : SRC == SRC_SQ ? 1 : 0) * (size_t)M * sizeof(T);
+static size_t udtw_lds(bool backward, int nw, int M) {
+  const size_t box = (backward ? 8 : 4) * (size_t)kSlots * nw;
+  return (box + (SRC != SRC_COST ? 2 * (size_t)M : 0)) * sizeof(T);
 }
 
 // Prefetch depth (diagonals) of the register ring for a row count.
@@ -649,7 +726,7 @@ static int launch_udtw(bool backward, const UdtwArgs<T>& a, int B, hipStream_t s
     return fail(TW_ESIZE, "%s: one pair's N*M matrix must stay below 2 GiB", what);
   }
   const int nw = sh.threads / 64;
-  const size_t lds = (backward ? 16 : 8) * (size_t)nw * sizeof(T) + col_lds<T, SRC>(a.M);
+  const size_t lds = udtw_lds<T, SRC>(backward, nw, a.M);
   if (lds > (size_t)max_lds_bytes()) {
     return fail(TW_ESIZE, "%s: %zu bytes of LDS needed (M = %d), %d available", what, lds, a.M,
                 max_lds_bytes());
