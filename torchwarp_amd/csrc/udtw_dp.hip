@@ -30,10 +30,11 @@
 //             Q = beta ln max(...)                      -> writes dS, dvx, dvy
 //   SRC_FEAT1 one feature per step, x [B,N], y [B,M] and variances,
 //             C from (x-y)^2 in registers               -> writes dx, dy, dvx, dvy
-// Column sums (dy, dvy) accumulate in LDS: on one diagonal every column is
-// touched by exactly one cell, so the adds never collide and their order is
-// fixed by the diagonal index (bitwise deterministic).
+// Column sums (dy, dvy) travel up the rows with their column and are stored
+// when the column leaves the sweep, so their order of summation is fixed
+// (bitwise deterministic).
 
+#include <limits.h>
 #include <stdlib.h>
 
 #include "tw_capi.hpp"
@@ -74,80 +75,84 @@ struct UdtwArgs {
   T band;        // <= 0: no band
 };
 
-// Cell cost in the scaled domain plus the pieces the chain rule needs.
-template <typename T>
-struct CellCost {
-  T ch;       // scaled cost  C * log2(e)/g
-  T q;        // penalty
-  T c;        // unscaled cost (SRC_SQ / SRC_FEAT1)
-  T rv;       // 1 / var
-  T sq_raw;   // squared distance before the clamp
-  T var_raw;  // variance before the clamp
-};
-
-template <typename T, int SRC, bool PEN>
-__device__ __forceinline__ CellCost<T> cell_cost(const UdtwArgs<T>& a, T cin, T qin, T x, T vx,
-                                                 T y, T vy) {
-  CellCost<T> o;
-  if (SRC == SRC_COST) {
-    o.c = cin;
-    o.ch = cin * a.k;
-    o.q = PEN ? qin : (T)0;
-    o.rv = (T)1;
-    o.sq_raw = (T)0;
-    o.var_raw = (T)1;
-  } else {
-    T sq_raw;
-    if (SRC == SRC_FEAT1) {
-      const T df = x - y;
-      sq_raw = df * df;
-    } else {
-      sq_raw = cin;
-    }
-    const T sq = sq_raw > (T)0 ? sq_raw : (T)0;
-    const T var_raw = (T)0.5 * (vx + vy);
-    const T var = var_raw > a.eps ? var_raw : a.eps;
-    o.rv = rcp(var);
-    o.c = sq * o.rv;
-    o.ch = o.c * a.k;
-    o.q = PEN ? a.beta_ln2 * lg2(var) : (T)0;
-    o.sq_raw = sq_raw;
-    o.var_raw = var_raw;
-  }
-  return o;
-}
-
 // ------------------------------------------------------------- pipeline
 //
-// Wavefront w of a workgroup runs LAG = 2 diagonals behind wavefront w-1
-// (forward; behind w+1 in the backward). The value a wavefront needs from its
-// neighbour at diagonal d was therefore stored two barriers earlier: it is
-// read from the LDS mailbox one step ahead and never waited for, and the
-// barrier itself only waits for LDS operations older than the mailbox store
-// just issued (lag_barrier). The edge wavefront feeds itself the same way:
-// it stores the border row and the column entering the sweep into its own
-// mailbox, so every wavefront runs one branch-free instruction stream.
+// Wavefront w of a workgroup runs kLag = 2 diagonals behind wavefront w-1
+// (forward; behind w+1 in the backward). At global step tau every wavefront
+// stores its boundary row into slot tau % 4 of its neighbour's mailbox and
+// reads the record stored two steps earlier (slot (tau + 2) % 4), which it
+// uses on the following step. lag_barrier() leaves only the newest LDS
+// operation in flight, so a record is complete one barrier after it is
+// stored and is read after the next barrier: no mailbox latency and no
+// barrier-side wait sit on the dependency chain. The store is one
+// instruction for the whole wavefront: the lane holding the boundary row
+// writes the mailbox slot, the other lanes a private dump area, so no
+// exec-mask branch is needed. The edge wavefront writes its own records (the
+// border row and the column entering the sweep). Four steps are unrolled per
+// loop trip so mailbox slots, prefetch registers and buffer offsets of a
+// step are compile-time constants.
 //
-// Column values (y, and half the column variance hy) travel with the sweep:
-// the cell of row i on diagonal d uses column j = d - i, which row i-1 used
-// on diagonal d-1, so a row takes its column operands from the row above
-// (forward) or below (backward) with the same DPP shift that moves R. The
-// backward's column-gradient sums ride along and are written out when their
-// column leaves the sweep at row 0, summed over rows in a fixed order.
+// Column values (y and hy = half the column variance) travel with the sweep:
+// row i on diagonal d uses column j = d - i, which row i-1 used on diagonal
+// d-1, so a row takes its column operands from the row above (forward) or
+// below (backward) with the DPP shift that moves R. The backward's column
+// gradient sums ride along the same way and are stored when their column
+// leaves the sweep at row 0, summed over rows in a fixed order.
 //
-// Global accesses are raw buffer operations with a lane-constant voffset
-// and a wave-uniform soffset; lanes outside the grid use an out-of-range
-// voffset, so their stores are dropped without branching. Loads of the cost
-// source (and, in the backward, of R/P) run PF diagonals ahead in a
-// register ring.
+// Global accesses are raw buffer operations with a lane-constant voffset and
+// a wave-uniform, non-negative soffset. The hardware range check covers the
+// voffset only; lanes outside the grid pass an out-of-range voffset, so their
+// loads return 0 and their stores are dropped without branching.
 
 constexpr int kLag = 2;
-constexpr int kSlots = 4;   // mailbox ring depth (> kLag + 1)
+constexpr int kSlots = 4;   // mailbox ring depth; also the steps per loop trip
+constexpr int kDump = 64 + kSlots;
+
+template <typename T>
+struct alignas(4 * sizeof(T)) Rec4 {
+  T x, y, z, w;
+};
+template <typename T>
+struct alignas(4 * sizeof(T)) Rec8 {
+  Rec4<T> a, b;
+};
+
+// Wave-uniform integer min / max on the scalar unit. Offsets built from them
+// stay in scalar registers; the compiler would otherwise fold nested min/max
+// into a vector min3 and carry the offset in a vector register. The operands
+// pass through readfirstlane so a vector copy of a uniform value never
+// reaches the scalar instruction.
+__device__ __forceinline__ int smin(int a, int b) {
+  int r;
+  asm("s_min_i32 %0, %1, %2"
+      : "=s"(r)
+      : "s"(__builtin_amdgcn_readfirstlane(a)), "s"(__builtin_amdgcn_readfirstlane(b))
+      : "scc");
+  return r;
+}
+__device__ __forceinline__ int smax(int a, int b) {
+  int r;
+  asm("s_max_i32 %0, %1, %2"
+      : "=s"(r)
+      : "s"(__builtin_amdgcn_readfirstlane(a)), "s"(__builtin_amdgcn_readfirstlane(b))
+      : "scc");
+  return r;
+}
+
+// soff(e+1) - soff(e) for soff(e) = (index of the first cell of diagonal e)
+// - (row of that cell) in the diagonal-major layout, N <= M; 0 outside the grid.
+__device__ __forceinline__ int diag_step(int e, int N, int M) {
+  return smax(0, smin(smin(e + 1, N), N + M - 2 - e));
+}
+
+template <int ROWS>
+struct MaxThreads {
+  static constexpr int value = ROWS >= 16 ? 1024 : 256;
+};
 
 template <typename T, int ROWS, int SRC, bool PEN, bool BAND, int PF>
-__global__ void __launch_bounds__(1024) udtw_fwd_kernel(UdtwArgs<T> a) {
+__global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwArgs<T> a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  T* sm = reinterpret_cast<T*>(smem_raw);
   constexpr int ES = sizeof(T);
   constexpr bool COLS = SRC != SRC_COST;
   const int N = a.N, M = a.M;
@@ -156,40 +161,45 @@ __global__ void __launch_bounds__(1024) udtw_fwd_kernel(UdtwArgs<T> a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const T INF = inf_v<T>();
   const long long NM = (long long)N * M;
+  const int Dn = N + M - 1;
 
-  // inbox[w][slot][4]: the row above wavefront w's first row on diagonal e
-  // (slot e & 3): R, P, y, hy.
-  T* inbox = sm;
-  T* cols = sm + 4 * kSlots * nw;   // (y, hy) per column
-  if (COLS) {
-    for (int t = tid; t < M; t += blockDim.x) {
-      cols[2 * t] = SRC == SRC_FEAT1 ? a.Y[(size_t)b * M + t] : (T)0;
-      cols[2 * t + 1] = (T)0.5 * a.VY[(size_t)b * M + t];
-    }
-  }
-  for (int t = tid; t < kSlots * nw; t += blockDim.x) {
-    inbox[4 * t + 0] = INF;
-    inbox[4 * t + 1] = (T)0;
-    inbox[4 * t + 2] = (T)0;
-    inbox[4 * t + 3] = (T)0.5;
-  }
-  __syncthreads();
-  // border record of diagonal -1 for wavefront 0: column 0 enters row 0 on diagonal 0
-  if (COLS && tid == 0) {
-    T* r = inbox + 4 * (3 & (kSlots - 1));
-    r[2] = cols[0];
-    r[3] = cols[1];
-  }
-  __syncthreads();
+  // box[v * kSlots + slot]: wavefront v's inbox (the row above its first
+  // row; box[nw] is the last wavefront's unread outbox), then the dump area.
+  Rec4<T>* box = reinterpret_cast<Rec4<T>*>(smem_raw);
+  Rec4<T>* dump = box + (nw + 1) * kSlots;
+  for (int t = tid; t < (nw + 1) * kSlots; t += blockDim.x) box[t] = {INF, (T)0, (T)0, (T)0.5};
 
-  Buf bR, bP, bC, bQ;
+  Buf bR, bP, bC, bQ, bY, bVY;
   bR.init(a.R + b * NM, NM);
   if (PEN) bP.init(a.P + b * NM, NM);
   if (SRC != SRC_FEAT1) bC.init(a.C + b * NM, NM);
   if (SRC == SRC_COST && PEN) bQ.init(a.Q + b * NM, NM);
+  if (SRC == SRC_FEAT1) bY.init(a.Y + (size_t)b * M, M);
+  if (COLS) bVY.init(a.VY + (size_t)b * M, M);
+  // column j's y and variance (wave-uniform loads; j is clamped into the sequence)
+  auto col_y = [&](int j) -> T {
+    return SRC == SRC_FEAT1 ? bY.ld<T>(0, smin(smax(j, 0), M - 1) * ES) : (T)0;
+  };
+  auto col_vy = [&](int j) -> T {
+    return COLS ? bVY.ld<T>(0, smin(smax(j, 0), M - 1) * ES) : (T)1;
+  };
+
+  Rec4<T>* const inbox = box + wave * kSlots;
+  Rec4<T>* const outbox = box + (wave + 1) * kSlots;
+  // the mailbox store of a step: lane 63 to the slot, the others to the dump
+  Rec4<T>* const my_out = lane == 63 ? outbox : dump + lane;
+  Rec4<T>* const my_self = lane == 63 ? inbox : dump + lane;
+  __syncthreads();
+  // record used on step 0 by wavefront 0: border row on diagonal -1, column 0 entering
+  if (wave == 0) {
+    const T y0 = col_y(0), hy0 = (T)0.5 * col_vy(0);
+    if (lane == 63) inbox[1] = {INF, (T)0, y0, hy0};
+  }
+  __syncthreads();
 
   const int row0 = tid * ROWS;
   T xr[ROWS], hxr[ROWS], r1[ROWS], r2[ROWS], p1[ROWS], p2[ROWS], yc[ROWS], hyc[ROWS];
+  int vst[ROWS], vnat[ROWS], jb[ROWS];
 #pragma unroll
   for (int k = 0; k < ROWS; ++k) {
     const int i = row0 + k;
@@ -199,32 +209,31 @@ __global__ void __launch_bounds__(1024) udtw_fwd_kernel(UdtwArgs<T> a) {
     p1[k] = p2[k] = (T)0;
     yc[k] = (T)0;
     hyc[k] = (T)0.5;
+    vst[k] = i * ES;                          // row offset within a diagonal
+    vnat[k] = i < N ? i * (M - 1) * ES : 0;   // [N, M] offset of (i, d - i) minus d
+    jb[k] = i < N ? -i : INT_MIN / 2;         // column of row i on diagonal d is d + jb
   }
-  // the row above this thread's first row on diagonals d-1 / d-2; for thread 0
-  // the border, whose 0 at the origin makes the update give R[0,0] = C[0,0]
   T nr1 = (tid == 0) ? (T)0 : INF, nr2 = INF, np1 = (T)0, np2 = (T)0;
 
   const int d_first = -kLag * wave;
-  const int steps = N + M - 1 + kLag * (nw - 1);
-  T* my_inbox = inbox + 4 * kSlots * wave;
-  T* next_inbox = inbox + 4 * kSlots * (wave + 1);
-  const T* rec_src = my_inbox + 4 * ((d_first - 1) & (kSlots - 1));
-  T rec0 = rec_src[0], rec1 = rec_src[1], rec2 = rec_src[2], rec3 = rec_src[3];
-  // columns wavefront 0 writes into its own mailbox (one step ahead)
-  T self_y = (T)0, self_hy = (T)0.5;
-  if (COLS && wave == 0) {
-    const int c = 1 < M ? 1 : M - 1;
-    self_y = cols[2 * c];
-    self_hy = cols[2 * c + 1];
+  const int steps = (Dn + kLag * (nw - 1) + kSlots - 1) / kSlots * kSlots;
+  Rec4<T> nxt = inbox[1];
+  // column entering row 0 on the diagonal after step u's, loaded kSlots
+  // steps ahead by every wavefront (wavefront 0 uses them): no divergent
+  // loads, so the ring stays in place and its wait lands at the use
+  T ey_ring[kSlots], evy_ring[kSlots];
+#pragma unroll
+  for (int u = 0; u < kSlots; ++u) {
+    ey_ring[u] = col_y(u + 1);
+    evy_ring[u] = col_vy(u + 1);
   }
 
   T rc[PF][ROWS], rq[PF][ROWS];
   auto fetch = [&](int d, T* c, T* q) {
+    const int so = smax(d, 0) * ES;
 #pragma unroll
     for (int k = 0; k < ROWS; ++k) {
-      const int i = row0 + k, j = d - i;
-      const int vo = (i < N && j >= 0 && j < M) ? i * (M - 1) * ES : kOob;
-      const int so = d > 0 ? d * ES : 0;
+      const int vo = (unsigned)(d + jb[k]) < (unsigned)M ? vnat[k] : kOob;
       c[k] = bC.ld<T>(vo, so);
       if (SRC == SRC_COST && PEN) q[k] = bQ.ld<T>(vo, so);
     }
@@ -234,49 +243,39 @@ __global__ void __launch_bounds__(1024) udtw_fwd_kernel(UdtwArgs<T> a) {
     for (int u = 0; u < PF; ++u) fetch(d_first + u, rc[u], rq[u]);
   }
 
-  long long off = 0;   // first element of diagonal d (diagonal-major layout)
-  for (int t0 = 0; t0 < steps; t0 += PF) {
+  int soff = 0;  // soff of diagonal d, in elements
+  // Drain the set-up loads here: the compiler derives each in-loop wait on a
+  // ring register from every path into the loop, and the entry path would
+  // otherwise force a near-full vmcnt wait on every trip.
+  __builtin_amdgcn_s_waitcnt(0);
+  for (int t0 = 0; t0 < steps; t0 += kSlots) {
 #pragma unroll
-    for (int u = 0; u < PF; ++u) {
-      const int tau = t0 + u;
-      if (tau >= steps) break;
-      const int d = d_first + tau;
+    for (int u = 0; u < kSlots; ++u) {
+      const int d = d_first + t0 + u;
       T cc[ROWS], cq[ROWS];
 #pragma unroll
       for (int k = 0; k < ROWS; ++k) {
-        cc[k] = rc[u][k];
-        cq[k] = rq[u][k];
+        cc[k] = rc[u % PF][k];
+        cq[k] = rq[u % PF][k];
       }
-      if (SRC != SRC_FEAT1) fetch(d + PF, rc[u], rq[u]);
+      if (SRC != SRC_FEAT1) fetch(d + PF, rc[u % PF], rq[u % PF]);
 
-      // wavefront 0: border record of diagonal d (column d+1 enters next)
-      if (COLS && wave == 0 && lane == 0) {
-        T* r = my_inbox + 4 * (d & (kSlots - 1));
-        r[2] = self_y;
-        r[3] = self_hy;
+      // wavefront 0 stores the border record of diagonal d (column d+1 enters next)
+      if (wave == 0) my_self[(u + 2) & 3] = {INF, (T)0, ey_ring[u], (T)0.5 * evy_ring[u]};
+      if (COLS) {
+        ey_ring[u] = col_y(d + 1 + kSlots);
+        evy_ring[u] = col_vy(d + 1 + kSlots);
       }
-      if (COLS && wave == 0) {
-        const int c = d + 2 < M ? d + 2 : M - 1;
-        self_y = cols[2 * c];
-        self_hy = cols[2 * c + 1];
-      }
-      // the record for diagonal d is what the next step needs
-      const T e0 = rec0, e1v = rec1, e2 = rec2, e3 = rec3;
-      {
-        const T* r = my_inbox + 4 * (d & (kSlots - 1));
-        rec0 = r[0];
-        rec1 = r[1];
-        rec2 = r[2];
-        rec3 = r[3];
-      }
+      const Rec4<T> e = nxt;
+      nxt = inbox[(u + 2) & 3];
 
       nr2 = nr1;
       np2 = np1;
-      nr1 = shift_prev(r1[ROWS - 1], e0);
-      if (PEN) np1 = shift_prev(p1[ROWS - 1], e1v);
-      {
-        const T ny = SRC == SRC_FEAT1 ? shift_prev(yc[ROWS - 1], e2) : (T)0;
-        const T nhy = COLS ? shift_prev(hyc[ROWS - 1], e3) : (T)0.5;
+      nr1 = shift_prev(r1[ROWS - 1], e.x);
+      if (PEN) np1 = shift_prev(p1[ROWS - 1], e.y);
+      if (COLS) {
+        const T ny = SRC == SRC_FEAT1 ? shift_prev(yc[ROWS - 1], e.z) : (T)0;
+        const T nhy = shift_prev(hyc[ROWS - 1], e.w);
 #pragma unroll
         for (int k = ROWS - 1; k > 0; --k) {
           yc[k] = yc[k - 1];
@@ -286,14 +285,12 @@ __global__ void __launch_bounds__(1024) udtw_fwd_kernel(UdtwArgs<T> a) {
         hyc[0] = nhy;
       }
 
-      const bool live = d >= 0 && d < N + M - 1;
-      const int lo = max(0, d - M + 1);
-      const int soff = live ? (int)(off - lo) * ES : 0;
+      const int so = soff * ES;
       T nr[ROWS], np[ROWS];
 #pragma unroll
       for (int k = 0; k < ROWS; ++k) {
-        const int i = row0 + k, j = d - i;
-        const bool valid = (i < N) & ((unsigned)j < (unsigned)M);
+        const int j = d + jb[k];
+        const bool valid = (unsigned)j < (unsigned)M;
         const T up = k ? r1[k - 1] : nr1;
         const T dg = k ? r2[k - 1] : nr2;
         const T lf = r1[k];
@@ -309,8 +306,7 @@ __global__ void __launch_bounds__(1024) udtw_fwd_kernel(UdtwArgs<T> a) {
           } else {
             sq = cc[k] > (T)0 ? cc[k] : (T)0;
           }
-          const T var_raw = hxr[k] + hyc[k];   // (vx + vy) / 2, exactly
-          const T var = var_raw > a.eps ? var_raw : a.eps;
+          const T var = fmax(hxr[k] + hyc[k], a.eps);   // max((vx + vy) / 2, eps)
           ch = sq * (rcp(var) * a.k);
           if (PEN) q = a.beta_ln2 * lg2(var);
         }
@@ -319,7 +315,7 @@ __global__ void __launch_bounds__(1024) udtw_fwd_kernel(UdtwArgs<T> a) {
         const T s = ed + eu + el;
         const T rv = ch + m - lg2(s);
         bool ok = valid;
-        if (BAND) ok = ok && (m < INF) && (fabs((T)(i - j)) <= a.band);
+        if (BAND) ok = ok && (m < INF) && (fabs((T)(2 * (row0 + k) - d)) <= a.band);
         nr[k] = ok ? rv : INF;
         if (PEN) {
           const T pup = k ? p1[k - 1] : np1;
@@ -329,9 +325,9 @@ __global__ void __launch_bounds__(1024) udtw_fwd_kernel(UdtwArgs<T> a) {
         } else {
           np[k] = (T)0;
         }
-        const int vo = valid ? i * ES : kOob;
-        bR.st(nr[k], vo, soff);
-        if (PEN) bP.st(np[k], vo, soff);
+        const int vo = valid ? vst[k] : kOob;
+        bR.st(nr[k], vo, so);
+        if (PEN) bP.st(np[k], vo, so);
       }
 #pragma unroll
       for (int k = 0; k < ROWS; ++k) {
@@ -340,34 +336,24 @@ __global__ void __launch_bounds__(1024) udtw_fwd_kernel(UdtwArgs<T> a) {
         p2[k] = p1[k];
         p1[k] = np[k];
       }
-      if (d == N + M - 2) {
-#pragma unroll
-        for (int k = 0; k < ROWS; ++k) {
-          if (row0 + k == N - 1) {
-            a.out_r[b] = r1[k] < INF ? r1[k] * a.inv_k : INF;
-            a.out_p[b] = PEN ? p1[k] : (T)0;
-          }
-        }
-      }
-      if (live) off += min(N - 1, d) - lo + 1;
-      if (nw > 1) {
-        if (wave + 1 < nw && lane == 63) {
-          T* r = next_inbox + 4 * (d & (kSlots - 1));
-          r[0] = r1[ROWS - 1];
-          r[1] = p1[ROWS - 1];
-          r[2] = yc[ROWS - 1];
-          r[3] = hyc[ROWS - 1];
-        }
-        lag_barrier();
-      }
+      soff += diag_step(d, N, M);
+      my_out[u] = {r1[ROWS - 1], p1[ROWS - 1], yc[ROWS - 1], hyc[ROWS - 1]};
+      lag_barrier();
     }
+  }
+  // cell (N-1, M-1) is the last element of the diagonal-major R / P; the
+  // thread that stored it reads it back
+  if (row0 <= N - 1 && N - 1 < row0 + ROWS) {
+    const int so = (int)(NM - 1) * ES;
+    const T rl = bR.ld<T>(0, so);
+    a.out_r[b] = rl < INF ? rl * a.inv_k : INF;
+    a.out_p[b] = PEN ? bP.ld<T>(0, so) : (T)0;
   }
 }
 
 template <typename T, int ROWS, int SRC, bool PEN, bool BAND, int PF>
-__global__ void __launch_bounds__(1024) udtw_bwd_kernel(UdtwArgs<T> a) {
+__global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwArgs<T> a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  T* sm = reinterpret_cast<T*>(smem_raw);
   constexpr int ES = sizeof(T);
   constexpr bool COLS = SRC != SRC_COST;
   const int N = a.N, M = a.M;
@@ -379,47 +365,63 @@ __global__ void __launch_bounds__(1024) udtw_bwd_kernel(UdtwArgs<T> a) {
   const bool vgrad = COLS && a.dVX != nullptr;
   const int Dn = N + M - 1;
 
-  // Rows are bottom-aligned: row N-1 is the last lane of the last wavefront,
+  // Rows are bottom-aligned: row N-1 is the last row of the last wavefront,
   // where every column enters the backward sweep.
-  const int shift = blockDim.x * ROWS - N;
-  const int row0 = tid * ROWS - shift;
+  const int row0 = tid * ROWS - ((int)blockDim.x * ROWS - N);
 
-  // inbox[w][slot][8]: the row below wavefront w's last row on diagonal e:
-  // E, G (Rbar), H (Pbar), A, y, hy, column sums dy, dvy.
-  T* inbox = sm;
-  T* cols = sm + 8 * kSlots * nw;
-  if (COLS) {
-    for (int t = tid; t < M; t += blockDim.x) {
-      cols[2 * t] = SRC == SRC_FEAT1 ? a.Y[(size_t)b * M + t] : (T)0;
-      cols[2 * t + 1] = (T)0.5 * a.VY[(size_t)b * M + t];
-    }
+  // box[(v + 1) * kSlots + slot]: wavefront v's inbox, the row below its last
+  // row: (E, G, H, A) and (y, hy, dy sum, dvy sum); box[0..kSlots) is
+  // wavefront 0's unread outbox. Then the dump area.
+  Rec8<T>* box = reinterpret_cast<Rec8<T>*>(smem_raw);
+  Rec8<T>* dump = box + (nw + 1) * kSlots;
+  for (int t = tid; t < (nw + 1) * kSlots; t += blockDim.x) {
+    box[t].a = {-INF, (T)0, (T)0, (T)0};
+    box[t].b = {(T)0, (T)0.5, (T)0, (T)0};
   }
-  for (int t = tid; t < kSlots * nw; t += blockDim.x) {
-    inbox[8 * t + 0] = -INF;
-#pragma unroll
-    for (int q = 1; q < 8; ++q) inbox[8 * t + q] = (T)0;
-    inbox[8 * t + 5] = (T)0.5;
-  }
-  __syncthreads();
 
-  Buf bR, bP, bC, bQ, bdC, bdQ, bdY, bdVY;
+  Buf bR, bP, bC, bQ, bdC, bdQ, bY, bVY, bdY, bdVY;
   bR.init(a.R + b * NM, NM);
   if (PEN) bP.init(a.P + b * NM, NM);
   if (SRC != SRC_FEAT1) {
     bC.init(a.C + b * NM, NM);
     bdC.init(a.dC + b * NM, NM);
   }
+  const bool want_dq = SRC == SRC_COST && PEN && a.dQ != nullptr;
   if (SRC == SRC_COST && PEN) {
     bQ.init(a.Q + b * NM, NM);
-    if (a.dQ) bdQ.init(a.dQ + b * NM, NM);
+    if (want_dq) bdQ.init(a.dQ + b * NM, NM);
   }
-  if (SRC == SRC_FEAT1) bdY.init(a.dY + (size_t)b * M, M);
+  if (SRC == SRC_FEAT1) {
+    bY.init(a.Y + (size_t)b * M, M);
+    bdY.init(a.dY + (size_t)b * M, M);
+  }
+  if (COLS) bVY.init(a.VY + (size_t)b * M, M);
   if (vgrad) bdVY.init(a.dVY + (size_t)b * M, M);
-  const bool want_dq = SRC == SRC_COST && PEN && a.dQ != nullptr;
+  auto col_y = [&](int j) -> T {
+    return SRC == SRC_FEAT1 ? bY.ld<T>(0, smin(smax(j, 0), M - 1) * ES) : (T)0;
+  };
+  auto col_vy = [&](int j) -> T {
+    return COLS ? bVY.ld<T>(0, smin(smax(j, 0), M - 1) * ES) : (T)1;
+  };
+
+  const bool last_wave = wave == nw - 1;
+  Rec8<T>* const inbox = box + (wave + 1) * kSlots;
+  Rec8<T>* const outbox = box + wave * kSlots;
+  Rec8<T>* const my_out = lane == 0 ? outbox : dump + lane;
+  Rec8<T>* const my_self = lane == 0 ? inbox : dump + lane;
+  __syncthreads();
+  // record used on step 0 by the last wavefront: virtual row N on diagonal
+  // Dn, with column M-1 entering row N-1
+  if (last_wave && COLS) {
+    const T yl = col_y(M - 1), hyl = (T)0.5 * col_vy(M - 1);
+    if (lane == 0) inbox[1].b = {yl, hyl, (T)0, (T)0};
+  }
+  __syncthreads();
 
   T xr[ROWS], hxr[ROWS], dxr[ROWS], dvr[ROWS];
   T e1[ROWS], e2[ROWS], g1[ROWS], g2[ROWS], h1[ROWS], h2[ROWS], a1[ROWS], a2[ROWS];
   T yc[ROWS], hyc[ROWS], cy[ROWS], cvy[ROWS];
+  int vst[ROWS], vnat[ROWS], jb[ROWS], vrow0[ROWS];
 #pragma unroll
   for (int k = 0; k < ROWS; ++k) {
     const int i = row0 + k;
@@ -431,112 +433,103 @@ __global__ void __launch_bounds__(1024) udtw_bwd_kernel(UdtwArgs<T> a) {
     g1[k] = g2[k] = h1[k] = h2[k] = a1[k] = a2[k] = (T)0;
     yc[k] = cy[k] = cvy[k] = (T)0;
     hyc[k] = (T)0.5;
+    vst[k] = in ? i * ES : 0;
+    vnat[k] = in ? i * (M - 1) * ES : 0;
+    jb[k] = in ? -i : INT_MIN / 2;
+    vrow0[k] = i == 0 ? 0 : kOob;   // the row that stores finished columns
   }
-  // the row below this thread's last row on diagonals d+1 / d+2
+  // Row below the last row on the two previous diagonals. The virtual cell
+  // (N, M) on diagonal Dn+1 is given E = Rh(N-1, M-1), A = P(N-1, M-1) and the
+  // incoming gradients, so the recursion yields grad_dist / grad_pen at
+  // (N-1, M-1) without a special case.
   T ne1 = -INF, ne2 = -INF, ng1 = 0, ng2 = 0, nh1 = 0, nh2 = 0, na1 = 0, na2 = 0;
-  const T gr = a.gr[b];
-  const T gp = PEN ? a.gp[b] : (T)0;
+  if (last_wave && lane == 63) {
+    const int so = (int)(NM - 1) * ES;
+    ne1 = bR.ld<T>(0, so);
+    ng1 = a.gr[b];
+    if (PEN) {
+      nh1 = a.gp[b];
+      na1 = bP.ld<T>(0, so);
+    }
+  }
 
   const int d_first = Dn - 1 + kLag * (nw - 1 - wave);
-  const int steps = Dn + kLag * (nw - 1);
-  T* my_inbox = inbox + 8 * kSlots * wave;
-  T* prev_inbox = inbox + 8 * kSlots * (wave - 1);
-  const bool last_wave = wave == nw - 1;
-  // the virtual row N on diagonal Dn: column M-1 enters row N-1 on diagonal Dn-1
-  if (COLS && last_wave && lane == 0) {
-    T* r = my_inbox + 8 * (Dn & (kSlots - 1));
-    r[4] = cols[2 * (M - 1)];
-    r[5] = cols[2 * (M - 1) + 1];
-  }
-  __syncthreads();
-  T rec[8];
-  {
-    const T* r = my_inbox + 8 * ((d_first + 1) & (kSlots - 1));
+  const int steps = (Dn + kLag * (nw - 1) + kSlots - 1) / kSlots * kSlots;
+  Rec8<T> nx = inbox[1];
+  // column entering row N-1 on the diagonal after step u's, loaded kSlots
+  // steps ahead by every wavefront (the last one uses them)
+  T ey_ring[kSlots], evy_ring[kSlots];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) rec[q] = r[q];
-  }
-  // column the last wavefront stores for the virtual row N on diagonal d
-  // (column d - N), one step ahead
-  T self_y = (T)0, self_hy = (T)0.5;
-  if (COLS && last_wave) {
-    const int c = min(max(Dn - 1 - N, 0), M - 1);
-    self_y = cols[2 * c];
-    self_hy = cols[2 * c + 1];
+  for (int u = 0; u < kSlots; ++u) {
+    ey_ring[u] = col_y(d_first - u - N);
+    evy_ring[u] = col_vy(d_first - u - N);
   }
 
   T rr[PF][ROWS], rp[PF][ROWS], rc[PF][ROWS], rq[PF][ROWS];
+  int sfetch = (int)(NM - N);  // soff of the next diagonal to fetch (min(d, Dn-1))
   auto fetch = [&](int d, T* r, T* p, T* c, T* q) {
-    const bool live = d >= 0 && d < Dn;
-    const int lo = max(0, d - M + 1);
-    const int soff_d = live ? (int)(diag_offset(d, N, M) - lo) * ES : 0;
+    const int so_d = sfetch * ES;
+    const int so_n = smax(d, 0) * ES;
 #pragma unroll
     for (int k = 0; k < ROWS; ++k) {
-      const int i = row0 + k, j = d - i;
-      const bool v = live && i >= 0 && i < N && j >= 0 && j < M;
-      r[k] = bR.ld<T>(v ? i * ES : kOob, soff_d);
-      if (PEN) p[k] = bP.ld<T>(v ? i * ES : kOob, soff_d);
+      const bool v = (unsigned)(d + jb[k]) < (unsigned)M;
+      const int vd = v ? vst[k] : kOob;
+      r[k] = bR.ld<T>(vd, so_d);
+      if (PEN) p[k] = bP.ld<T>(vd, so_d);
       if (SRC != SRC_FEAT1) {
-        const int vn = v ? i * (M - 1) * ES : kOob;
-        const int so = live ? d * ES : 0;
-        c[k] = bC.ld<T>(vn, so);
-        if (SRC == SRC_COST && PEN) q[k] = bQ.ld<T>(vn, so);
+        const int vn = v ? vnat[k] : kOob;
+        c[k] = bC.ld<T>(vn, so_n);
+        if (SRC == SRC_COST && PEN) q[k] = bQ.ld<T>(vn, so_n);
       }
     }
+    sfetch -= diag_step(d - 1, N, M);
   };
 #pragma unroll
   for (int u = 0; u < PF; ++u) fetch(d_first - u, rr[u], rp[u], rc[u], rq[u]);
 
-  for (int t0 = 0; t0 < steps; t0 += PF) {
+  __builtin_amdgcn_s_waitcnt(0);   // drain the set-up loads (as in the forward)
+  for (int t0 = 0; t0 < steps; t0 += kSlots) {
 #pragma unroll
-    for (int u = 0; u < PF; ++u) {
-      const int tau = t0 + u;
-      if (tau >= steps) break;
-      const int d = d_first - tau;
+    for (int u = 0; u < kSlots; ++u) {
+      const int d = d_first - t0 - u;
       T cr[ROWS], cp[ROWS], cc[ROWS], cq[ROWS];
 #pragma unroll
       for (int k = 0; k < ROWS; ++k) {
-        cr[k] = rr[u][k];
-        cp[k] = rp[u][k];
-        cc[k] = rc[u][k];
-        cq[k] = rq[u][k];
+        cr[k] = rr[u % PF][k];
+        cp[k] = rp[u % PF][k];
+        cc[k] = rc[u % PF][k];
+        cq[k] = rq[u % PF][k];
       }
-      fetch(d - PF, rr[u], rp[u], rc[u], rq[u]);
+      fetch(d - PF, rr[u % PF], rp[u % PF], rc[u % PF], rq[u % PF]);
 
-      // last wavefront: virtual row N on diagonal d (column d - N enters row N-1 on d-1)
-      if (COLS && last_wave && lane == 0) {
-        T* r = my_inbox + 8 * (d & (kSlots - 1));
-        r[4] = self_y;
-        r[5] = self_hy;
+      // the last wavefront stores the virtual row N of diagonal d
+      if (COLS) {
+        if (last_wave) my_self[(u + 2) & 3].b = {ey_ring[u], (T)0.5 * evy_ring[u], (T)0, (T)0};
+        ey_ring[u] = col_y(d - kSlots - N);
+        evy_ring[u] = col_vy(d - kSlots - N);
       }
-      if (COLS && last_wave) {
-        const int c = min(max(d - 1 - N, 0), M - 1);
-        self_y = cols[2 * c];
-        self_hy = cols[2 * c + 1];
-      }
-      T er[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) er[q] = rec[q];
-      {
-        const T* r = my_inbox + 8 * (d & (kSlots - 1));
-#pragma unroll
-        for (int q = 0; q < 8; ++q) rec[q] = r[q];
+      const Rec8<T> ex = nx;
+      if (COLS) {
+        nx = inbox[(u + 2) & 3];
+      } else {
+        nx.a = inbox[(u + 2) & 3].a;
       }
 
       ne2 = ne1;
       ng2 = ng1;
       nh2 = nh1;
       na2 = na1;
-      ne1 = shift_next(e1[0], er[0]);
-      ng1 = shift_next(g1[0], er[1]);
+      ne1 = shift_next(e1[0], ex.a.x);
+      ng1 = shift_next(g1[0], ex.a.y);
       if (PEN) {
-        nh1 = shift_next(h1[0], er[2]);
-        na1 = shift_next(a1[0], er[3]);
+        nh1 = shift_next(h1[0], ex.a.z);
+        na1 = shift_next(a1[0], ex.a.w);
       }
       if (COLS) {
-        const T fy = SRC == SRC_FEAT1 ? shift_next(yc[0], er[4]) : (T)0;
-        const T fhy = shift_next(hyc[0], er[5]);
-        const T fcy = SRC == SRC_FEAT1 ? shift_next(cy[0], er[6]) : (T)0;
-        const T fcvy = vgrad ? shift_next(cvy[0], er[7]) : (T)0;
+        const T fy = SRC == SRC_FEAT1 ? shift_next(yc[0], ex.b.x) : (T)0;
+        const T fhy = shift_next(hyc[0], ex.b.y);
+        const T fcy = SRC == SRC_FEAT1 ? shift_next(cy[0], ex.b.z) : (T)0;
+        const T fcvy = vgrad ? shift_next(cvy[0], ex.b.w) : (T)0;
 #pragma unroll
         for (int k = 0; k + 1 < ROWS; ++k) {
           yc[k] = yc[k + 1];
@@ -550,12 +543,11 @@ __global__ void __launch_bounds__(1024) udtw_bwd_kernel(UdtwArgs<T> a) {
         cvy[ROWS - 1] = fcvy;
       }
 
-      const bool live = d >= 0 && d < Dn;
+      const int so_n = smax(d, 0) * ES;
       T xe[ROWS], xg[ROWS], xh[ROWS], xa[ROWS];
 #pragma unroll
       for (int k = 0; k < ROWS; ++k) {
-        const int i = row0 + k, j = d - i;
-        const bool valid = (i >= 0) & (i < N) & ((unsigned)j < (unsigned)M);
+        const bool valid = (unsigned)(d + jb[k]) < (unsigned)M;
         const T rk = valid ? cr[k] : INF;
         const T pk = cp[k];
         T ch, q = (T)0, c = (T)0, rv = (T)1, sq_raw = (T)0, var_raw = (T)1;
@@ -571,7 +563,7 @@ __global__ void __launch_bounds__(1024) udtw_bwd_kernel(UdtwArgs<T> a) {
           }
           const T sq = sq_raw > (T)0 ? sq_raw : (T)0;
           var_raw = hxr[k] + hyc[k];
-          const T var = var_raw > a.eps ? var_raw : a.eps;
+          const T var = fmax(var_raw, a.eps);
           rv = rcp(var);
           c = sq * rv;
           ch = c * a.k;
@@ -582,46 +574,35 @@ __global__ void __launch_bounds__(1024) udtw_bwd_kernel(UdtwArgs<T> a) {
         const T gdn = (k + 1 < ROWS) ? g1[k + 1] : ng1;
         const T edg = (k + 1 < ROWS) ? e2[k + 1] : ne2;
         const T gdg = (k + 1 < ROWS) ? g2[k + 1] : ng2;
-        T g, h = (T)0;
-        if (d == Dn - 1) {
-          g = gr;
-          h = gp;
-        } else {
-          const T wdn = ex2(edn - rk), wrt = ex2(e1[k] - rk), wdg = ex2(edg - rk);
-          g = wdn * gdn + wrt * g1[k] + wdg * gdg;
-          if (PEN) {
-            const T hdn = (k + 1 < ROWS) ? h1[k + 1] : nh1;
-            const T adn = (k + 1 < ROWS) ? a1[k + 1] : na1;
-            const T hdg = (k + 1 < ROWS) ? h2[k + 1] : nh2;
-            const T adg = (k + 1 < ROWS) ? a2[k + 1] : na2;
-            const T wh_dn = wdn * hdn, wh_rt = wrt * h1[k], wh_dg = wdg * hdg;
-            g -= (wh_dn * (pk - adn) + wh_rt * (pk - a1[k]) + wh_dg * (pk - adg)) * a.inv_gamma;
-            h = wh_dn + wh_rt + wh_dg;
-          }
-          if (BAND) {
-            if (!(rk < INF)) {
-              g = (T)0;
-              h = (T)0;
-            }
-          }
+        const T wdn = ex2(edn - rk), wrt = ex2(e1[k] - rk), wdg = ex2(edg - rk);
+        T g = wdn * gdn + wrt * g1[k] + wdg * gdg;
+        T h = (T)0;
+        if (PEN) {
+          const T hdn = (k + 1 < ROWS) ? h1[k + 1] : nh1;
+          const T adn = (k + 1 < ROWS) ? a1[k + 1] : na1;
+          const T hdg = (k + 1 < ROWS) ? h2[k + 1] : nh2;
+          const T adg = (k + 1 < ROWS) ? a2[k + 1] : na2;
+          const T wh_dn = wdn * hdn, wh_rt = wrt * h1[k], wh_dg = wdg * hdg;
+          g -= (wh_dn * (pk - adn) + wh_rt * (pk - a1[k]) + wh_dg * (pk - adg)) * a.inv_gamma;
+          h = wh_dn + wh_rt + wh_dg;
         }
-        if (!valid) {
-          g = (T)0;
-          h = (T)0;
-        }
-        xe[k] = (valid && (!BAND || rk < INF)) ? rk - ch : -INF;
+        // outside the grid, and (band) at unreachable cells, nothing flows
+        bool live = valid;
+        if (BAND) live = live && rk < INF;
+        g = live ? g : (T)0;
+        h = live ? h : (T)0;
+        xe[k] = live ? rk - ch : -INF;
         xg[k] = g;
         xh[k] = h;
         xa[k] = valid ? pk - q : (T)0;
 
-        const int vn = valid ? i * (M - 1) * ES : kOob;
-        const int so = live ? d * ES : 0;
+        const int vn = valid ? vnat[k] : kOob;
         if (SRC == SRC_COST) {
-          bdC.st(g, vn, so);
-          if (want_dq) bdQ.st(h, vn, so);
+          bdC.st(g, vn, so_n);
+          if (want_dq) bdQ.st(h, vn, so_n);
         } else {
           const T dsq = sq_raw > (T)0 ? g * rv : (T)0;
-          if (SRC == SRC_SQ) bdC.st(dsq, vn, so);
+          if (SRC == SRC_SQ) bdC.st(dsq, vn, so_n);
           if (SRC == SRC_FEAT1) {
             const T df = valid ? (T)2 * dsq * (xr[k] - yc[k]) : (T)0;
             dxr[k] += df;
@@ -634,9 +615,9 @@ __global__ void __launch_bounds__(1024) udtw_bwd_kernel(UdtwArgs<T> a) {
             cvy[k] += dvar;
           }
           // column d leaves the sweep at row 0: store its sums
-          const int vc = (row0 + k == 0 && d >= 0 && d < M) ? 0 : kOob;
-          if (SRC == SRC_FEAT1) bdY.st(cy[k], vc, so);
-          if (vgrad) bdVY.st(cvy[k], vc, so);
+          const int vc = ((unsigned)d < (unsigned)M) ? vrow0[k] : kOob;
+          if (SRC == SRC_FEAT1) bdY.st(cy[k], vc, so_n);
+          if (vgrad) bdVY.st(cvy[k], vc, so_n);
         }
       }
 #pragma unroll
@@ -650,20 +631,12 @@ __global__ void __launch_bounds__(1024) udtw_bwd_kernel(UdtwArgs<T> a) {
         a2[k] = a1[k];
         a1[k] = xa[k];
       }
-      if (nw > 1) {
-        if (wave > 0 && lane == 0) {
-          T* r = prev_inbox + 8 * (d & (kSlots - 1));
-          r[0] = e1[0];
-          r[1] = g1[0];
-          r[2] = h1[0];
-          r[3] = a1[0];
-          r[4] = yc[0];
-          r[5] = hyc[0];
-          r[6] = cy[0];
-          r[7] = cvy[0];
-        }
-        lag_barrier();
+      if (COLS) {
+        my_out[u] = {{e1[0], g1[0], h1[0], a1[0]}, {yc[0], hyc[0], cy[0], cvy[0]}};
+      } else {
+        my_out[u].a = {e1[0], g1[0], h1[0], a1[0]};
       }
+      lag_barrier();
     }
   }
 #pragma unroll
@@ -688,23 +661,26 @@ struct Shape {
 static Shape pick_shape(int N) {
   int rows = 1;
   while (rows < 16 && (N + rows - 1) / rows > 256) rows *= 2;
-  // tuning override: TORCHWARP_UDTW_ROWS = 1, 2, 4, 8 or 16 rows per thread
+  // tuning override: TORCHWARP_UDTW_ROWS = 1, 2, 4, 8 or 16 rows per thread,
+  // taken when the kernel's thread limit for that row count allows it
   static const int forced = [] {
     const char* e = getenv("TORCHWARP_UDTW_ROWS");
     return e ? atoi(e) : 0;
   }();
-  if (forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16) rows = forced;
+  if ((forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16) &&
+      (N + forced - 1) / forced <= (forced >= 16 ? 1024 : 256))
+    rows = forced;
   int threads = (N + rows - 1) / rows;
   if (threads > 1024) return {0, 0};
   threads = ((threads + 63) / 64) * 64;
   return {rows, threads};
 }
 
-// LDS of one workgroup: mailbox rings plus the (y, hy) table of the columns.
-template <typename T, int SRC>
-static size_t udtw_lds(bool backward, int nw, int M) {
-  const size_t box = (backward ? 8 : 4) * (size_t)kSlots * nw;
-  return (box + (SRC != SRC_COST ? 2 * (size_t)M : 0)) * sizeof(T);
+// LDS of one workgroup: the mailbox rings and the dump area of the
+// mailbox stores (records of 4 values forward, 8 backward).
+template <typename T>
+static size_t udtw_lds(bool backward, int nw) {
+  return (size_t)((nw + 1) * kSlots + kDump) * (backward ? 8 : 4) * sizeof(T);
 }
 
 // Prefetch depth (diagonals) of the register ring for a row count.
@@ -726,9 +702,9 @@ static int launch_udtw(bool backward, const UdtwArgs<T>& a, int B, hipStream_t s
     return fail(TW_ESIZE, "%s: one pair's N*M matrix must stay below 2 GiB", what);
   }
   const int nw = sh.threads / 64;
-  const size_t lds = udtw_lds<T, SRC>(backward, nw, a.M);
+  const size_t lds = udtw_lds<T>(backward, nw);
   if (lds > (size_t)max_lds_bytes()) {
-    return fail(TW_ESIZE, "%s: %zu bytes of LDS needed (M = %d), %d available", what, lds, a.M,
+    return fail(TW_ESIZE, "%s: %zu bytes of LDS needed, %d available", what, lds,
                 max_lds_bytes());
   }
   dim3 grid(B), block(sh.threads);
