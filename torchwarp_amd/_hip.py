@@ -87,26 +87,42 @@ def available():
     return _load() is not None and torch.cuda.is_available()
 
 
-def _arg(x):
-    if x is None:
-        return None
-    if isinstance(x, torch.Tensor):
-        return ctypes.c_void_p(x.data_ptr()) if x.numel() else None
-    return x
+_FNS = {}
+
+
+def _entry(base, dtype):
+    fn = _FNS.get((base, dtype))
+    if fn is None:
+        suffix = {torch.float32: "_f32", torch.float64: "_f64"}.get(dtype)
+        if suffix is None:
+            raise TypeError("torchwarp_amd computes in float32 or float64, got {}".format(dtype))
+        fn = _FNS[(base, dtype)] = getattr(library(), base + suffix)
+    return fn
 
 
 def call(base, dtype, *args):
-    """Call ``base``_f32/_f64 on the current stream of the first tensor's device."""
-    lib = library()
-    suffix = {torch.float32: "_f32", torch.float64: "_f64"}.get(dtype)
-    if suffix is None:
-        raise TypeError("torchwarp_amd computes in float32 or float64, got {}".format(dtype))
-    dev = next(a.device for a in args if isinstance(a, torch.Tensor))
-    with torch.cuda.device(dev):
-        stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
-        rc = getattr(lib, base + suffix)(*[_arg(a) for a in args], stream)
+    """Call ``base``_f32/_f64 on the current stream of the first tensor's device.
+
+    Kernels launch on the HIP device that is current during the call, so the
+    tensors' device is made current when it is not already.
+    """
+    fn = _entry(base, dtype)
+    dev = None
+    cargs = []
+    for a in args:
+        if isinstance(a, torch.Tensor):
+            if dev is None:
+                dev = a.device.index
+            cargs.append(a.data_ptr() if a.numel() else None)
+        else:
+            cargs.append(a)
+    if torch._C._cuda_getDevice() == dev:
+        rc = fn(*cargs, torch._C._cuda_getCurrentRawStream(dev))
+    else:
+        with torch.cuda.device(dev):
+            rc = fn(*cargs, torch._C._cuda_getCurrentRawStream(dev))
     if rc != 0:
-        raise RuntimeError("torchwarp_amd: " + lib.tw_last_error().decode())
+        raise RuntimeError("torchwarp_amd: " + _lib.tw_last_error().decode())
 
 
 def udtw_workspace_elems(B, N, M, D):

@@ -61,9 +61,53 @@ def without_jvp(cls):
     return type(cls.__name__ + "Compiled", (torch.autograd.Function,), ns)
 
 
+_PLAIN = (Tensor, torch.nn.Parameter)
+
+
+def plain_eager(args):
+    """True for a call that no tracing, transform, mode or autocast can observe:
+    not compiling, no functorch transform, no dispatch / torch-function mode,
+    autocast off, and only plain tensors among the arguments."""
+    if torch.compiler.is_compiling() or torch._C._are_functorch_transforms_active():
+        return False
+    if torch._C._len_torch_dispatch_stack() or torch._C._is_torch_function_mode_enabled():
+        return False
+    if torch.is_autocast_enabled("cuda") or torch.is_autocast_enabled("cpu"):
+        return False
+    return all(type(a) in _PLAIN for a in args if isinstance(a, Tensor))
+
+
+def direct(op):
+    """Call a custom op; in plain eager mode call its implementation directly.
+
+    The op (fake kernel, vmap rule, autocast) serves every traced or
+    transformed call; a plain eager call gets the same implementation without
+    the dispatcher round trip.
+    """
+    impl = op._init_fn
+
+    def call(*args):
+        if plain_eager(args):
+            return impl(*args)
+        return op(*args)
+    return call
+
+
 def pick(cls, compiled):
+    """``cls.apply``, with the compiled twin while torch.compile traces.
+
+    With all arguments given positionally and no functorch transform active,
+    ``Function.apply`` only adds a per-call ``inspect.signature`` binding of
+    default arguments before the C++ apply; the plain path calls the C++
+    apply directly (dead functorch wrappers are still unwrapped).
+    """
+    base_apply = super(torch.autograd.Function, cls).apply
+    unwrap = torch._functorch.utils.unwrap_if_dead
+
     def apply(*args):
         if torch.compiler.is_compiling():
             return compiled.apply(*args)
-        return cls.apply(*args)
+        if torch._C._are_functorch_transforms_active():
+            return cls.apply(*args)
+        return base_apply(*(unwrap(a) if isinstance(a, Tensor) else a for a in args))
     return apply

@@ -28,8 +28,8 @@ import torch
 from torch import Tensor
 
 from .. import _hip
-from .._opsutil import (jvp_of, pick, register_autocast, register_vmap, vjp_of, without_jvp,
-                        zeros_if_none)
+from .._opsutil import (direct, jvp_of, pick, register_autocast, register_vmap, vjp_of,
+                        without_jvp, zeros_if_none)
 from . import _autograd
 
 METRIC_CODES = {"sqeuclidean": _hip.METRIC_SQEUC, "euclidean": _hip.METRIC_EUC}
@@ -87,7 +87,7 @@ class Pair(torch.autograd.Function):
 
     @staticmethod
     def forward(A, Bm, metric, backend):
-        return pair(A, Bm, metric, backend)
+        return _pair_direct(A, Bm, metric, backend)
 
     @staticmethod
     def setup_context(ctx, inputs, output):
@@ -116,7 +116,7 @@ class PairBackward(torch.autograd.Function):
 
     @staticmethod
     def forward(A, Bm, cost, g, metric, backend):
-        return pair_backward(A, Bm, cost, g, metric, backend)
+        return _pair_backward_direct(A, Bm, cost, g, metric, backend)
 
     @staticmethod
     def setup_context(ctx, inputs, output):
@@ -201,7 +201,7 @@ class DP(torch.autograd.Function):
 
     @staticmethod
     def forward(cost, s1, s2, gamma, backend, natural_R):
-        return dp(cost, s1, s2, gamma, backend)
+        return _dp_direct(cost, s1, s2, gamma, backend)
 
     @staticmethod
     def setup_context(ctx, inputs, output):
@@ -245,7 +245,7 @@ class DPBackward(torch.autograd.Function):
 
     @staticmethod
     def forward(cost, R, g_out, g_R, s1, s2, gamma, backend):
-        return dp_backward(cost, R, g_out, g_R, s1, s2, gamma, backend)
+        return _dp_backward_direct(cost, R, g_out, g_R, s1, s2, gamma, backend)
 
     @staticmethod
     def setup_context(ctx, inputs, output):
@@ -343,7 +343,7 @@ class Features(torch.autograd.Function):
 
     @staticmethod
     def forward(query, support, s1, s2, gamma, metric, backend, natural_R):
-        return features(query, support, s1, s2, gamma, metric, backend)
+        return _features_direct(query, support, s1, s2, gamma, metric, backend)
 
     @staticmethod
     def setup_context(ctx, inputs, output):
@@ -384,7 +384,7 @@ class FeaturesBackward(torch.autograd.Function):
 
     @staticmethod
     def forward(query, support, cost, R, g_out, g_R, s1, s2, gamma, metric, backend):
-        return features_backward(query, support, cost, R, g_out, g_R, s1, s2, gamma, metric,
+        return _features_backward_direct(query, support, cost, R, g_out, g_R, s1, s2, gamma, metric,
                                  backend)
 
     @staticmethod
@@ -456,6 +456,14 @@ register_vmap(fvm, 1)
 register_vmap(fvm_backward, 4)
 register_autocast(fvm)
 register_autocast(fvm_backward)
+_pair_direct = direct(pair)
+_pair_backward_direct = direct(pair_backward)
+_dp_direct = direct(dp)
+_dp_backward_direct = direct(dp_backward)
+_features_direct = direct(features)
+_features_backward_direct = direct(features_backward)
+_fvm_direct = direct(fvm)
+_fvm_backward_direct = direct(fvm_backward)
 
 
 class FVM(torch.autograd.Function):
@@ -463,7 +471,7 @@ class FVM(torch.autograd.Function):
 
     @staticmethod
     def forward(cost, gamma, backend):
-        return fvm(cost, gamma, backend)
+        return _fvm_direct(cost, gamma, backend)
 
     @staticmethod
     def setup_context(ctx, inputs, output):
@@ -495,7 +503,7 @@ class FVMBackward(torch.autograd.Function):
 
     @staticmethod
     def forward(cost, temporal, R, g_out, gamma, backend):
-        return fvm_backward(cost, temporal, R, g_out, gamma, backend)
+        return _fvm_backward_direct(cost, temporal, R, g_out, gamma, backend)
 
     @staticmethod
     def setup_context(ctx, inputs, output):

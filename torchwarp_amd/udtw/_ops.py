@@ -25,8 +25,8 @@ import torch
 from torch import Tensor
 
 from .. import _hip
-from .._opsutil import (jvp_of, pick, register_autocast, register_vmap, vjp_of, without_jvp,
-                        zeros_if_none)
+from .._opsutil import (direct, jvp_of, pick, register_autocast, register_vmap, vjp_of,
+                        without_jvp, zeros_if_none)
 from . import _autograd
 
 # ---------------------------------------------------- DP on given matrices
@@ -144,6 +144,10 @@ register_vmap(fused, 4)
 register_vmap(fused_backward, 8)
 register_autocast(fused)
 register_autocast(fused_backward)
+_dp_direct = direct(dp)
+_dp_backward_direct = direct(dp_backward)
+_fused_direct = direct(fused)
+_fused_backward_direct = direct(fused_backward)
 
 
 # ------------------------------------------------------ autograd Functions
@@ -167,7 +171,7 @@ class DP(torch.autograd.Function):
 
     @staticmethod
     def forward(cost, penalty, gamma, bandwidth, backend):
-        return dp(cost, penalty, gamma, bandwidth, backend)
+        return _dp_direct(cost, penalty, gamma, bandwidth, backend)
 
     @staticmethod
     def setup_context(ctx, inputs, output):
@@ -206,7 +210,7 @@ class DPBackward(torch.autograd.Function):
 
     @staticmethod
     def forward(cost, penalty, R, P, g_r, g_p, gamma, bandwidth, backend):
-        return dp_backward(cost, penalty, R, P, g_r, g_p, gamma, bandwidth, backend)
+        return _dp_backward_direct(cost, penalty, R, P, g_r, g_p, gamma, bandwidth, backend)
 
     @staticmethod
     def setup_context(ctx, inputs, output):
@@ -249,7 +253,7 @@ class Fused(torch.autograd.Function):
 
     @staticmethod
     def forward(X, Y, vx, vy, gamma, beta, eps, bandwidth, backend):
-        return fused(X, Y, vx, vy, gamma, beta, eps, bandwidth, backend)
+        return _fused_direct(X, Y, vx, vy, gamma, beta, eps, bandwidth, backend)
 
     @staticmethod
     def setup_context(ctx, inputs, output):
@@ -291,7 +295,8 @@ class FusedBackward(torch.autograd.Function):
 
     @staticmethod
     def forward(X, Y, vx, vy, R, P, g_r, g_p, gamma, beta, eps, bandwidth, backend):
-        return fused_backward(X, Y, vx, vy, R, P, g_r, g_p, gamma, beta, eps, bandwidth, backend)
+        return _fused_backward_direct(X, Y, vx, vy, R, P, g_r, g_p, gamma, beta, eps, bandwidth,
+                                      backend)
 
     @staticmethod
     def setup_context(ctx, inputs, output):
