@@ -1,6 +1,7 @@
 """Benchmark of the torchwarp alignment hot path on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--config cfg2] [--all] [--no-cpu]
+    python bench.py --copy-probe      # HBM counter calibration: 5 copies of 256 MiB
 
 A "step" is one forward + loss + backward of the configured alignment loss on
 synthetic inputs already resident in HBM (inputs are
@@ -24,6 +25,8 @@ import time
 import torch
 
 HBM_PEAK_GBS = 8000.0
+METRIC = ("DP cells/sec & pairs/sec fwd+bwd (uDTW B=256 N=M=140; JEANIE K=25), "
+          "% HBM roofline")
 LAST_TIMES = {}   # label -> mean ms of every kernel timed by the last _hip_call_times
 CONFIGS = ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5a", "cfg5b")
 
@@ -244,7 +247,7 @@ def cpu_baseline(name, budget_s=10.0):
         el = time.perf_counter() - t0
         if el >= budget_s or n >= 50:
             break
-    return {"value": w["cells"] * n / el, "unit": "DP cells/s", "cores": cores,
+    return {"value": w["cells"] * n / el, "unit": "cells/s", "cores": cores,
             "kind": "port",
             "sample": "{}: full batch fwd+bwd x{} in {:.1f} s, fp32, oracle/ on {} threads"
                       .format(name, n, el, cores)}
@@ -276,7 +279,18 @@ def main():
     ap.add_argument("--config", default="cfg2", choices=CONFIGS)
     ap.add_argument("--all", action="store_true", help="also time every config (stderr)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run 5 device copies of 256 MiB (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
+    if args.copy_probe:
+        src = torch.ones(64 << 20, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes_read": src.numel() * 4,
+                          "copy_probe_bytes_written": dst.numel() * 4, "launches": 5}))
+        return
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; pairs are independent, so N GPUs would "
               "each run this same per-GPU workload on B/N pairs (no collective inside the op). "
@@ -294,7 +308,7 @@ def main():
                 "frac": round(gbs / HBM_PEAK_GBS, 5), "traffic": _traffic(label, name),
                 "kernel": label, "kernel_ms": round(kms, 5), "algorithmic_bytes": nbytes}
     line = {
-        "metric": "DP cells/s fwd+bwd (uDTW B=256 N=M=140)",
+        "metric": METRIC,
         "value": round(cells_s, 1),
         "unit": "cells/s",
         "n_gpus": 1,
@@ -304,7 +318,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": name, "pairs_per_s": round(pairs_s, 1), "cells": work(name)["cells"],
                    "pairs": work(name)["pairs"]},

@@ -103,10 +103,13 @@ def test_cfg3_udtw_long(dtype):
         assert errs[0] < F32_VALUE_TOL
         # gamma = 0.1 at N = 1024: R reaches ~1.4e5 (scaled), so float32 holds
         # it to ~1e-2 absolute; the penalty (a softmax expectation) keeps
-        # ~4e-5 and the gradients ~3e-2 in any float32 implementation (the
-        # reference documents 1e-2 .. 3e-2 for its own kernel at this length)
+        # ~4e-5 and the gradients a few 1e-2 in any float32 implementation,
+        # and they move with the rounding of the cost itself (summation
+        # order of |x|^2 + |y|^2 - 2 x.y). The reference documents, at
+        # N = 1000 and gamma = 0.1, 1e-2 for its float32 kernel and 0.6 for
+        # its float32 PyTorch backend (docs/limitations.md:31-42).
         assert errs[1] < 1e-4
-        assert max(errs[2:]) < 5e-2
+        assert max(errs[2:]) < 1e-1
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])

@@ -11,8 +11,11 @@
 // (cost > 0), else 0, then
 //   dA = 2 (rowsum(dS) A - dS Bm),  dB = 2 (colsum(dS) Bm - dS^T A).
 //
-// fp32 with D a multiple of 4 runs on the matrix cores (v_mfma_f32_16x16x4f32,
-// one 16x16 output tile per wavefront); every other case on plain FMA.
+// Forward: fp32 with D a multiple of 4 runs on the matrix cores
+// (v_mfma_f32_16x16x4f32, a 16 x 16*TN output strip per wavefront); fp64 and
+// other D on a plain FMA kernel. Backward: when a pair's dS fits in LDS and
+// C <= 64, one fused kernel per pair streams A and B once (threads along D,
+// dB partial sums in registers); otherwise two FMA kernels (dA, dB).
 
 #include "tw_capi.hpp"
 #include "tw_common.hpp"
@@ -100,6 +103,162 @@ __global__ void __launch_bounds__(256) pair_bwd_b_fma(const T* __restrict__ A,
   dB[((size_t)p * C + c) * D + d] = (T)2 * (cs * Bm[((size_t)p * C + c) * D + d] - acc);
 }
 
+
+// ----------------------------------------------------------- MFMA forward
+//
+// v_mfma_f32_16x16x4f32 operand layout (wave64): A (16x4) lane l holds
+// A[l % 16][l / 16]; B (4x16) lane l holds B[l / 16][l % 16]; the 16x16
+// result gives lane l, register i the element (4 (l / 16) + i, l % 16).
+// The reduction index may be permuted consistently in both operands: lane l
+// loads the float4 A[row][k0 + 4 g .. +3] (g = l / 16) and its B row
+// likewise, and MFMA j of a 16-wide k block consumes component j, i.e.
+// k = k0 + 4 g + j. Each row then contributes one contiguous 64-byte segment
+// per k block.
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 ld4(const Buf& b, int v, int s) {
+  const unsigned int __attribute__((ext_vector_type(4))) w =
+      __builtin_amdgcn_raw_buffer_load_b128(b.r, v, s, 0);
+  return f32x4{__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z),
+               __uint_as_float(w.w)};
+}
+
+template <int MET, int TN>
+__global__ void __launch_bounds__(256) pair_fwd_mfma(const float* __restrict__ A,
+                                                     const float* __restrict__ Bm,
+                                                     float* __restrict__ out, int R, int C,
+                                                     int D) {
+  const int p = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int strip = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int RT = (R + 15) >> 4, CT = (C + 16 * TN - 1) / (16 * TN);
+  if (strip >= RT * CT) return;   // no barrier below: a finished wave may leave
+  const int r0 = (strip % RT) * 16, c0 = (strip / RT) * 16 * TN;
+  const int g = lane >> 4, li = lane & 15;
+
+  Buf ba, bb;
+  ba.init(A + (size_t)p * R * D, (long long)R * D);
+  bb.init(Bm + (size_t)p * C * D, (long long)C * D);
+  const int ra = r0 + li;
+  const int va = ra < R ? (ra * D + 4 * g) * 4 : kOob;
+  int vb[TN];
+#pragma unroll
+  for (int t = 0; t < TN; ++t) {
+    const int cb = c0 + 16 * t + li;
+    vb[t] = cb < C ? (cb * D + 4 * g) * 4 : kOob;
+  }
+  f32x4 acc[TN];
+  float na = 0.f, nb[TN];
+#pragma unroll
+  for (int t = 0; t < TN; ++t) {
+    acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    nb[t] = 0.f;
+  }
+  for (int k0 = 0; k0 < D; k0 += 16) {
+    const bool kin = k0 + 4 * g < D;   // D % 4 == 0: a chunk is all in or all out
+    const f32x4 a4 = ld4(ba, kin ? va : kOob, k0 * 4);
+    na += a4.x * a4.x + a4.y * a4.y + a4.z * a4.z + a4.w * a4.w;
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      const f32x4 b4 = ld4(bb, kin ? vb[t] : kOob, k0 * 4);
+      nb[t] += b4.x * b4.x + b4.y * b4.y + b4.z * b4.z + b4.w * b4.w;
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.x, b4.x, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.y, b4.y, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.z, b4.z, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.w, b4.w, acc[t], 0, 0, 0);
+    }
+  }
+  // squared norms: sum the four k groups of each row (lanes li, li+16, li+32, li+48)
+  na += __shfl_xor(na, 16);
+  na += __shfl_xor(na, 32);
+#pragma unroll
+  for (int t = 0; t < TN; ++t) {
+    nb[t] += __shfl_xor(nb[t], 16);
+    nb[t] += __shfl_xor(nb[t], 32);
+  }
+  float* o = out + (size_t)p * R * C;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = r0 + 4 * g + i;
+    const float nr = __shfl(na, 4 * g + i);   // lane 4g+i holds row 4g+i's norm
+#pragma unroll
+    for (int t = 0; t < TN; ++t) {
+      const int c = c0 + 16 * t + li;
+      if (r < R && c < C) o[(size_t)r * C + c] = finish_cost<float, MET>(nr + nb[t] - 2.f * acc[t][i]);
+    }
+  }
+}
+
+// ------------------------------------------------ fused per-pair backward
+//
+// One workgroup per pair with dS = adjoint(dcost) [R, C] in LDS together
+// with its row and column sums. Threads run along D; each keeps the C values
+// B[:, d] and the C partial sums of dB[:, d] in registers and walks the rows
+// once: dA[r, d] = 2 (rs[r] a - sum_c dS[r,c] B[c,d]), dB partial
+// += dS[r, c] a, a = A[r, d]. A and B are read once and dA, dB written once.
+
+template <typename T, int MET, int CMAX>
+__global__ void __launch_bounds__(256) pair_bwd_small(const T* __restrict__ A,
+                                                      const T* __restrict__ Bm,
+                                                      const T* __restrict__ cost,
+                                                      const T* __restrict__ dcost,
+                                                      T* __restrict__ dA, T* __restrict__ dB,
+                                                      int R, int C, int D) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* dS = reinterpret_cast<T*>(smem_raw);   // [R][CMAX], zero-padded
+  T* rs = dS + (size_t)R * CMAX;            // [R]
+  T* cs = rs + R;                           // [CMAX]
+  const int p = blockIdx.x, tid = threadIdx.x;
+  const size_t prc = (size_t)p * R * C;
+  for (int e = tid; e < R * CMAX; e += blockDim.x) {
+    const int r = e / CMAX, c = e % CMAX;
+    T v = (T)0;
+    if (c < C) {
+      const size_t o = prc + (size_t)r * C + c;
+      v = cost_adjoint<T, MET>(dcost[o], MET == MET_RAW ? (T)0 : cost[o]);
+    }
+    dS[e] = v;
+  }
+  __syncthreads();
+  for (int r = tid; r < R; r += blockDim.x) {
+    T acc = 0;
+    for (int c = 0; c < C; ++c) acc += dS[r * CMAX + c];
+    rs[r] = acc;
+  }
+  for (int c = tid; c < CMAX; c += blockDim.x) {
+    T acc = 0;
+    for (int r = 0; r < R; ++r) acc += dS[r * CMAX + c];
+    cs[c] = acc;
+  }
+  __syncthreads();
+  const T* Ap = A + (size_t)p * R * D;
+  const T* Bp = Bm + (size_t)p * C * D;
+  for (int d = tid; d < D; d += blockDim.x) {
+    T bc[CMAX], gb[CMAX];
+#pragma unroll
+    for (int c = 0; c < CMAX; ++c) {
+      bc[c] = c < C ? Bp[(size_t)c * D + d] : (T)0;
+      gb[c] = (T)0;
+    }
+#pragma unroll 4
+    for (int r = 0; r < R; ++r) {
+      const T a = Ap[(size_t)r * D + d];
+      const T* row = dS + r * CMAX;
+      T s = (T)0;
+#pragma unroll
+      for (int c = 0; c < CMAX; ++c) {
+        s += row[c] * bc[c];
+        gb[c] += row[c] * a;
+      }
+      dA[((size_t)p * R + r) * D + d] = (T)2 * (rs[r] * a - s);
+    }
+#pragma unroll
+    for (int c = 0; c < CMAX; ++c)
+      if (c < C) dB[((size_t)p * C + c) * D + d] = (T)2 * (cs[c] * bc[c] - gb[c]);
+  }
+}
+
 // ------------------------------------------------------------- launchers
 
 static inline unsigned blocks_for(long long n) { return (unsigned)((n + 255) / 256); }
@@ -111,12 +270,36 @@ int pair_cost_fwd(const T* A, const T* Bm, int P, int R, int C, int D, int metri
   if (!A || !Bm || !out) return fail(TW_EINVAL, "%s: null pointer", what);
   if (P == 0) return TW_OK;
   if (P > 65535) return fail(TW_ESIZE, "%s: at most 65535 pairs per call", what);
+  if (metric != MET_RAW && metric != MET_SQ && metric != MET_EUC)
+    return fail(TW_EINVAL, "%s: unknown metric %d", what, metric);
+  if ((long long)R * D >= (1LL << 29) || (long long)C * D >= (1LL << 29))
+    return fail(TW_ESIZE, "%s: one pair's block must stay below 2 GiB", what);
+  if (sizeof(T) == 4 && D % 4 == 0) {
+    // TN column tiles of 16 per wavefront share the A operand
+    const int TN = C > 32 ? 4 : (C > 16 ? 2 : 1);
+    const long long strips = (long long)((R + 15) / 16) * ((C + 16 * TN - 1) / (16 * TN));
+    dim3 grid((unsigned)((strips + 3) / 4), P), block(256);
+    const float* Af = reinterpret_cast<const float*>(A);
+    const float* Bf = reinterpret_cast<const float*>(Bm);
+    float* of = reinterpret_cast<float*>(out);
+#define TW_PAIR_MFMA(MET_, TN_) \
+  hipLaunchKernelGGL((pair_fwd_mfma<MET_, TN_>), grid, block, 0, s, Af, Bf, of, R, C, D)
+#define TW_PAIR_MFMA_TN(MET_)          \
+  if (TN == 4) TW_PAIR_MFMA(MET_, 4);  \
+  else if (TN == 2) TW_PAIR_MFMA(MET_, 2); \
+  else TW_PAIR_MFMA(MET_, 1);
+    if (metric == MET_RAW) { TW_PAIR_MFMA_TN(MET_RAW) }
+    else if (metric == MET_SQ) { TW_PAIR_MFMA_TN(MET_SQ) }
+    else { TW_PAIR_MFMA_TN(MET_EUC) }
+#undef TW_PAIR_MFMA_TN
+#undef TW_PAIR_MFMA
+    return check_launch(what);
+  }
   dim3 grid(blocks_for((long long)R * C), P), block(256);
   switch (metric) {
     case MET_RAW: hipLaunchKernelGGL((pair_fwd_fma<T, MET_RAW>), grid, block, 0, s, A, Bm, out, R, C, D); break;
     case MET_SQ: hipLaunchKernelGGL((pair_fwd_fma<T, MET_SQ>), grid, block, 0, s, A, Bm, out, R, C, D); break;
-    case MET_EUC: hipLaunchKernelGGL((pair_fwd_fma<T, MET_EUC>), grid, block, 0, s, A, Bm, out, R, C, D); break;
-    default: return fail(TW_EINVAL, "%s: unknown metric %d", what, metric);
+    default: hipLaunchKernelGGL((pair_fwd_fma<T, MET_EUC>), grid, block, 0, s, A, Bm, out, R, C, D); break;
   }
   return check_launch(what);
 }
@@ -129,6 +312,26 @@ int pair_cost_bwd(const T* A, const T* Bm, const T* cost, const T* dcost, int P,
   if (metric != MET_RAW && !cost) return fail(TW_EINVAL, "%s: metric needs the cost", what);
   if (P == 0) return TW_OK;
   if (P > 65535) return fail(TW_ESIZE, "%s: at most 65535 pairs per call", what);
+  if (metric != MET_RAW && metric != MET_SQ && metric != MET_EUC)
+    return fail(TW_EINVAL, "%s: unknown metric %d", what, metric);
+  const int cmax = C <= 8 ? 8 : (C <= 16 ? 16 : (C <= 32 ? 32 : (C <= 64 ? 64 : 0)));
+  const size_t lds = ((size_t)R * cmax + R + cmax) * sizeof(T);
+  if (cmax && lds <= 48 * 1024) {
+#define TW_PAIR_SMALL(MET_, CM_)                                                            \
+  hipLaunchKernelGGL((pair_bwd_small<T, MET_, CM_>), dim3(P), dim3(256), lds, s, A, Bm, cost, \
+                     dcost, dA, dB, R, C, D)
+#define TW_PAIR_SMALL_C(MET_)                  \
+  if (cmax == 8) TW_PAIR_SMALL(MET_, 8);        \
+  else if (cmax == 16) TW_PAIR_SMALL(MET_, 16); \
+  else if (cmax == 32) TW_PAIR_SMALL(MET_, 32); \
+  else TW_PAIR_SMALL(MET_, 64);
+    if (metric == MET_RAW) { TW_PAIR_SMALL_C(MET_RAW) }
+    else if (metric == MET_SQ) { TW_PAIR_SMALL_C(MET_SQ) }
+    else { TW_PAIR_SMALL_C(MET_EUC) }
+#undef TW_PAIR_SMALL_C
+#undef TW_PAIR_SMALL
+    return check_launch(what);
+  }
   dim3 ga(blocks_for((long long)R * D), P), gb(blocks_for((long long)C * D), P), block(256);
 #define TW_PAIR_BWD(MET_)                                                                     \
   hipLaunchKernelGGL((pair_bwd_a_fma<T, MET_>), ga, block, 0, s, A, Bm, cost, dcost, dA, R,   \
