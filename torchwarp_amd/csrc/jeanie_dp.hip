@@ -188,6 +188,257 @@ __global__ void __launch_bounds__(1024) jeanie_bwd_kernel(JeanieArgs<T> a) {
   }
 }
 
+// --------------------------------------------------------- JEANIE v2
+//
+// The viewpoint window is a product W1 x W2 (|n1'-n1| <= s1, |n2'-n2| <= s2)
+// and a softmin over a union of disjoint sets is the softmin of their
+// softmins, so
+//   R[n,t,u] = C + softmin{ Rw[n,t-1,u], Rw[n,t,u-1], Rw[n,t-1,u-1] },
+//   Rw[n,.]  = softmin_{a1 in W1(n1)} S2[a1,n2],  S2[a1,n2] = softmin_{a2 in W2(n2)} R[a1,a2]
+// exactly: a cell costs 3 + (2 s2 + 1) + (2 s1 + 1) exps instead of
+// 3 (2 s1 + 1)(2 s2 + 1). The backward runs the same three stages in reverse:
+//   RWbar[n,tau] = sum_{s in temporal successors} Rbar_s 2^(Fh_s - Rwh[n,tau]),  Fh = Rh - Ch
+//   S2bar[a1,n2] = sum_{n1: |n1-a1| <= s1} RWbar[n1,n2] 2^(Rwh[n1,n2] - S2h[a1,n2])
+//   Rbar[a1,a2]  = sum_{n2: |n2-a2| <= s2} S2bar[a1,n2] 2^(S2h[a1,n2] - Rh[a1,a2]) (+ seeds)
+// with Rw and S2 recomputed from R (cheaper than carrying them through HBM).
+//
+// Threads: one group of KP lanes (KP = power of two >= K, <= 64) per DP row
+// t, one lane per viewpoint n = n1 K2 + n2, so a group never straddles a
+// wavefront: window neighbours come from ds_bpermute shuffles with no
+// barrier. Only the temporal "up" value crosses groups, through a two-slot
+// LDS ring (one barrier per diagonal); "left" and "diagonal" stay in
+// registers. With STAGE the pair's cost (and R) sits in LDS as [t][u][n]
+// (n fastest: conflict-free per diagonal) and moves to and from HBM with
+// coalesced loops in the caller's layout.
+
+template <typename T, int SMAX>
+__device__ __forceinline__ T win_softmin(T v, int lane, int stride, int pos, int cnt, int s) {
+  if (s == 0) return v;
+  T w[2 * SMAX + 1];
+  T m = inf_v<T>();
+#pragma unroll
+  for (int o = -SMAX; o <= SMAX; ++o) {
+    T x = __shfl(v, lane + o * stride);
+    const bool in = o >= -s && o <= s && pos + o >= 0 && pos + o < cnt;
+    x = in ? x : inf_v<T>();
+    w[o + SMAX] = x;
+    m = fmin(m, x);
+  }
+  T sum = 0;
+#pragma unroll
+  for (int o = -SMAX; o <= SMAX; ++o)
+    if (o >= -s && o <= s) sum += ex2(m - w[o + SMAX]);
+  return m - lg2(sum);
+}
+
+// sum over window neighbours q = lane + o stride of g[q] 2^(h[q] - x)
+template <typename T, int SMAX>
+__device__ __forceinline__ T win_adjoint(T g, T h, T x, int lane, int stride, int pos, int cnt,
+                                         int s) {
+  if (s == 0) return g;
+  T acc = 0;
+#pragma unroll
+  for (int o = -SMAX; o <= SMAX; ++o) {
+    const T gq = __shfl(g, lane + o * stride);
+    const T hq = __shfl(h, lane + o * stride);
+    const bool in = o >= -s && o <= s && pos + o >= 0 && pos + o < cnt;
+    if (o >= -s && o <= s) acc += in ? gq * ex2(hq - x) : (T)0;
+  }
+  return acc;
+}
+
+// softmin over the K lanes of a group (in the scaled domain)
+template <typename T>
+__device__ __forceinline__ T group_softmin(T v, int KP) {
+  T m = v;
+  for (int o = 1; o < KP; o <<= 1) m = fmin(m, __shfl_xor(m, o));
+  T sum = ex2(m - v);
+  for (int o = 1; o < KP; o <<= 1) sum += __shfl_xor(sum, o);
+  return m - lg2(sum);
+}
+
+// (t, u) of position r of a caller-layout plane ([T][U], or [U][T] with swap), as t * U + u
+template <typename T>
+__device__ __forceinline__ int caller_tu(const JeanieArgs<T>& a, int r) {
+  const int inner = a.swap ? a.Tn : a.Un;
+  const int q = r / inner, rem = r - q * inner;
+  const int t = a.swap ? rem : q, u = a.swap ? q : rem;
+  return t * a.Un + u;
+}
+
+template <typename T, bool STAGE, int SMAX>
+__global__ void __launch_bounds__(1024) jeanie2_fwd_kernel(JeanieArgs<T> a, int KP) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const int K = a.K, Tn = a.Tn, Un = a.Un, K2 = a.K2, K1 = a.K1;
+  const int b = blockIdx.x, tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63;
+  const int t = tid / KP, n = tid - t * KP;
+  const bool vn = n < K && t < Tn;
+  const int n1 = vn ? n / K2 : 0, n2 = vn ? n - n1 * K2 : 0;
+  const int plane = Tn * Un;
+  const size_t pair = (size_t)K * plane;
+  const T* Cb = a.C + b * pair;
+  T* Rb = a.Rw + b * pair;
+  const T INF = inf_v<T>();
+  const int Dn = Tn + Un - 1;
+
+  T* ring = reinterpret_cast<T*>(smem_raw);   // [2][nthr] Rwh of the last diagonal
+  T* Cs = ring + 2 * nthr;                    // STAGE: [t][u][n] scaled cost
+  T* Rs = Cs + pair;                          // STAGE: [t][u][n] R (unscaled)
+  if (STAGE) {
+    for (int e = tid; e < (int)pair; e += nthr) {
+      const int nn = e / plane;
+      Cs[caller_tu(a, e - nn * plane) * K + nn] = Cb[e] * a.k;
+    }
+    __syncthreads();
+  }
+
+  T lf = INF, dgv = INF, rh = INF;
+  for (int d = 0; d < Dn; ++d) {
+    const int u = d - t;
+    const bool valid = vn && u >= 0 && u < Un;
+    T up = (d > 0 && t > 0) ? ring[((d - 1) & 1) * nthr + tid - KP] : INF;
+    T ch = (T)0;
+    if (valid) ch = STAGE ? Cs[(t * Un + u) * K + n] : Cb[jidx(a, n, t, u)] * a.k;
+    if (d == 0) {
+      rh = ch;   // cells (n, 0, 0): every viewpoint may start
+    } else {
+      const T m = min3(up, lf, dgv);
+      const T sum = ex2(m - up) + ex2(m - lf) + ex2(m - dgv);
+      rh = ch + m - lg2(sum);
+    }
+    rh = valid ? rh : INF;
+    const T s2h = win_softmin<T, SMAX>(rh, lane, 1, n2, K2, a.s2);
+    T rwh = win_softmin<T, SMAX>(s2h, lane, K2, n1, K1, a.s1);
+    rwh = valid ? rwh : INF;
+    if (valid) {
+      const T rv = rh * a.inv_k;
+      if (STAGE)
+        Rs[(t * Un + u) * K + n] = rv;
+      else
+        Rb[jidx(a, n, t, u)] = rv;
+    }
+    ring[(d & 1) * nthr + tid] = rwh;
+    dgv = up;
+    lf = rwh;
+    lds_barrier();
+  }
+  // out = softmin over the viewpoints of R[., T-1, U-1] (the last row group holds them)
+  const T fin = group_softmin(vn ? rh : INF, KP);
+  if (t == Tn - 1 && n == 0) a.out[b] = fin * a.inv_k;
+  if (STAGE) {
+    __syncthreads();
+    for (int e = tid; e < (int)pair; e += nthr) {
+      const int nn = e / plane;
+      Rb[e] = Rs[caller_tu(a, e - nn * plane) * K + nn];
+    }
+  }
+}
+
+template <typename T, bool STAGE, int SMAX>
+__global__ void __launch_bounds__(1024) jeanie2_bwd_kernel(JeanieArgs<T> a, int KP) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const int K = a.K, Tn = a.Tn, Un = a.Un, K2 = a.K2, K1 = a.K1;
+  const int b = blockIdx.x, tid = threadIdx.x, nthr = blockDim.x, lane = tid & 63;
+  const int t = tid / KP, n = tid - t * KP;
+  const bool vn = n < K && t < Tn;
+  const int n1 = vn ? n / K2 : 0, n2 = vn ? n - n1 * K2 : 0;
+  const int plane = Tn * Un;
+  const size_t pair = (size_t)K * plane;
+  const T* Cb = a.C + b * pair;
+  const T* Rb = a.R + b * pair;
+  const T* gRb = a.gR ? a.gR + b * pair : nullptr;
+  T* dCb = a.dC + b * pair;
+  const T INF = inf_v<T>();
+  const int Dn = Tn + Un - 1;
+  const T gout = a.gout[b];
+
+  T* ringF = reinterpret_cast<T*>(smem_raw);   // [2][nthr] Fh = Rh - Ch of the last diagonal
+  T* ringG = ringF + 2 * nthr;                 // [2][nthr] Rbar of the last diagonal
+  T* Cs = ringG + 2 * nthr;                    // STAGE: [t][u][n] scaled cost, then dC
+  T* Rs = Cs + pair;                           // STAGE: [t][u][n] scaled R
+  if (STAGE) {
+    for (int e = tid; e < (int)pair; e += nthr) {
+      const int nn = e / plane;
+      const int l = caller_tu(a, e - nn * plane) * K + nn;
+      Cs[l] = Cb[e] * a.k;
+      Rs[l] = Rb[e] * a.k;
+    }
+    __syncthreads();
+  }
+
+  T Fr = -INF, Gr = 0, Fdg = -INF, Gdg = 0, fin = INF;
+  for (int d = Dn - 1; d >= 0; --d) {
+    const int u = d - t;
+    const bool valid = vn && u >= 0 && u < Un;
+    const bool has_down = d < Dn - 1 && t + 1 < Tn;
+    const int dslot = ((d + 1) & 1) * nthr + tid + KP;
+    const T Fd = has_down ? ringF[dslot] : -INF;
+    const T Gd = has_down ? ringG[dslot] : (T)0;
+    T rh = INF, ch = 0;
+    if (valid) {
+      if (STAGE) {
+        const int l = (t * Un + u) * K + n;
+        rh = Rs[l];
+        ch = Cs[l];
+      } else {
+        const size_t o = jidx(a, n, t, u);
+        rh = Rb[o] * a.k;
+        ch = Cb[o] * a.k;
+      }
+    }
+    if (d == Dn - 1) fin = group_softmin(rh, KP);   // valid lanes: the last row group
+    const T s2h = win_softmin<T, SMAX>(rh, lane, 1, n2, K2, a.s2);
+    const T rwh = win_softmin<T, SMAX>(s2h, lane, K2, n1, K1, a.s1);
+    T wbar = Gr * ex2(Fr - rwh) + Gd * ex2(Fd - rwh) + Gdg * ex2(Fdg - rwh);
+    wbar = valid ? wbar : (T)0;
+    const T s2bar = win_adjoint<T, SMAX>(wbar, valid ? rwh : (T)0, s2h, lane, K2, n1, K1, a.s1);
+    T rbar = win_adjoint<T, SMAX>(valid ? s2bar : (T)0, valid ? s2h : (T)0, rh, lane, 1, n2, K2,
+                                  a.s2);
+    if (d == Dn - 1) rbar += gout * ex2(fin - rh);
+    if (gRb && valid) rbar += gRb[jidx(a, n, t, u)];
+    rbar = valid ? rbar : (T)0;
+    const T F = valid ? rh - ch : -INF;
+    if (valid) {
+      if (STAGE)
+        Cs[(t * Un + u) * K + n] = rbar;   // the cell's cost is no longer needed
+      else
+        dCb[jidx(a, n, t, u)] = rbar;
+    }
+    ringF[(d & 1) * nthr + tid] = F;
+    ringG[(d & 1) * nthr + tid] = rbar;
+    Fdg = Fd;
+    Gdg = Gd;
+    Fr = F;
+    Gr = rbar;
+    lds_barrier();
+  }
+  if (STAGE) {
+    __syncthreads();
+    for (int e = tid; e < (int)pair; e += nthr) {
+      const int nn = e / plane;
+      dCb[e] = Cs[caller_tu(a, e - nn * plane) * K + nn];
+    }
+  }
+}
+
+// Launch shape of the v2 kernels: 0 threads when the shape needs the
+// general kernels (more than 64 viewpoints, shifts above 2, > 1024 threads).
+struct J2Shape {
+  int KP, threads, smax;
+};
+static J2Shape jeanie2_shape(int K, int Tn, int s1, int s2) {
+  J2Shape sh = {0, 0, 0};
+  if (K > 64 || s1 > 2 || s2 > 2) return sh;
+  int kp = 1;
+  while (kp < K) kp <<= 1;
+  const int threads = ((Tn * kp + 63) / 64) * 64;
+  if (threads > 1024) return sh;
+  sh.KP = kp;
+  sh.threads = threads;
+  sh.smax = (s1 > 1 || s2 > 1) ? 2 : 1;
+  return sh;
+}
+
 static int jeanie_threads(int cells) {
   int t = ((cells + 63) / 64) * 64;
   return t < 64 ? 64 : (t > 1024 ? 1024 : t);
@@ -230,6 +481,22 @@ int jeanie_cost_fwd(const T* C, int B, int K1, int K2, int Tn, int Un, int swap,
   a.Rw = R;
   a.out = out;
   jeanie_fill(a, K1, K2, Tn, Un, s1, s2, swap, gamma);
+  const J2Shape sh = jeanie2_shape(a.K, Tn, a.s1, a.s2);
+  if (sh.threads) {
+    const size_t ring = (size_t)2 * sh.threads * sizeof(T);
+    const size_t stage = ring + (size_t)2 * a.K * Tn * Un * sizeof(T);
+    const bool st = stage <= (size_t)(64 * 1024) && stage <= (size_t)max_lds_bytes();
+    const size_t lds = st ? stage : ring;
+#define TW_J2F(ST_, SM_) \
+  hipLaunchKernelGGL((jeanie2_fwd_kernel<T, ST_, SM_>), dim3(B), dim3(sh.threads), lds, s, a, sh.KP)
+    if (st) {
+      if (sh.smax == 1) TW_J2F(true, 1); else TW_J2F(true, 2);
+    } else {
+      if (sh.smax == 1) TW_J2F(false, 1); else TW_J2F(false, 2);
+    }
+#undef TW_J2F
+    return check_launch(what);
+  }
   const int threads = jeanie_threads(Tn * a.K);
   const size_t lds = (size_t)3 * Tn * a.K * sizeof(T);
   if (lds <= (size_t)max_lds_bytes())
@@ -253,6 +520,22 @@ int jeanie_cost_bwd(const T* C, const T* R, const T* gout, const T* gR, int B, i
   a.gR = gR;
   a.dC = dC;
   jeanie_fill(a, K1, K2, Tn, Un, s1, s2, swap, gamma);
+  const J2Shape sh = jeanie2_shape(a.K, Tn, a.s1, a.s2);
+  if (sh.threads) {
+    const size_t ring = (size_t)4 * sh.threads * sizeof(T);
+    const size_t stage = ring + (size_t)2 * a.K * Tn * Un * sizeof(T);
+    const bool st = stage <= (size_t)(64 * 1024) && stage <= (size_t)max_lds_bytes();
+    const size_t lds = st ? stage : ring;
+#define TW_J2B(ST_, SM_) \
+  hipLaunchKernelGGL((jeanie2_bwd_kernel<T, ST_, SM_>), dim3(B), dim3(sh.threads), lds, s, a, sh.KP)
+    if (st) {
+      if (sh.smax == 1) TW_J2B(true, 1); else TW_J2B(true, 2);
+    } else {
+      if (sh.smax == 1) TW_J2B(false, 1); else TW_J2B(false, 2);
+    }
+#undef TW_J2B
+    return check_launch(what);
+  }
   const int threads = jeanie_threads(Tn * a.K);
   const size_t lds = (size_t)6 * Tn * a.K * sizeof(T);
   if (lds + sizeof(T) <= (size_t)max_lds_bytes())
