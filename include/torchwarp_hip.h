@@ -176,6 +176,17 @@ int tw_pair_cost_bwd_f64(const double* A, const double* Bm, const double* cost,
                          const double* d_cost, int P, int R, int C, int D, int metric,
                          double* dA, double* dB, hipStream_t stream);
 
+/* --------------------------------------------------------- hard paths --
+ * Optimal (gamma = 0) alignment path with bit-exact indices. Replaces the
+ * numpy DP + backtrack of paths.py:85-127 (_optimal_3d / optimal_path).
+ * cost: [B, K, T, U] float64 (K = 1 for a plain cost matrix); max_shift: the
+ * viewpoint window; start_view: -1 or the only viewpoint allowed at (0,0).
+ * Workspace r_ws: B*K*T*U doubles, back_ws: B*K*T*U ints. Output path:
+ * [B, T+U-1, 3] ints (t, u, k) from (0,0) on, path_len: [B] entries used. */
+int tw_optimal_path_f64(const double* cost, int B, int K, int T, int U, int max_shift,
+                        int start_view, double* r_ws, int* back_ws, int* path, int* path_len,
+                        hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -25,7 +25,7 @@ def _declared():
 def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(_hip.LIB_PATH))
     names = _declared()
-    assert len(names) == 27
+    assert len(names) == 28
     for name in names:
         assert hasattr(lib, name), name
     assert lib.tw_version() == 1
@@ -35,6 +35,7 @@ def test_binding_covers_every_entry_point():
     bound = {"tw_version", "tw_last_error", "tw_udtw_feat_workspace_bytes"}
     for base in _hip.SIGNATURES:
         bound |= {base + "_f32", base + "_f64"}
+    bound |= {base + "_f64" for base in _hip.SIGNATURES_F64}
     assert set(_declared()) == bound
 
 
@@ -55,6 +56,8 @@ def test_cpu_tensors_fail_loudly():
         TF.fvm_from_cost(torch.rand(1, 2, 4, 5))
     with pytest.raises(ValueError, match="backend='torch'"):
         TF.soft_dtw_from_cost(torch.rand(1, 4, 5), backend="torch")
+    with pytest.raises(RuntimeError, match="ROCm"):
+        tw.paths.optimal_path(torch.rand(1, 4, 5))
 
 
 def test_udtw_input_validation():

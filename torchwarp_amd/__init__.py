@@ -6,7 +6,7 @@ A drop-in for torchwarp's public API (``src/torchwarp/__init__.py:1-21``):
     import torchwarp_amd.functional as TF
 """
 
-from . import functional
+from . import functional, paths
 from .jeanie import FVM, JEANIE, euclidean_cost, rbf_cost, squared_euclidean_cost
 from .sdtw import SoftDTW
 from .udtw import UDTW
@@ -15,5 +15,5 @@ __version__ = "0.1.0"
 
 __all__ = [
     "UDTW", "SoftDTW", "JEANIE", "FVM", "euclidean_cost", "squared_euclidean_cost",
-    "rbf_cost", "functional",
+    "rbf_cost", "functional", "paths",
 ]

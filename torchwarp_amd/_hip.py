@@ -32,6 +32,11 @@ SIGNATURES = {
     "tw_pair_cost_bwd": "ppppiiiiipps",
 }
 
+# entry points that exist in float64 only
+SIGNATURES_F64 = {
+    "tw_optimal_path": "piiiiiipppps",
+}
+
 METRIC_RAW, METRIC_SQEUC, METRIC_EUC = 0, 1, 2
 
 _lib = None
@@ -65,6 +70,10 @@ def _load():
             fn = getattr(lib, base + suffix)
             fn.restype = ctypes.c_int
             fn.argtypes = [_ctype(c, real) for c in sig]
+    for base, sig in SIGNATURES_F64.items():
+        fn = getattr(lib, base + "_f64")
+        fn.restype = ctypes.c_int
+        fn.argtypes = [_ctype(c, ctypes.c_double) for c in sig]
     _lib = lib
     return lib
 

@@ -247,6 +247,54 @@ __device__ __forceinline__ T win_adjoint(T g, T h, T x, int lane, int stride, in
   return acc;
 }
 
+// The same two reductions along the stride-1 axis (neighbouring lanes), with
+// DPP wave shifts instead of LDS-routed shuffles; offsets beyond +-1 chain
+// shifts. The shift's source lane is masked by `pos` exactly as above.
+template <typename T>
+__device__ __forceinline__ T lane_shift(T v, int o) {
+  // o in [-2, 2]: value of lane (l + o)
+  if (o == -1) return shift_prev(v, v);
+  if (o == 1) return shift_next(v, v);
+  if (o == -2) return shift_prev(shift_prev(v, v), v);
+  if (o == 2) return shift_next(shift_next(v, v), v);
+  return v;
+}
+
+template <typename T, int SMAX>
+__device__ __forceinline__ T win_softmin_dpp(T v, int pos, int cnt, int s) {
+  if (s == 0) return v;
+  T w[2 * SMAX + 1];
+  T m = inf_v<T>();
+#pragma unroll
+  for (int o = -SMAX; o <= SMAX; ++o) {
+    T x = lane_shift(v, o);
+    const bool in = o >= -s && o <= s && pos + o >= 0 && pos + o < cnt;
+    x = in ? x : inf_v<T>();
+    w[o + SMAX] = x;
+    m = fmin(m, x);
+  }
+  T sum = 0;
+#pragma unroll
+  for (int o = -SMAX; o <= SMAX; ++o)
+    if (o >= -s && o <= s) sum += ex2(m - w[o + SMAX]);
+  return m - lg2(sum);
+}
+
+template <typename T, int SMAX>
+__device__ __forceinline__ T win_adjoint_dpp(T g, T h, T x, int pos, int cnt, int s) {
+  if (s == 0) return g;
+  T acc = 0;
+#pragma unroll
+  for (int o = -SMAX; o <= SMAX; ++o) {
+    if (o < -s || o > s) continue;
+    const T gq = lane_shift(g, o);
+    const T hq = lane_shift(h, o);
+    const bool in = pos + o >= 0 && pos + o < cnt;
+    acc += in ? gq * ex2(hq - x) : (T)0;
+  }
+  return acc;
+}
+
 // softmin over the K lanes of a group (in the scaled domain)
 template <typename T>
 __device__ __forceinline__ T group_softmin(T v, int KP) {
@@ -285,15 +333,36 @@ __global__ void __launch_bounds__(1024) jeanie2_fwd_kernel(JeanieArgs<T> a, int 
   T* Cs = ring + 2 * nthr;                    // STAGE: [t][u][n] scaled cost
   T* Rs = Cs + pair;                          // STAGE: [t][u][n] R (unscaled)
   if (STAGE) {
-    for (int e = tid; e < (int)pair; e += nthr) {
-      const int nn = e / plane;
-      Cs[caller_tu(a, e - nn * plane) * K + nn] = Cb[e] * a.k;
+    // eight loads in flight per thread, then the scattered LDS stores
+    for (int e0 = 0; e0 < (int)pair; e0 += 8 * nthr) {
+      T v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = e0 + j * nthr + tid;
+        v[j] = e < (int)pair ? Cb[e] : (T)0;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = e0 + j * nthr + tid;
+        const int nn = e / plane;
+        if (e < (int)pair) Cs[caller_tu(a, e - nn * plane) * K + nn] = v[j] * a.k;
+      }
     }
     __syncthreads();
   }
 
+  // rows t_lo .. t_lo + 64/KP - 1 share this wavefront; a wavefront with no
+  // row on the diagonal only publishes the neutral values its neighbours read
+  const int t_lo = __builtin_amdgcn_readfirstlane(tid >> 6) * (64 / KP);
+  const int t_hi = t_lo + 64 / KP - 1;
   T lf = INF, dgv = INF, rh = INF;
   for (int d = 0; d < Dn; ++d) {
+    if (t_lo > min(Tn - 1, d) || t_hi < max(0, d - Un + 1)) {
+      ring[(d & 1) * nthr + tid] = INF;
+      lf = dgv = rh = INF;
+      lds_barrier();
+      continue;
+    }
     const int u = d - t;
     const bool valid = vn && u >= 0 && u < Un;
     T up = (d > 0 && t > 0) ? ring[((d - 1) & 1) * nthr + tid - KP] : INF;
@@ -307,7 +376,7 @@ __global__ void __launch_bounds__(1024) jeanie2_fwd_kernel(JeanieArgs<T> a, int 
       rh = ch + m - lg2(sum);
     }
     rh = valid ? rh : INF;
-    const T s2h = win_softmin<T, SMAX>(rh, lane, 1, n2, K2, a.s2);
+    const T s2h = win_softmin_dpp<T, SMAX>(rh, n2, K2, a.s2);
     T rwh = win_softmin<T, SMAX>(s2h, lane, K2, n1, K1, a.s1);
     rwh = valid ? rwh : INF;
     if (valid) {
@@ -357,17 +426,41 @@ __global__ void __launch_bounds__(1024) jeanie2_bwd_kernel(JeanieArgs<T> a, int 
   T* Cs = ringG + 2 * nthr;                    // STAGE: [t][u][n] scaled cost, then dC
   T* Rs = Cs + pair;                           // STAGE: [t][u][n] scaled R
   if (STAGE) {
-    for (int e = tid; e < (int)pair; e += nthr) {
-      const int nn = e / plane;
-      const int l = caller_tu(a, e - nn * plane) * K + nn;
-      Cs[l] = Cb[e] * a.k;
-      Rs[l] = Rb[e] * a.k;
+    for (int e0 = 0; e0 < (int)pair; e0 += 4 * nthr) {
+      T vc[4], vr[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = e0 + j * nthr + tid;
+        vc[j] = e < (int)pair ? Cb[e] : (T)0;
+        vr[j] = e < (int)pair ? Rb[e] : (T)0;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int e = e0 + j * nthr + tid;
+        const int nn = e / plane;
+        const int l = caller_tu(a, e - nn * plane) * K + nn;
+        if (e < (int)pair) {
+          Cs[l] = vc[j] * a.k;
+          Rs[l] = vr[j] * a.k;
+        }
+      }
     }
     __syncthreads();
   }
 
+  const int t_lo = __builtin_amdgcn_readfirstlane(tid >> 6) * (64 / KP);
+  const int t_hi = t_lo + 64 / KP - 1;
   T Fr = -INF, Gr = 0, Fdg = -INF, Gdg = 0, fin = INF;
   for (int d = Dn - 1; d >= 0; --d) {
+    if (t_lo > min(Tn - 1, d) || t_hi < max(0, d - Un + 1)) {
+      // no row of this wavefront on diagonal d (see the forward)
+      ringF[(d & 1) * nthr + tid] = -INF;
+      ringG[(d & 1) * nthr + tid] = (T)0;
+      Fr = Fdg = -INF;
+      Gr = Gdg = (T)0;
+      lds_barrier();
+      continue;
+    }
     const int u = d - t;
     const bool valid = vn && u >= 0 && u < Un;
     const bool has_down = d < Dn - 1 && t + 1 < Tn;
@@ -387,13 +480,12 @@ __global__ void __launch_bounds__(1024) jeanie2_bwd_kernel(JeanieArgs<T> a, int 
       }
     }
     if (d == Dn - 1) fin = group_softmin(rh, KP);   // valid lanes: the last row group
-    const T s2h = win_softmin<T, SMAX>(rh, lane, 1, n2, K2, a.s2);
+    const T s2h = win_softmin_dpp<T, SMAX>(rh, n2, K2, a.s2);
     const T rwh = win_softmin<T, SMAX>(s2h, lane, K2, n1, K1, a.s1);
     T wbar = Gr * ex2(Fr - rwh) + Gd * ex2(Fd - rwh) + Gdg * ex2(Fdg - rwh);
     wbar = valid ? wbar : (T)0;
     const T s2bar = win_adjoint<T, SMAX>(wbar, valid ? rwh : (T)0, s2h, lane, K2, n1, K1, a.s1);
-    T rbar = win_adjoint<T, SMAX>(valid ? s2bar : (T)0, valid ? s2h : (T)0, rh, lane, 1, n2, K2,
-                                  a.s2);
+    T rbar = win_adjoint_dpp<T, SMAX>(valid ? s2bar : (T)0, valid ? s2h : (T)0, rh, n2, K2, a.s2);
     if (d == Dn - 1) rbar += gout * ex2(fin - rh);
     if (gRb && valid) rbar += gRb[jidx(a, n, t, u)];
     rbar = valid ? rbar : (T)0;
