@@ -131,6 +131,7 @@ def _hip_call_times(name, inputs, iters):
     f32 = torch.float32
     calls = []
     if name in ("cfg1", "cfg2", "cfg3"):
+        # standard deviations, squared inside the kernels (as the public API calls them)
         if name == "cfg1":
             X, Y = inputs
             vx = torch.ones(X.shape[:2], device=dev)
@@ -138,7 +139,7 @@ def _hip_call_times(name, inputs, iters):
             beta, gamma = 0.0, 1.0
         else:
             X, Y, sx, sy = inputs
-            vx, vy = sx.squeeze(-1) ** 2, sy.squeeze(-1) ** 2
+            vx, vy = sx.squeeze(-1), sy.squeeze(-1)
             beta, gamma = 1.0, (1.0 if name == "cfg2" else 0.1)
         B, N, D = X.shape
         M = Y.shape[1]
@@ -154,11 +155,11 @@ def _hip_call_times(name, inputs, iters):
         io = 4 * (X.numel() + Y.numel() + vx.numel() + vy.numel())
         carried = 4 * B * N * M * (2 if pen else 1)
         calls.append(("udtw_fwd", lambda: _hip.call(
-            "tw_udtw_feat_fwd", f32, X, Y, vx, vy, B, N, M, D, gamma, beta, 1e-8, 0.0, R, P, o1,
-            o2, ws, wsb), io + carried))
+            "tw_udtw_feat_fwd", f32, X, Y, vx, vy, B, N, M, D, gamma, beta, 1e-8, 0.0, 1, R, P,
+            o1, o2, ws, wsb), io + carried))
         calls.append(("udtw_bwd", lambda: _hip.call(
             "tw_udtw_feat_bwd", f32, X, Y, vx, vy, R, P, g, g if pen else None, B, N, M, D, gamma,
-            beta, 1e-8, 0.0, dX, dY, dvx, dvy, ws, wsb), 2 * io + carried))
+            beta, 1e-8, 0.0, 1, 1, dX, dY, dvx, dvy, ws, wsb), 2 * io + carried))
     elif name == "cfg5a":
         (c,) = inputs
         B = c.shape[0]

@@ -51,7 +51,9 @@ const char* tw_last_error(void);
  * cost, pen: [B,N,M]; pen may be NULL (zero penalty, P unused).
  * R, P: [B, N*M] internal; out_dist, out_pen: [B].
  * Backward: the forward's bandwidth; grad_dist, grad_pen [B] (grad_pen may be
- * NULL iff pen is NULL); d_cost, d_pen [B,N,M] (d_pen may be NULL). */
+ * NULL iff pen is NULL), read with element stride grad_stride (1, or 0 for one
+ * value shared by every pair, e.g. the expanded gradient of a mean);
+ * d_cost, d_pen [B,N,M] (d_pen may be NULL). */
 int tw_udtw_cost_fwd_f32(const float* cost, const float* pen, int B, int N, int M, float gamma,
                          float bandwidth, float* R, float* P, float* out_dist, float* out_pen,
                          hipStream_t stream);
@@ -60,43 +62,49 @@ int tw_udtw_cost_fwd_f64(const double* cost, const double* pen, int B, int N, in
                          double* out_pen, hipStream_t stream);
 int tw_udtw_cost_bwd_f32(const float* cost, const float* pen, const float* R, const float* P,
                          const float* grad_dist, const float* grad_pen, int B, int N, int M,
-                         float gamma, float bandwidth, float* d_cost, float* d_pen,
-                         hipStream_t stream);
+                         float gamma, float bandwidth, int grad_stride, float* d_cost,
+                         float* d_pen, hipStream_t stream);
 int tw_udtw_cost_bwd_f64(const double* cost, const double* pen, const double* R,
                          const double* P, const double* grad_dist, const double* grad_pen, int B,
-                         int N, int M, double gamma, double bandwidth, double* d_cost,
-                         double* d_pen, hipStream_t stream);
+                         int N, int M, double gamma, double bandwidth, int grad_stride,
+                         double* d_cost, double* d_pen, hipStream_t stream);
 
 /* uDTW straight from the features, N <= M. Replaces udtw_cuda.cu:738-775
  * (fused_forward) / :777-814 (fused_backward) together with the bmm / vecdot /
  * diagonal permutations of the ops torchwarp_udtw::fused / fused_backward
- * (udtw/_ops.py:157-211). X [B,N,D], Y [B,M,D], vx [B,N], vy [B,M] (sigma^2).
+ * (udtw/_ops.py:157-211). X [B,N,D], Y [B,M,D], vx [B,N], vy [B,M]: the
+ * variances sigma^2, or with sigma != 0 the standard deviations sigma (the
+ * kernels square them; this folds the reference's sigma.pow(2) of
+ * udtw/functional.py:157-158 and its backward into the call).
  * beta == 0 (soft-DTW) skips the penalty: P may be NULL, out_pen gets 0.
  * D == 1 runs fully fused; D > 1 needs workspace of
- * tw_udtw_feat_workspace_bytes(...) bytes. Backward writes dX [B,N,D],
- * dY [B,M,D] and, unless both are NULL, dvx [B,N], dvy [B,M]. */
+ * tw_udtw_feat_workspace_bytes(...) bytes. Backward: grad_dist / grad_pen
+ * with element stride grad_stride (1, or 0: one shared value); writes
+ * dX [B,N,D], dY [B,M,D] and, unless both are NULL, dvx [B,N], dvy [B,M]
+ * (gradients with respect to vx, vy as given: d sigma when sigma != 0). */
 size_t tw_udtw_feat_workspace_bytes(int B, int N, int M, int D, int elem_size);
 int tw_udtw_feat_fwd_f32(const float* X, const float* Y, const float* vx, const float* vy, int B,
                          int N, int M, int D, float gamma, float beta, float eps,
-                         float bandwidth, float* R, float* P, float* out_dist, float* out_pen,
-                         float* workspace, size_t workspace_bytes, hipStream_t stream);
+                         float bandwidth, int sigma, float* R, float* P, float* out_dist,
+                         float* out_pen, float* workspace, size_t workspace_bytes,
+                         hipStream_t stream);
 int tw_udtw_feat_fwd_f64(const double* X, const double* Y, const double* vx, const double* vy,
                          int B, int N, int M, int D, double gamma, double beta, double eps,
-                         double bandwidth, double* R, double* P, double* out_dist,
+                         double bandwidth, int sigma, double* R, double* P, double* out_dist,
                          double* out_pen, double* workspace, size_t workspace_bytes,
                          hipStream_t stream);
 int tw_udtw_feat_bwd_f32(const float* X, const float* Y, const float* vx, const float* vy,
                          const float* R, const float* P, const float* grad_dist,
                          const float* grad_pen, int B, int N, int M, int D, float gamma,
-                         float beta, float eps, float bandwidth, float* dX, float* dY,
-                         float* dvx, float* dvy, float* workspace, size_t workspace_bytes,
-                         hipStream_t stream);
+                         float beta, float eps, float bandwidth, int sigma, int grad_stride,
+                         float* dX, float* dY, float* dvx, float* dvy, float* workspace,
+                         size_t workspace_bytes, hipStream_t stream);
 int tw_udtw_feat_bwd_f64(const double* X, const double* Y, const double* vx, const double* vy,
                          const double* R, const double* P, const double* grad_dist,
                          const double* grad_pen, int B, int N, int M, int D, double gamma,
-                         double beta, double eps, double bandwidth, double* dX, double* dY,
-                         double* dvx, double* dvy, double* workspace, size_t workspace_bytes,
-                         hipStream_t stream);
+                         double beta, double eps, double bandwidth, int sigma, int grad_stride,
+                         double* dX, double* dY, double* dvx, double* dvy, double* workspace,
+                         size_t workspace_bytes, hipStream_t stream);
 
 /* -------------------------------------------------------------- JEANIE --
  * 3-D DP on a cost [B, K1*K2, T, U] (swap_tu = 0) or [B, K1*K2, U, T]

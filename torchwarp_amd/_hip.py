@@ -19,9 +19,9 @@ LIB_PATH = Path(__file__).resolve().parent / "libtorchwarp_hip.so"
 # z size_t, s stream
 SIGNATURES = {
     "tw_udtw_cost_fwd": "ppiiiffpppps",
-    "tw_udtw_cost_bwd": "ppppppiiiffpps",
-    "tw_udtw_feat_fwd": "ppppiiiiffffpppppzs",
-    "tw_udtw_feat_bwd": "ppppppppiiiiffffpppppzs",
+    "tw_udtw_cost_bwd": "ppppppiiiffipps",
+    "tw_udtw_feat_fwd": "ppppiiiiffffipppppzs",
+    "tw_udtw_feat_bwd": "ppppppppiiiiffffiipppppzs",
     "tw_jeanie_cost_fwd": "piiiiiiiifpps",
     "tw_jeanie_cost_bwd": "ppppiiiiiiiifps",
     "tw_jeanie_feat_fwd": "ppiiiiiiiifippps",
@@ -135,7 +135,17 @@ def call(base, dtype, *args):
 
 
 def udtw_workspace_elems(B, N, M, D):
+    if D <= 1:
+        return 0
     return library().tw_udtw_feat_workspace_bytes(B, N, M, D, 1)
+
+
+def per_pair(*grads):
+    """Per-pair gradient tensors [B] and their common element stride: a stride-0
+    expansion (a mean's backward) is passed as is, anything else contiguous."""
+    if all(g.dim() == 1 and g.stride(0) == 0 for g in grads):
+        return grads, 0
+    return tuple(g.contiguous() for g in grads), 1
 
 
 def check_backend(backend):

@@ -73,7 +73,15 @@ struct UdtwArgs {
   T beta_ln2;    // beta ln 2
   T eps;
   T band;        // <= 0: no band
+  int sigma;     // VX / VY hold standard deviations: variances are their squares
+  int gstride;   // element stride of gr / gp (0: one value for every pair)
 };
+
+// Half of a variance input: 0.5 v, or 0.5 v^2 when the input is a standard deviation.
+template <typename T>
+__device__ __forceinline__ T half_var(const UdtwArgs<T>& a, T v) {
+  return (T)0.5 * (a.sigma ? v * v : v);
+}
 
 // ------------------------------------------------------------- pipeline
 //
@@ -192,7 +200,7 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwA
   __syncthreads();
   // record used on step 0 by wavefront 0: border row on diagonal -1, column 0 entering
   if (wave == 0) {
-    const T y0 = col_y(0), hy0 = (T)0.5 * col_vy(0);
+    const T y0 = col_y(0), hy0 = half_var(a, col_vy(0));
     if (lane == 63) inbox[1] = {INF, (T)0, y0, hy0};
   }
   __syncthreads();
@@ -204,7 +212,7 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwA
   for (int k = 0; k < ROWS; ++k) {
     const int i = row0 + k;
     xr[k] = (SRC == SRC_FEAT1 && i < N) ? a.X[(size_t)b * N + i] : (T)0;
-    hxr[k] = (COLS && i < N) ? (T)0.5 * a.VX[(size_t)b * N + i] : (T)0.5;
+    hxr[k] = (COLS && i < N) ? half_var(a, a.VX[(size_t)b * N + i]) : (T)0.5;
     r1[k] = r2[k] = INF;
     p1[k] = p2[k] = (T)0;
     yc[k] = (T)0;
@@ -261,7 +269,7 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwA
       if (SRC != SRC_FEAT1) fetch(d + PF, rc[u % PF], rq[u % PF]);
 
       // wavefront 0 stores the border record of diagonal d (column d+1 enters next)
-      if (wave == 0) my_self[(u + 2) & 3] = {INF, (T)0, ey_ring[u], (T)0.5 * evy_ring[u]};
+      if (wave == 0) my_self[(u + 2) & 3] = {INF, (T)0, ey_ring[u], half_var(a, evy_ring[u])};
       if (COLS) {
         ey_ring[u] = col_y(d + 1 + kSlots);
         evy_ring[u] = col_vy(d + 1 + kSlots);
@@ -413,7 +421,7 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
   // record used on step 0 by the last wavefront: virtual row N on diagonal
   // Dn, with column M-1 entering row N-1
   if (last_wave && COLS) {
-    const T yl = col_y(M - 1), hyl = (T)0.5 * col_vy(M - 1);
+    const T yl = col_y(M - 1), hyl = half_var(a, col_vy(M - 1));
     if (lane == 0) inbox[1].b = {yl, hyl, (T)0, (T)0};
   }
   __syncthreads();
@@ -427,7 +435,7 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
     const int i = row0 + k;
     const bool in = i >= 0 && i < N;
     xr[k] = (SRC == SRC_FEAT1 && in) ? a.X[(size_t)b * N + i] : (T)0;
-    hxr[k] = (COLS && in) ? (T)0.5 * a.VX[(size_t)b * N + i] : (T)0.5;
+    hxr[k] = (COLS && in) ? half_var(a, a.VX[(size_t)b * N + i]) : (T)0.5;
     dxr[k] = dvr[k] = (T)0;
     e1[k] = e2[k] = -INF;
     g1[k] = g2[k] = h1[k] = h2[k] = a1[k] = a2[k] = (T)0;
@@ -446,9 +454,9 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
   if (last_wave && lane == 63) {
     const int so = (int)(NM - 1) * ES;
     ne1 = bR.ld<T>(0, so);
-    ng1 = a.gr[b];
+    ng1 = a.gr[(size_t)b * a.gstride];
     if (PEN) {
-      nh1 = a.gp[b];
+      nh1 = a.gp[(size_t)b * a.gstride];
       na1 = bP.ld<T>(0, so);
     }
   }
@@ -504,7 +512,7 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
 
       // the last wavefront stores the virtual row N of diagonal d
       if (COLS) {
-        if (last_wave) my_self[(u + 2) & 3].b = {ey_ring[u], (T)0.5 * evy_ring[u], (T)0, (T)0};
+        if (last_wave) my_self[(u + 2) & 3].b = {ey_ring[u], half_var(a, evy_ring[u]), (T)0, (T)0};
         ey_ring[u] = col_y(d - kSlots - N);
         evy_ring[u] = col_vy(d - kSlots - N);
       }
@@ -782,8 +790,8 @@ static int cost_fwd(const T* C, const T* Q, int B, int N, int M, double gamma, d
 
 template <typename T>
 static int cost_bwd(const T* C, const T* Q, const T* R, const T* P, const T* gr, const T* gp,
-                    int B, int N, int M, double gamma, double band, T* dC, T* dQ, hipStream_t s,
-                    const char* what) {
+                    int B, int N, int M, double gamma, double band, int gstride, T* dC, T* dQ,
+                    hipStream_t s, const char* what) {
   if (int e = check_dims(what, B, N, M, gamma)) return e;
   if (!C || !R || !gr || !dC) return fail(TW_EINVAL, "%s: null pointer", what);
   const bool pen = Q != nullptr;
@@ -799,6 +807,8 @@ static int cost_bwd(const T* C, const T* Q, const T* R, const T* P, const T* gr,
   a.dQ = pen ? dQ : nullptr;
   a.N = N;
   a.M = M;
+  if (gstride != 0 && gstride != 1) return fail(TW_EINVAL, "%s: grad_stride must be 0 or 1", what);
+  a.gstride = gstride;
   set_hyper(a, gamma, 0.0, 1.0, band);
   return launch_pen<T, SRC_COST>(pen, true, a, B, s, what);
 }
@@ -812,7 +822,7 @@ template <typename T>
 int udtw_cost_bwd_any(const T* C, const T* Q, const T* R, const T* P, const T* gr, const T* gp,
                       int B, int N, int M, double gamma, T* dC, T* dQ, hipStream_t s,
                       const char* what) {
-  return cost_bwd<T>(C, Q, R, P, gr, gp, B, N, M, gamma, 0.0, dC, dQ, s, what);
+  return cost_bwd<T>(C, Q, R, P, gr, gp, B, N, M, gamma, 0.0, 1, dC, dQ, s, what);
 }
 template int udtw_cost_fwd_any<float>(const float*, const float*, int, int, int, double, double,
                                       float*, float*, float*, float*, hipStream_t, const char*);
@@ -850,18 +860,18 @@ int tw_udtw_cost_fwd_f64(const double* cost, const double* pen, int B, int N, in
 
 int tw_udtw_cost_bwd_f32(const float* cost, const float* pen, const float* R, const float* P,
                          const float* grad_dist, const float* grad_pen, int B, int N, int M,
-                         float gamma, float bandwidth, float* d_cost, float* d_pen,
-                         hipStream_t stream) {
-  return cost_bwd<float>(cost, pen, R, P, grad_dist, grad_pen, B, N, M, gamma, bandwidth, d_cost,
-                         d_pen, stream, "tw_udtw_cost_bwd_f32");
+                         float gamma, float bandwidth, int grad_stride, float* d_cost,
+                         float* d_pen, hipStream_t stream) {
+  return cost_bwd<float>(cost, pen, R, P, grad_dist, grad_pen, B, N, M, gamma, bandwidth,
+                         grad_stride, d_cost, d_pen, stream, "tw_udtw_cost_bwd_f32");
 }
 
 int tw_udtw_cost_bwd_f64(const double* cost, const double* pen, const double* R,
                          const double* P, const double* grad_dist, const double* grad_pen, int B,
-                         int N, int M, double gamma, double bandwidth, double* d_cost,
-                         double* d_pen, hipStream_t stream) {
+                         int N, int M, double gamma, double bandwidth, int grad_stride,
+                         double* d_cost, double* d_pen, hipStream_t stream) {
   return cost_bwd<double>(cost, pen, R, P, grad_dist, grad_pen, B, N, M, gamma, bandwidth,
-                          d_cost, d_pen, stream, "tw_udtw_cost_bwd_f64");
+                          grad_stride, d_cost, d_pen, stream, "tw_udtw_cost_bwd_f64");
 }
 
 }  // extern "C"
@@ -878,8 +888,9 @@ int sqdist_raw_bwd(const T* X, const T* Y, const T* dS, int P, int R, int C, int
 
 template <typename T>
 static int feat_fwd(const T* X, const T* Y, const T* vx, const T* vy, int B, int N, int M, int D,
-                    double gamma, double beta, double eps, double band, T* R, T* P, T* out_r,
-                    T* out_p, T* ws, size_t ws_bytes, hipStream_t s, const char* what) {
+                    double gamma, double beta, double eps, double band, int sigma, T* R, T* P,
+                    T* out_r, T* out_p, T* ws, size_t ws_bytes, hipStream_t s,
+                    const char* what) {
   if (int e = check_dims(what, B, N, M, gamma)) return e;
   if (D <= 0) return fail(TW_EINVAL, "%s: D must be > 0", what);
   if (!X || !Y || !vx || !vy || !R || !out_r || !out_p)
@@ -895,6 +906,7 @@ static int feat_fwd(const T* X, const T* Y, const T* vx, const T* vy, int B, int
   a.out_p = out_p;
   a.N = N;
   a.M = M;
+  a.sigma = sigma != 0;
   set_hyper(a, gamma, beta, eps, band);
   if (D == 1) {
     a.X = X;
@@ -909,11 +921,32 @@ static int feat_fwd(const T* X, const T* Y, const T* vx, const T* vy, int B, int
   return launch_pen<T, SRC_SQ>(pen, false, a, B, s, what);
 }
 
+// d sigma = 2 sigma d var, in place over the variance gradients of both sides
+template <typename T>
+__global__ void __launch_bounds__(256) sigma_grad_kernel(const T* __restrict__ sx,
+                                                         const T* __restrict__ sy, T* dsx, T* dsy,
+                                                         long long nx, long long ny) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < nx)
+    dsx[i] *= (T)2 * sx[i];
+  else if (i < nx + ny)
+    dsy[i - nx] *= (T)2 * sy[i - nx];
+}
+
+template <typename T>
+static int sigma_grads(const T* sx, const T* sy, T* dsx, T* dsy, long long nx, long long ny,
+                       hipStream_t s, const char* what) {
+  const long long n = nx + ny;
+  hipLaunchKernelGGL((sigma_grad_kernel<T>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                     sx, sy, dsx, dsy, nx, ny);
+  return check_launch(what);
+}
+
 template <typename T>
 static int feat_bwd(const T* X, const T* Y, const T* vx, const T* vy, const T* R, const T* P,
                     const T* gr, const T* gp, int B, int N, int M, int D, double gamma,
-                    double beta, double eps, double band, T* dX, T* dY, T* dvx, T* dvy, T* ws,
-                    size_t ws_bytes, hipStream_t s, const char* what) {
+                    double beta, double eps, double band, int sigma, int gstride, T* dX, T* dY,
+                    T* dvx, T* dvy, T* ws, size_t ws_bytes, hipStream_t s, const char* what) {
   if (int e = check_dims(what, B, N, M, gamma)) return e;
   if (D <= 0) return fail(TW_EINVAL, "%s: D must be > 0", what);
   if (!X || !Y || !vx || !vy || !R || !gr || !dX || !dY)
@@ -933,13 +966,19 @@ static int feat_bwd(const T* X, const T* Y, const T* vx, const T* vy, const T* R
   a.dVY = dvy;
   a.N = N;
   a.M = M;
+  if (gstride != 0 && gstride != 1) return fail(TW_EINVAL, "%s: grad_stride must be 0 or 1", what);
+  a.gstride = gstride;
+  a.sigma = sigma != 0;
   set_hyper(a, gamma, beta, eps, band);
+  const bool sig_grads = sigma && dvx != nullptr;
   if (D == 1) {
     a.X = X;
     a.Y = Y;
     a.dX = dX;
     a.dY = dY;
-    return launch_pen<T, SRC_FEAT1>(pen, true, a, B, s, what);
+    if (int e = launch_pen<T, SRC_FEAT1>(pen, true, a, B, s, what)) return e;
+    return sig_grads ? sigma_grads<T>(vx, vy, dvx, dvy, (long long)B * N, (long long)B * M, s, what)
+                     : TW_OK;
   }
   const size_t need = (size_t)B * N * M * sizeof(T);
   if (!ws || ws_bytes < need)
@@ -950,7 +989,9 @@ static int feat_bwd(const T* X, const T* Y, const T* vx, const T* vy, const T* R
   a.C = ws;
   a.dC = ws;
   if (int e = launch_pen<T, SRC_SQ>(pen, true, a, B, s, what)) return e;
-  return sqdist_raw_bwd<T>(X, Y, ws, B, N, M, D, dX, dY, s, what);
+  if (int e = sqdist_raw_bwd<T>(X, Y, ws, B, N, M, D, dX, dY, s, what)) return e;
+  return sig_grads ? sigma_grads<T>(vx, vy, dvx, dvy, (long long)B * N, (long long)B * M, s, what)
+                   : TW_OK;
 }
 
 }  // namespace tw
@@ -964,41 +1005,44 @@ size_t tw_udtw_feat_workspace_bytes(int B, int N, int M, int D, int elem_size) {
 
 int tw_udtw_feat_fwd_f32(const float* X, const float* Y, const float* vx, const float* vy, int B,
                          int N, int M, int D, float gamma, float beta, float eps,
-                         float bandwidth, float* R, float* P, float* out_dist, float* out_pen,
-                         float* workspace, size_t workspace_bytes, hipStream_t stream) {
-  return feat_fwd<float>(X, Y, vx, vy, B, N, M, D, gamma, beta, eps, bandwidth, R, P, out_dist,
-                         out_pen, workspace, workspace_bytes, stream, "tw_udtw_feat_fwd_f32");
+                         float bandwidth, int sigma, float* R, float* P, float* out_dist,
+                         float* out_pen, float* workspace, size_t workspace_bytes,
+                         hipStream_t stream) {
+  return feat_fwd<float>(X, Y, vx, vy, B, N, M, D, gamma, beta, eps, bandwidth, sigma, R, P,
+                         out_dist, out_pen, workspace, workspace_bytes, stream,
+                         "tw_udtw_feat_fwd_f32");
 }
 
 int tw_udtw_feat_fwd_f64(const double* X, const double* Y, const double* vx, const double* vy,
                          int B, int N, int M, int D, double gamma, double beta, double eps,
-                         double bandwidth, double* R, double* P, double* out_dist,
+                         double bandwidth, int sigma, double* R, double* P, double* out_dist,
                          double* out_pen, double* workspace, size_t workspace_bytes,
                          hipStream_t stream) {
-  return feat_fwd<double>(X, Y, vx, vy, B, N, M, D, gamma, beta, eps, bandwidth, R, P, out_dist,
-                          out_pen, workspace, workspace_bytes, stream, "tw_udtw_feat_fwd_f64");
+  return feat_fwd<double>(X, Y, vx, vy, B, N, M, D, gamma, beta, eps, bandwidth, sigma, R, P,
+                          out_dist, out_pen, workspace, workspace_bytes, stream,
+                          "tw_udtw_feat_fwd_f64");
 }
 
 int tw_udtw_feat_bwd_f32(const float* X, const float* Y, const float* vx, const float* vy,
                          const float* R, const float* P, const float* grad_dist,
                          const float* grad_pen, int B, int N, int M, int D, float gamma,
-                         float beta, float eps, float bandwidth, float* dX, float* dY,
-                         float* dvx, float* dvy, float* workspace, size_t workspace_bytes,
-                         hipStream_t stream) {
+                         float beta, float eps, float bandwidth, int sigma, int grad_stride,
+                         float* dX, float* dY, float* dvx, float* dvy, float* workspace,
+                         size_t workspace_bytes, hipStream_t stream) {
   return feat_bwd<float>(X, Y, vx, vy, R, P, grad_dist, grad_pen, B, N, M, D, gamma, beta, eps,
-                         bandwidth, dX, dY, dvx, dvy, workspace, workspace_bytes, stream,
-                         "tw_udtw_feat_bwd_f32");
+                         bandwidth, sigma, grad_stride, dX, dY, dvx, dvy, workspace,
+                         workspace_bytes, stream, "tw_udtw_feat_bwd_f32");
 }
 
 int tw_udtw_feat_bwd_f64(const double* X, const double* Y, const double* vx, const double* vy,
                          const double* R, const double* P, const double* grad_dist,
                          const double* grad_pen, int B, int N, int M, int D, double gamma,
-                         double beta, double eps, double bandwidth, double* dX, double* dY,
-                         double* dvx, double* dvy, double* workspace, size_t workspace_bytes,
-                         hipStream_t stream) {
+                         double beta, double eps, double bandwidth, int sigma, int grad_stride,
+                         double* dX, double* dY, double* dvx, double* dvy, double* workspace,
+                         size_t workspace_bytes, hipStream_t stream) {
   return feat_bwd<double>(X, Y, vx, vy, R, P, grad_dist, grad_pen, B, N, M, D, gamma, beta, eps,
-                          bandwidth, dX, dY, dvx, dvy, workspace, workspace_bytes, stream,
-                          "tw_udtw_feat_bwd_f64");
+                          bandwidth, sigma, grad_stride, dX, dY, dvx, dvy, workspace,
+                          workspace_bytes, stream, "tw_udtw_feat_bwd_f64");
 }
 
 }  // extern "C"

@@ -65,9 +65,10 @@ def dp_backward(cost: Tensor, penalty: Tensor, R: Tensor, P: Tensor, grad_r: Ten
     q = penalty.to(c.dtype).contiguous() if pen else None
     d_cost = torch.empty_like(c)
     d_pen = torch.empty_like(c) if pen else c.new_empty(0)
-    _hip.call("tw_udtw_cost_bwd", c.dtype, c, q, R, P, grad_r.to(c.dtype).contiguous(),
-              grad_p.to(c.dtype).contiguous() if pen else None, B, N, M, gamma, bandwidth, d_cost,
-              d_pen)
+    grads, gs = _hip.per_pair(*((grad_r.to(c.dtype), grad_p.to(c.dtype)) if pen
+                                else (grad_r.to(c.dtype),)))
+    _hip.call("tw_udtw_cost_bwd", c.dtype, c, q, R, P, grads[0], grads[1] if pen else None,
+              B, N, M, gamma, bandwidth, gs, d_cost, d_pen)
     return d_cost, d_pen
 
 
@@ -92,7 +93,9 @@ def _feat_ws(X, N, M):
 
 @torch.library.custom_op("twamd_udtw::fused", mutates_args=())
 def fused(X: Tensor, Y: Tensor, vx: Tensor, vy: Tensor, gamma: float, beta: float, eps: float,
-          bandwidth: float, backend: str) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+          bandwidth: float, backend: str, sigma: bool) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+    """vx, vy: variances [B,N] / [B,M], or with ``sigma`` the standard deviations
+    (any shape holding B*N / B*M values), squared inside the kernel."""
     _hip.require(X, backend, "uDTW")
     B, N, D = X.shape
     M = Y.shape[1]
@@ -104,12 +107,13 @@ def fused(X: Tensor, Y: Tensor, vx: Tensor, vy: Tensor, gamma: float, beta: floa
     out_r, out_p = X.new_empty(B), X.new_empty(B)
     ws = _feat_ws(X, N, M)
     _hip.call("tw_udtw_feat_fwd", X.dtype, X, Y, vx, vy, B, N, M, D, gamma, beta, eps, bandwidth,
-              R, P, out_r, out_p, ws, 0 if ws is None else ws.numel() * ws.element_size())
+              int(sigma), R, P, out_r, out_p, ws,
+              0 if ws is None else ws.numel() * ws.element_size())
     return out_r, out_p, R, P
 
 
 @fused.register_fake
-def _(X, Y, vx, vy, gamma, beta, eps, bandwidth, backend):
+def _(X, Y, vx, vy, gamma, beta, eps, bandwidth, backend, sigma):
     B, N, M = X.shape[0], X.shape[1], Y.shape[1]
     P = X.new_empty(B, N * M) if beta != 0.0 else X.new_empty(0)
     return X.new_empty(B), X.new_empty(B), X.new_empty(B, N * M), P
@@ -118,7 +122,8 @@ def _(X, Y, vx, vy, gamma, beta, eps, bandwidth, backend):
 @torch.library.custom_op("twamd_udtw::fused_backward", mutates_args=())
 def fused_backward(X: Tensor, Y: Tensor, vx: Tensor, vy: Tensor, R: Tensor, P: Tensor,
                    grad_r: Tensor, grad_p: Tensor, gamma: float, beta: float, eps: float,
-                   bandwidth: float, backend: str) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+                   bandwidth: float, backend: str,
+                   sigma: bool) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
     _hip.require(X, backend, "uDTW")
     B, N, D = X.shape
     M = Y.shape[1]
@@ -128,15 +133,16 @@ def fused_backward(X: Tensor, Y: Tensor, vx: Tensor, vy: Tensor, R: Tensor, P: T
     dX, dY = torch.empty_like(X), torch.empty_like(Y)
     dvx, dvy = torch.empty_like(vx), torch.empty_like(vy)
     ws = _feat_ws(X, N, M)
-    _hip.call("tw_udtw_feat_bwd", X.dtype, X, Y, vx, vy, R, P if pen else None,
-              grad_r.to(X.dtype).contiguous(), grad_p.to(X.dtype).contiguous() if pen else None,
-              B, N, M, D, gamma, beta, eps, bandwidth, dX, dY, dvx, dvy, ws,
-              0 if ws is None else ws.numel() * ws.element_size())
+    grads, gs = _hip.per_pair(*((grad_r.to(X.dtype), grad_p.to(X.dtype)) if pen
+                                else (grad_r.to(X.dtype),)))
+    _hip.call("tw_udtw_feat_bwd", X.dtype, X, Y, vx, vy, R, P if pen else None, grads[0],
+              grads[1] if pen else None, B, N, M, D, gamma, beta, eps, bandwidth, int(sigma), gs,
+              dX, dY, dvx, dvy, ws, 0 if ws is None else ws.numel() * ws.element_size())
     return dX, dY, dvx, dvy
 
 
 @fused_backward.register_fake
-def _(X, Y, vx, vy, R, P, grad_r, grad_p, gamma, beta, eps, bandwidth, backend):
+def _(X, Y, vx, vy, R, P, grad_r, grad_p, gamma, beta, eps, bandwidth, backend, sigma):
     return torch.empty_like(X), torch.empty_like(Y), torch.empty_like(vx), torch.empty_like(vy)
 
 
@@ -246,39 +252,47 @@ class DPBackward(torch.autograd.Function):
         return out[0], (out[1] if penalty.numel() else penalty.new_empty(0))
 
 
+def _variance(v, seq, sigma):
+    """Variances [B, L] of the autograd-native path from a fused-op input."""
+    v = v.reshape(seq.shape[0], seq.shape[1])
+    return v * v if sigma else v
+
+
 class Fused(torch.autograd.Function):
     """(X, Y, vx, vy) -> (distance, penalty_sum, R, P); R, P internal."""
 
     generate_vmap_rule = True
 
     @staticmethod
-    def forward(X, Y, vx, vy, gamma, beta, eps, bandwidth, backend):
-        return _fused_direct(X, Y, vx, vy, gamma, beta, eps, bandwidth, backend)
+    def forward(X, Y, vx, vy, gamma, beta, eps, bandwidth, backend, sigma):
+        return _fused_direct(X, Y, vx, vy, gamma, beta, eps, bandwidth, backend, sigma)
 
     @staticmethod
     def setup_context(ctx, inputs, output):
-        X, Y, vx, vy, gamma, beta, eps, bandwidth, backend = inputs
+        X, Y, vx, vy, gamma, beta, eps, bandwidth, backend, sigma = inputs
         ctx.mark_non_differentiable(output[2], output[3])
         ctx.set_materialize_grads(False)
         ctx.save_for_backward(X, Y, vx, vy, output[2], output[3])
         ctx.save_for_forward(X, Y, vx, vy)
-        ctx.args = (gamma, beta, eps, bandwidth, backend)
+        ctx.args = (gamma, beta, eps, bandwidth, backend, sigma)
 
     @staticmethod
     def _f(ctx):
-        gamma, beta, eps, bandwidth, _ = ctx.args
-        return lambda x, y, a, b: _autograd.udtw_features(x, y, a, b, gamma, beta, eps, bandwidth)
+        gamma, beta, eps, bandwidth, _, sigma = ctx.args
+        return lambda x, y, a, b: _autograd.udtw_features(x, y, _variance(a, x, sigma),
+                                                          _variance(b, y, sigma), gamma, beta,
+                                                          eps, bandwidth)
 
     @staticmethod
     def backward(ctx, g_r, g_p, _g_R, _g_P):
         X, Y, vx, vy, R, P = ctx.saved_tensors
-        gamma, beta, eps, bandwidth, backend = ctx.args
+        gamma, beta, eps, bandwidth, backend, sigma = ctx.args
         B = X.shape[0]
         g_r = X.new_zeros(B) if g_r is None else g_r
         g_p = X.new_zeros(B) if g_p is None else g_p
         grads = fused_backward_apply(X, Y, vx, vy, R, P, g_r, g_p, gamma, beta, eps, bandwidth,
-                                     backend)
-        return (*grads, None, None, None, None, None)
+                                     backend, sigma)
+        return (*grads, None, None, None, None, None, None)
 
     @staticmethod
     def jvp(ctx, t_X, t_Y, t_vx, t_vy, *_):
@@ -294,22 +308,24 @@ class FusedBackward(torch.autograd.Function):
     generate_vmap_rule = True
 
     @staticmethod
-    def forward(X, Y, vx, vy, R, P, g_r, g_p, gamma, beta, eps, bandwidth, backend):
+    def forward(X, Y, vx, vy, R, P, g_r, g_p, gamma, beta, eps, bandwidth, backend, sigma):
         return _fused_backward_direct(X, Y, vx, vy, R, P, g_r, g_p, gamma, beta, eps, bandwidth,
-                                      backend)
+                                      backend, sigma)
 
     @staticmethod
     def setup_context(ctx, inputs, output):
-        X, Y, vx, vy, R, P, g_r, g_p, gamma, beta, eps, bandwidth, backend = inputs
+        X, Y, vx, vy, R, P, g_r, g_p, gamma, beta, eps, bandwidth, backend, sigma = inputs
         ctx.save_for_backward(X, Y, vx, vy, g_r, g_p)
         ctx.save_for_forward(X, Y, vx, vy, g_r, g_p)
-        ctx.args = (gamma, beta, eps, bandwidth)
+        ctx.args = (gamma, beta, eps, bandwidth, sigma)
 
     @staticmethod
     def _first(ctx):
-        gamma, beta, eps, bandwidth = ctx.args
+        gamma, beta, eps, bandwidth, sigma = ctx.args
         return _first_order(
-            lambda x, y, a, b: _autograd.udtw_features(x, y, a, b, gamma, beta, eps, bandwidth), 4)
+            lambda x, y, a, b: _autograd.udtw_features(x, y, _variance(a, x, sigma),
+                                                       _variance(b, y, sigma), gamma, beta, eps,
+                                                       bandwidth), 4)
 
     @staticmethod
     def backward(ctx, gg_X, gg_Y, gg_vx, gg_vy):
@@ -317,7 +333,7 @@ class FusedBackward(torch.autograd.Function):
         cot = tuple(zeros_if_none(g, p) for g, p in zip((gg_X, gg_Y, gg_vx, gg_vy), (X, Y, vx, vy)))
         d = vjp_of(FusedBackward._first(ctx), (X, Y, vx, vy, g_r, g_p), cot)
         return (d[0], d[1], d[2], d[3], None, None, d[4], d[5],
-                None, None, None, None, None)
+                None, None, None, None, None, None)
 
     @staticmethod
     def jvp(ctx, t_X, t_Y, t_vx, t_vy, _t_R, _t_P, t_gr, t_gp, *_):

@@ -134,11 +134,13 @@ def _udtw_fused(X, Y, sigma_x, sigma_y, beta, gamma, bandwidth, eps, backend):
     if Y is X:
         # d(X, X): torch.compile cannot trace a Function receiving one tensor twice
         Y = X.view_as(X)
-    vx = sigma_x.squeeze(-1).to(dtype).pow(2)
-    vy = sigma_y.squeeze(-1).to(dtype).pow(2)
+    # the kernels square the standard deviations themselves (and return d sigma)
+    sx, sy = sigma_x.to(dtype), sigma_y.to(dtype)
+    if sy is sx:
+        sy = sx.view_as(sx)
     band = 0.0 if bandwidth is None else float(bandwidth)
-    distance, pen, _, _ = _ops.fused_apply(X, Y, vx, vy, float(gamma), float(beta), float(eps),
-                                           band, backend)
+    distance, pen, _, _ = _ops.fused_apply(X, Y, sx, sy, float(gamma), float(beta), float(eps),
+                                           band, backend, True)
     _check_band_reached(distance, band)
     return UDTWOutput(distance, pen)
 
