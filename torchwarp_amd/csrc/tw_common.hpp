@@ -123,6 +123,28 @@ __device__ __forceinline__ double shift_prev<double>(double v, double edge) {
   int hi = dpp_prev_i((int)(b >> 32), (int)(e >> 32));
   return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
+// A wave-uniform value, taken from the first active lane (into a scalar register).
+__device__ __forceinline__ float uniform(float v) {
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+__device__ __forceinline__ double uniform(double v) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readfirstlane((int)b);
+  const int hi = __builtin_amdgcn_readfirstlane((int)(b >> 32));
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+// lane l takes lane l-1's value; lane 0 takes 0 (DPP bound_ctrl zero fill)
+__device__ __forceinline__ float shift_prev0(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x138, 0xf, 0xf, true));
+}
+__device__ __forceinline__ double shift_prev0(double v) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)b, 0x138, 0xf, 0xf, true);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), 0x138, 0xf, 0xf, true);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
 template <typename T>
 __device__ __forceinline__ T shift_next(T v, T edge);
 template <>
@@ -134,6 +156,17 @@ __device__ __forceinline__ double shift_next<double>(double v, double edge) {
   long long b = __double_as_longlong(v), e = __double_as_longlong(edge);
   int lo = dpp_next_i((int)b, (int)e);
   int hi = dpp_next_i((int)(b >> 32), (int)(e >> 32));
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+// lane l takes lane l+1's value; lane 63 takes 0 (DPP bound_ctrl zero fill)
+__device__ __forceinline__ float shift_next0(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x130, 0xf, 0xf, true));
+}
+__device__ __forceinline__ double shift_next0(double v) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)b, 0x130, 0xf, 0xf, true);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), 0x130, 0xf, 0xf, true);
   return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
 }
 

@@ -35,6 +35,7 @@
 // (bitwise deterministic).
 
 #include <limits.h>
+#include <type_traits>
 #include <stdlib.h>
 
 #include "tw_capi.hpp"
@@ -74,13 +75,15 @@ struct UdtwArgs {
   T eps;
   T band;        // <= 0: no band
   int sigma;     // VX / VY hold standard deviations: variances are their squares
+  T hv1, hv0;    // half variance of an input v: v (hv1 v + hv0)
   int gstride;   // element stride of gr / gp (0: one value for every pair)
 };
 
-// Half of a variance input: 0.5 v, or 0.5 v^2 when the input is a standard deviation.
+// Half of a variance input: 0.5 v, or 0.5 v^2 when the input is a standard
+// deviation, as v (hv1 v + hv0) with (hv1, hv0) = (0, 0.5) or (0.5, 0).
 template <typename T>
 __device__ __forceinline__ T half_var(const UdtwArgs<T>& a, T v) {
-  return (T)0.5 * (a.sigma ? v * v : v);
+  return v * (a.hv1 * v + a.hv0);
 }
 
 // ------------------------------------------------------------- pipeline
@@ -184,25 +187,15 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwA
   if (SRC == SRC_COST && PEN) bQ.init(a.Q + b * NM, NM);
   if (SRC == SRC_FEAT1) bY.init(a.Y + (size_t)b * M, M);
   if (COLS) bVY.init(a.VY + (size_t)b * M, M);
-  // column j's y and variance (wave-uniform loads; j is clamped into the sequence)
-  auto col_y = [&](int j) -> T {
-    return SRC == SRC_FEAT1 ? bY.ld<T>(0, smin(smax(j, 0), M - 1) * ES) : (T)0;
-  };
-  auto col_vy = [&](int j) -> T {
-    return COLS ? bVY.ld<T>(0, smin(smax(j, 0), M - 1) * ES) : (T)1;
-  };
+  // column operands of the edge wavefront: loads at byte offset vcol (lane
+  // uniform); columns past the end fail the range check and read 0
+  auto col_y = [&](int vcol) -> T { return SRC == SRC_FEAT1 ? bY.ld<T>(vcol, 0) : (T)0; };
+  auto col_vy = [&](int vcol) -> T { return COLS ? bVY.ld<T>(vcol, 0) : (T)1; };
 
   Rec4<T>* const inbox = box + wave * kSlots;
   Rec4<T>* const outbox = box + (wave + 1) * kSlots;
   // the mailbox store of a step: lane 63 to the slot, the others to the dump
   Rec4<T>* const my_out = lane == 63 ? outbox : dump + lane;
-  Rec4<T>* const my_self = lane == 63 ? inbox : dump + lane;
-  __syncthreads();
-  // record used on step 0 by wavefront 0: border row on diagonal -1, column 0 entering
-  if (wave == 0) {
-    const T y0 = col_y(0), hy0 = half_var(a, col_vy(0));
-    if (lane == 63) inbox[1] = {INF, (T)0, y0, hy0};
-  }
   __syncthreads();
 
   const int row0 = tid * ROWS;
@@ -225,16 +218,6 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwA
 
   const int d_first = -kLag * wave;
   const int steps = (Dn + kLag * (nw - 1) + kSlots - 1) / kSlots * kSlots;
-  Rec4<T> nxt = inbox[1];
-  // column entering row 0 on the diagonal after step u's, loaded kSlots
-  // steps ahead by every wavefront (wavefront 0 uses them): no divergent
-  // loads, so the ring stays in place and its wait lands at the use
-  T ey_ring[kSlots], evy_ring[kSlots];
-#pragma unroll
-  for (int u = 0; u < kSlots; ++u) {
-    ey_ring[u] = col_y(u + 1);
-    evy_ring[u] = col_vy(u + 1);
-  }
 
   T rc[PF][ROWS], rq[PF][ROWS];
   auto fetch = [&](int d, T* c, T* q) {
@@ -251,104 +234,141 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwA
     for (int u = 0; u < PF; ++u) fetch(d_first + u, rc[u], rq[u]);
   }
 
-  int soff = 0;  // soff of diagonal d, in elements
-  // Drain the set-up loads here: the compiler derives each in-loop wait on a
-  // ring register from every path into the loop, and the entry path would
-  // otherwise force a near-full vmcnt wait on every trip.
-  __builtin_amdgcn_s_waitcnt(0);
-  for (int t0 = 0; t0 < steps; t0 += kSlots) {
+  // The sweep, instantiated for the edge wavefront (0: its row above is the
+  // border, its entering column comes from a register ring of column loads)
+  // and for the others (row above and columns from the mailbox).
+  auto sweep = [&](auto edge_tag) {
+    constexpr bool EDGE = decltype(edge_tag)::value;
+    T ey_ring[kSlots], evy_ring[kSlots];   // EDGE: column d of ring slot d % kSlots
+    int vcol = 0;                          // EDGE: byte offset of column t0
+    if (EDGE && COLS) {
 #pragma unroll
-    for (int u = 0; u < kSlots; ++u) {
-      const int d = d_first + t0 + u;
-      T cc[ROWS], cq[ROWS];
-#pragma unroll
-      for (int k = 0; k < ROWS; ++k) {
-        cc[k] = rc[u % PF][k];
-        cq[k] = rq[u % PF][k];
+      for (int u = 0; u < kSlots; ++u) {
+        ey_ring[u] = col_y(u * ES);
+        evy_ring[u] = col_vy(u * ES);
       }
-      if (SRC != SRC_FEAT1) fetch(d + PF, rc[u % PF], rq[u % PF]);
-
-      // wavefront 0 stores the border record of diagonal d (column d+1 enters next)
-      if (wave == 0) my_self[(u + 2) & 3] = {INF, (T)0, ey_ring[u], half_var(a, evy_ring[u])};
-      if (COLS) {
-        ey_ring[u] = col_y(d + 1 + kSlots);
-        evy_ring[u] = col_vy(d + 1 + kSlots);
-      }
-      const Rec4<T> e = nxt;
-      nxt = inbox[(u + 2) & 3];
-
-      nr2 = nr1;
-      np2 = np1;
-      nr1 = shift_prev(r1[ROWS - 1], e.x);
-      if (PEN) np1 = shift_prev(p1[ROWS - 1], e.y);
-      if (COLS) {
-        const T ny = SRC == SRC_FEAT1 ? shift_prev(yc[ROWS - 1], e.z) : (T)0;
-        const T nhy = shift_prev(hyc[ROWS - 1], e.w);
-#pragma unroll
-        for (int k = ROWS - 1; k > 0; --k) {
-          yc[k] = yc[k - 1];
-          hyc[k] = hyc[k - 1];
-        }
-        yc[0] = ny;
-        hyc[0] = nhy;
-      }
-
-      const int so = soff * ES;
-      T nr[ROWS], np[ROWS];
-#pragma unroll
-      for (int k = 0; k < ROWS; ++k) {
-        const int j = d + jb[k];
-        const bool valid = (unsigned)j < (unsigned)M;
-        const T up = k ? r1[k - 1] : nr1;
-        const T dg = k ? r2[k - 1] : nr2;
-        const T lf = r1[k];
-        T ch, q = (T)0;
-        if (SRC == SRC_COST) {
-          ch = cc[k] * a.k;
-          if (PEN) q = cq[k];
-        } else {
-          T sq;
-          if (SRC == SRC_FEAT1) {
-            const T df = xr[k] - yc[k];
-            sq = df * df;
-          } else {
-            sq = cc[k] > (T)0 ? cc[k] : (T)0;
-          }
-          const T var = fmax(hxr[k] + hyc[k], a.eps);   // max((vx + vy) / 2, eps)
-          ch = sq * (rcp(var) * a.k);
-          if (PEN) q = a.beta_ln2 * lg2(var);
-        }
-        const T m = min3(dg, up, lf);
-        const T ed = ex2(m - dg), eu = ex2(m - up), el = ex2(m - lf);
-        const T s = ed + eu + el;
-        const T rv = ch + m - lg2(s);
-        bool ok = valid;
-        if (BAND) ok = ok && (m < INF) && (fabs((T)(2 * (row0 + k) - d)) <= a.band);
-        nr[k] = ok ? rv : INF;
-        if (PEN) {
-          const T pup = k ? p1[k - 1] : np1;
-          const T pdg = k ? p2[k - 1] : np2;
-          const T pv = q + (ed * pdg + eu * pup + el * p1[k]) * rcp(s);
-          np[k] = ok ? pv : (T)0;
-        } else {
-          np[k] = (T)0;
-        }
-        const int vo = valid ? vst[k] : kOob;
-        bR.st(nr[k], vo, so);
-        if (PEN) bP.st(np[k], vo, so);
-      }
-#pragma unroll
-      for (int k = 0; k < ROWS; ++k) {
-        r2[k] = r1[k];
-        r1[k] = nr[k];
-        p2[k] = p1[k];
-        p1[k] = np[k];
-      }
-      soff += diag_step(d, N, M);
-      my_out[u] = {r1[ROWS - 1], p1[ROWS - 1], yc[ROWS - 1], hyc[ROWS - 1]};
-      lag_barrier();
     }
-  }
+    Rec4<T> nxt = {INF, (T)0, (T)0, (T)0.5};
+    if (!EDGE) nxt = inbox[1];
+    int soff = 0;  // soff of diagonal d, in elements
+    // Drain the set-up loads here: the compiler derives each in-loop wait on
+    // a ring register from every path into the loop, and the entry path
+    // would otherwise force a near-full vmcnt wait on every trip.
+    __builtin_amdgcn_s_waitcnt(0);
+    for (int t0 = 0; t0 < steps; t0 += kSlots) {
+#pragma unroll
+      for (int u = 0; u < kSlots; ++u) {
+        const int d = d_first + t0 + u;
+        T cc[ROWS], cq[ROWS];
+#pragma unroll
+        for (int k = 0; k < ROWS; ++k) {
+          cc[k] = rc[u % PF][k];
+          cq[k] = rq[u % PF][k];
+        }
+        // the row above the first row on diagonal d-1, and the column
+        // entering the first row on diagonal d
+        Rec4<T> e;
+        if (EDGE)
+          e = {INF, (T)0, ey_ring[u], COLS ? half_var(a, evy_ring[u]) : (T)0.5};
+        else
+          e = nxt;
+
+        nr2 = nr1;
+        np2 = np1;
+        nr1 = shift_prev(r1[ROWS - 1], e.x);
+        if (PEN) np1 = EDGE ? shift_prev0(p1[ROWS - 1]) : shift_prev(p1[ROWS - 1], e.y);
+        if (COLS) {
+          // the edge wavefront's column operands are wave-uniform: passing
+          // them through readfirstlane gives each shift a fresh copy, so the
+          // ring registers are never tied to (and overwritten by) a shift
+          const T ny = SRC != SRC_FEAT1 ? (T)0
+                       : shift_prev(yc[ROWS - 1], EDGE ? uniform(e.z) : e.z);
+          const T nhy = shift_prev(hyc[ROWS - 1], EDGE ? uniform(e.w) : e.w);
+#pragma unroll
+          for (int k = ROWS - 1; k > 0; --k) {
+            yc[k] = yc[k - 1];
+            hyc[k] = hyc[k - 1];
+          }
+          yc[0] = ny;
+          hyc[0] = nhy;
+        }
+
+        const int so = soff * ES;
+        T nr[ROWS], np[ROWS];
+#pragma unroll
+        for (int k = 0; k < ROWS; ++k) {
+          const int j = d + jb[k];
+          const bool valid = (unsigned)j < (unsigned)M;
+          const T up = k ? r1[k - 1] : nr1;
+          const T dg = k ? r2[k - 1] : nr2;
+          const T lf = r1[k];
+          T ch, q = (T)0;
+          if (SRC == SRC_COST) {
+            ch = cc[k] * a.k;
+            if (PEN) q = cq[k];
+          } else {
+            T sq;
+            if (SRC == SRC_FEAT1) {
+              const T df = xr[k] - yc[k];
+              sq = df * df;
+            } else {
+              sq = cc[k] > (T)0 ? cc[k] : (T)0;
+            }
+            const T var = fmax(hxr[k] + hyc[k], a.eps);   // max((vx + vy) / 2, eps)
+            ch = sq * (rcp(var) * a.k);
+            if (PEN) q = a.beta_ln2 * lg2(var);
+          }
+          const T m = min3(dg, up, lf);
+          const T ed = ex2(m - dg), eu = ex2(m - up), el = ex2(m - lf);
+          const T s = ed + eu + el;
+          const T rv = ch + m - lg2(s);
+          bool ok = valid;
+          if (BAND) ok = ok && (m < INF) && (fabs((T)(2 * (row0 + k) - d)) <= a.band);
+          nr[k] = ok ? rv : INF;
+          if (PEN) {
+            const T pup = k ? p1[k - 1] : np1;
+            const T pdg = k ? p2[k - 1] : np2;
+            const T pv = q + (ed * pdg + eu * pup + el * p1[k]) * rcp(s);
+            np[k] = ok ? pv : (T)0;
+          } else {
+            np[k] = (T)0;
+          }
+          const int vo = valid ? vst[k] : kOob;
+          bR.st(nr[k], vo, so);
+          if (PEN) bP.st(np[k], vo, so);
+        }
+#pragma unroll
+        for (int k = 0; k < ROWS; ++k) {
+          r2[k] = r1[k];
+          r1[k] = nr[k];
+          p2[k] = p1[k];
+          p1[k] = np[k];
+        }
+        soff += diag_step(d, N, M);
+        // Read the record for the next step (stored two steps ago, complete
+        // since the last barrier) only now, after this step's shifts: the
+        // scheduling barrier keeps it there, so its destination registers
+        // never collide with the shifts' results.
+        // The ring reloads follow the same rule: issued after the last use
+        // of the slot they refill, so the slot's register is reused in place
+        // and the loop back edge needs no copies (nor the waits they imply).
+        __builtin_amdgcn_sched_barrier(0);
+        if (SRC != SRC_FEAT1) fetch(d + PF, rc[u % PF], rq[u % PF]);
+        if (EDGE && COLS) {
+          ey_ring[u] = col_y(vcol + (u + kSlots) * ES);
+          evy_ring[u] = col_vy(vcol + (u + kSlots) * ES);
+        }
+        if (!EDGE) nxt = inbox[(u + 2) & 3];
+        my_out[u] = {r1[ROWS - 1], p1[ROWS - 1], yc[ROWS - 1], hyc[ROWS - 1]};
+        lag_barrier();
+      }
+      vcol += kSlots * ES;
+    }
+  };
+  if (wave == 0)
+    sweep(std::true_type{});
+  else
+    sweep(std::false_type{});
   // cell (N-1, M-1) is the last element of the diagonal-major R / P; the
   // thread that stored it reads it back
   if (row0 <= N - 1 && N - 1 < row0 + ROWS) {
@@ -405,25 +425,15 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
   }
   if (COLS) bVY.init(a.VY + (size_t)b * M, M);
   if (vgrad) bdVY.init(a.dVY + (size_t)b * M, M);
-  auto col_y = [&](int j) -> T {
-    return SRC == SRC_FEAT1 ? bY.ld<T>(0, smin(smax(j, 0), M - 1) * ES) : (T)0;
-  };
-  auto col_vy = [&](int j) -> T {
-    return COLS ? bVY.ld<T>(0, smin(smax(j, 0), M - 1) * ES) : (T)1;
-  };
+  // column operands of the edge wavefront at byte offset vcol (lane uniform);
+  // columns before the first fail the range check and read 0
+  auto col_y = [&](int vcol) -> T { return SRC == SRC_FEAT1 ? bY.ld<T>(vcol, 0) : (T)0; };
+  auto col_vy = [&](int vcol) -> T { return COLS ? bVY.ld<T>(vcol, 0) : (T)1; };
 
   const bool last_wave = wave == nw - 1;
   Rec8<T>* const inbox = box + (wave + 1) * kSlots;
   Rec8<T>* const outbox = box + wave * kSlots;
   Rec8<T>* const my_out = lane == 0 ? outbox : dump + lane;
-  Rec8<T>* const my_self = lane == 0 ? inbox : dump + lane;
-  __syncthreads();
-  // record used on step 0 by the last wavefront: virtual row N on diagonal
-  // Dn, with column M-1 entering row N-1
-  if (last_wave && COLS) {
-    const T yl = col_y(M - 1), hyl = half_var(a, col_vy(M - 1));
-    if (lane == 0) inbox[1].b = {yl, hyl, (T)0, (T)0};
-  }
   __syncthreads();
 
   T xr[ROWS], hxr[ROWS], dxr[ROWS], dvr[ROWS];
@@ -463,15 +473,6 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
 
   const int d_first = Dn - 1 + kLag * (nw - 1 - wave);
   const int steps = (Dn + kLag * (nw - 1) + kSlots - 1) / kSlots * kSlots;
-  Rec8<T> nx = inbox[1];
-  // column entering row N-1 on the diagonal after step u's, loaded kSlots
-  // steps ahead by every wavefront (the last one uses them)
-  T ey_ring[kSlots], evy_ring[kSlots];
-#pragma unroll
-  for (int u = 0; u < kSlots; ++u) {
-    ey_ring[u] = col_y(d_first - u - N);
-    evy_ring[u] = col_vy(d_first - u - N);
-  }
 
   T rr[PF][ROWS], rp[PF][ROWS], rc[PF][ROWS], rq[PF][ROWS];
   int sfetch = (int)(NM - N);  // soff of the next diagonal to fetch (min(d, Dn-1))
@@ -495,158 +496,190 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
 #pragma unroll
   for (int u = 0; u < PF; ++u) fetch(d_first - u, rr[u], rp[u], rc[u], rq[u]);
 
-  __builtin_amdgcn_s_waitcnt(0);   // drain the set-up loads (as in the forward)
-  for (int t0 = 0; t0 < steps; t0 += kSlots) {
+  // The sweep, instantiated for the edge wavefront (the last: its row below
+  // is the virtual row N, its entering column comes from a register ring of
+  // column loads) and for the others (row below and columns from the mailbox).
+  auto sweep = [&](auto edge_tag) {
+    constexpr bool EDGE = decltype(edge_tag)::value;
+    // EDGE: ring slot u of a trip holds column M-1-t0-u, the one entering row
+    // N-1 on that step's diagonal
+    T ey_ring[kSlots], evy_ring[kSlots];
+    int vcol = (M - 1) * ES;   // EDGE: byte offset of column M-1-t0
+    if (EDGE && COLS) {
 #pragma unroll
-    for (int u = 0; u < kSlots; ++u) {
-      const int d = d_first - t0 - u;
-      T cr[ROWS], cp[ROWS], cc[ROWS], cq[ROWS];
-#pragma unroll
-      for (int k = 0; k < ROWS; ++k) {
-        cr[k] = rr[u % PF][k];
-        cp[k] = rp[u % PF][k];
-        cc[k] = rc[u % PF][k];
-        cq[k] = rq[u % PF][k];
+      for (int u = 0; u < kSlots; ++u) {
+        ey_ring[u] = col_y(vcol - u * ES);
+        evy_ring[u] = col_vy(vcol - u * ES);
       }
-      fetch(d - PF, rr[u % PF], rp[u % PF], rc[u % PF], rq[u % PF]);
-
-      // the last wavefront stores the virtual row N of diagonal d
-      if (COLS) {
-        if (last_wave) my_self[(u + 2) & 3].b = {ey_ring[u], half_var(a, evy_ring[u]), (T)0, (T)0};
-        ey_ring[u] = col_y(d - kSlots - N);
-        evy_ring[u] = col_vy(d - kSlots - N);
-      }
-      const Rec8<T> ex = nx;
-      if (COLS) {
-        nx = inbox[(u + 2) & 3];
-      } else {
-        nx.a = inbox[(u + 2) & 3].a;
-      }
-
-      ne2 = ne1;
-      ng2 = ng1;
-      nh2 = nh1;
-      na2 = na1;
-      ne1 = shift_next(e1[0], ex.a.x);
-      ng1 = shift_next(g1[0], ex.a.y);
-      if (PEN) {
-        nh1 = shift_next(h1[0], ex.a.z);
-        na1 = shift_next(a1[0], ex.a.w);
-      }
-      if (COLS) {
-        const T fy = SRC == SRC_FEAT1 ? shift_next(yc[0], ex.b.x) : (T)0;
-        const T fhy = shift_next(hyc[0], ex.b.y);
-        const T fcy = SRC == SRC_FEAT1 ? shift_next(cy[0], ex.b.z) : (T)0;
-        const T fcvy = vgrad ? shift_next(cvy[0], ex.b.w) : (T)0;
-#pragma unroll
-        for (int k = 0; k + 1 < ROWS; ++k) {
-          yc[k] = yc[k + 1];
-          hyc[k] = hyc[k + 1];
-          cy[k] = cy[k + 1];
-          cvy[k] = cvy[k + 1];
-        }
-        yc[ROWS - 1] = fy;
-        hyc[ROWS - 1] = fhy;
-        cy[ROWS - 1] = fcy;
-        cvy[ROWS - 1] = fcvy;
-      }
-
-      const int so_n = smax(d, 0) * ES;
-      T xe[ROWS], xg[ROWS], xh[ROWS], xa[ROWS];
-#pragma unroll
-      for (int k = 0; k < ROWS; ++k) {
-        const bool valid = (unsigned)(d + jb[k]) < (unsigned)M;
-        const T rk = valid ? cr[k] : INF;
-        const T pk = cp[k];
-        T ch, q = (T)0, c = (T)0, rv = (T)1, sq_raw = (T)0, var_raw = (T)1;
-        if (SRC == SRC_COST) {
-          ch = cc[k] * a.k;
-          if (PEN) q = cq[k];
-        } else {
-          if (SRC == SRC_FEAT1) {
-            const T df = xr[k] - yc[k];
-            sq_raw = df * df;
-          } else {
-            sq_raw = cc[k];
-          }
-          const T sq = sq_raw > (T)0 ? sq_raw : (T)0;
-          var_raw = hxr[k] + hyc[k];
-          const T var = fmax(var_raw, a.eps);
-          rv = rcp(var);
-          c = sq * rv;
-          ch = c * a.k;
-          if (PEN) q = a.beta_ln2 * lg2(var);
-        }
-        // successors: down (i+1, j) and right (i, j+1) on d+1, diagonal (i+1, j+1) on d+2
-        const T edn = (k + 1 < ROWS) ? e1[k + 1] : ne1;
-        const T gdn = (k + 1 < ROWS) ? g1[k + 1] : ng1;
-        const T edg = (k + 1 < ROWS) ? e2[k + 1] : ne2;
-        const T gdg = (k + 1 < ROWS) ? g2[k + 1] : ng2;
-        const T wdn = ex2(edn - rk), wrt = ex2(e1[k] - rk), wdg = ex2(edg - rk);
-        T g = wdn * gdn + wrt * g1[k] + wdg * gdg;
-        T h = (T)0;
-        if (PEN) {
-          const T hdn = (k + 1 < ROWS) ? h1[k + 1] : nh1;
-          const T adn = (k + 1 < ROWS) ? a1[k + 1] : na1;
-          const T hdg = (k + 1 < ROWS) ? h2[k + 1] : nh2;
-          const T adg = (k + 1 < ROWS) ? a2[k + 1] : na2;
-          const T wh_dn = wdn * hdn, wh_rt = wrt * h1[k], wh_dg = wdg * hdg;
-          g -= (wh_dn * (pk - adn) + wh_rt * (pk - a1[k]) + wh_dg * (pk - adg)) * a.inv_gamma;
-          h = wh_dn + wh_rt + wh_dg;
-        }
-        // outside the grid, and (band) at unreachable cells, nothing flows
-        bool live = valid;
-        if (BAND) live = live && rk < INF;
-        g = live ? g : (T)0;
-        h = live ? h : (T)0;
-        xe[k] = live ? rk - ch : -INF;
-        xg[k] = g;
-        xh[k] = h;
-        xa[k] = valid ? pk - q : (T)0;
-
-        const int vn = valid ? vnat[k] : kOob;
-        if (SRC == SRC_COST) {
-          bdC.st(g, vn, so_n);
-          if (want_dq) bdQ.st(h, vn, so_n);
-        } else {
-          const T dsq = sq_raw > (T)0 ? g * rv : (T)0;
-          if (SRC == SRC_SQ) bdC.st(dsq, vn, so_n);
-          if (SRC == SRC_FEAT1) {
-            const T df = valid ? (T)2 * dsq * (xr[k] - yc[k]) : (T)0;
-            dxr[k] += df;
-            cy[k] -= df;
-          }
-          if (vgrad) {
-            T dvar = var_raw > a.eps ? (T)0.5 * (a.beta * h - g * c) * rv : (T)0;
-            dvar = valid ? dvar : (T)0;
-            dvr[k] += dvar;
-            cvy[k] += dvar;
-          }
-          // column d leaves the sweep at row 0: store its sums
-          const int vc = ((unsigned)d < (unsigned)M) ? vrow0[k] : kOob;
-          if (SRC == SRC_FEAT1) bdY.st(cy[k], vc, so_n);
-          if (vgrad) bdVY.st(cvy[k], vc, so_n);
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < ROWS; ++k) {
-        e2[k] = e1[k];
-        e1[k] = xe[k];
-        g2[k] = g1[k];
-        g1[k] = xg[k];
-        h2[k] = h1[k];
-        h1[k] = xh[k];
-        a2[k] = a1[k];
-        a1[k] = xa[k];
-      }
-      if (COLS) {
-        my_out[u] = {{e1[0], g1[0], h1[0], a1[0]}, {yc[0], hyc[0], cy[0], cvy[0]}};
-      } else {
-        my_out[u].a = {e1[0], g1[0], h1[0], a1[0]};
-      }
-      lag_barrier();
     }
-  }
+    Rec8<T> nx = {{-INF, (T)0, (T)0, (T)0}, {(T)0, (T)0.5, (T)0, (T)0}};
+    if (!EDGE) nx = inbox[1];
+    __builtin_amdgcn_s_waitcnt(0);   // drain the set-up loads (as in the forward)
+    for (int t0 = 0; t0 < steps; t0 += kSlots) {
+#pragma unroll
+      for (int u = 0; u < kSlots; ++u) {
+        const int d = d_first - t0 - u;
+        T cr[ROWS], cp[ROWS], cc[ROWS], cq[ROWS];
+  #pragma unroll
+        for (int k = 0; k < ROWS; ++k) {
+          cr[k] = rr[u % PF][k];
+          cp[k] = rp[u % PF][k];
+          cc[k] = rc[u % PF][k];
+          cq[k] = rq[u % PF][k];
+        }
+        // the row below the last row on diagonal d+1, and the column entering
+        // the last row on diagonal d
+        Rec8<T> ex;
+        if (EDGE)
+          ex = {{-INF, (T)0, (T)0, (T)0},
+                {ey_ring[u], COLS ? half_var(a, evy_ring[u]) : (T)0.5, (T)0, (T)0}};
+        else
+          ex = nx;
+
+        ne2 = ne1;
+        ng2 = ng1;
+        nh2 = nh1;
+        na2 = na1;
+        ne1 = shift_next(e1[0], ex.a.x);
+        ng1 = EDGE ? shift_next0(g1[0]) : shift_next(g1[0], ex.a.y);
+        if (PEN) {
+          nh1 = EDGE ? shift_next0(h1[0]) : shift_next(h1[0], ex.a.z);
+          na1 = EDGE ? shift_next0(a1[0]) : shift_next(a1[0], ex.a.w);
+        }
+        if (COLS) {
+          const T fy = SRC != SRC_FEAT1 ? (T)0
+                       : shift_next(yc[0], EDGE ? uniform(ex.b.x) : ex.b.x);
+          const T fhy = shift_next(hyc[0], EDGE ? uniform(ex.b.y) : ex.b.y);
+          const T fcy = SRC != SRC_FEAT1 ? (T)0 : EDGE ? shift_next0(cy[0]) : shift_next(cy[0], ex.b.z);
+          const T fcvy = !vgrad ? (T)0 : EDGE ? shift_next0(cvy[0]) : shift_next(cvy[0], ex.b.w);
+  #pragma unroll
+          for (int k = 0; k + 1 < ROWS; ++k) {
+            yc[k] = yc[k + 1];
+            hyc[k] = hyc[k + 1];
+            cy[k] = cy[k + 1];
+            cvy[k] = cvy[k + 1];
+          }
+          yc[ROWS - 1] = fy;
+          hyc[ROWS - 1] = fhy;
+          cy[ROWS - 1] = fcy;
+          cvy[ROWS - 1] = fcvy;
+        }
+
+        const int so_n = smax(d, 0) * ES;
+        T xe[ROWS], xg[ROWS], xh[ROWS], xa[ROWS];
+  #pragma unroll
+        for (int k = 0; k < ROWS; ++k) {
+          const bool valid = (unsigned)(d + jb[k]) < (unsigned)M;
+          const T rk = valid ? cr[k] : INF;
+          const T pk = cp[k];
+          T ch, q = (T)0, c = (T)0, rv = (T)1, sq_raw = (T)0, var_raw = (T)1;
+          if (SRC == SRC_COST) {
+            ch = cc[k] * a.k;
+            if (PEN) q = cq[k];
+          } else {
+            if (SRC == SRC_FEAT1) {
+              const T df = xr[k] - yc[k];
+              sq_raw = df * df;
+            } else {
+              sq_raw = cc[k];
+            }
+            const T sq = sq_raw > (T)0 ? sq_raw : (T)0;
+            var_raw = hxr[k] + hyc[k];
+            const T var = fmax(var_raw, a.eps);
+            rv = rcp(var);
+            c = sq * rv;
+            ch = c * a.k;
+            if (PEN) q = a.beta_ln2 * lg2(var);
+          }
+          // successors: down (i+1, j) and right (i, j+1) on d+1, diagonal (i+1, j+1) on d+2
+          const T edn = (k + 1 < ROWS) ? e1[k + 1] : ne1;
+          const T gdn = (k + 1 < ROWS) ? g1[k + 1] : ng1;
+          const T edg = (k + 1 < ROWS) ? e2[k + 1] : ne2;
+          const T gdg = (k + 1 < ROWS) ? g2[k + 1] : ng2;
+          const T wdn = ex2(edn - rk), wrt = ex2(e1[k] - rk), wdg = ex2(edg - rk);
+          T g = wdn * gdn + wrt * g1[k] + wdg * gdg;
+          T h = (T)0;
+          if (PEN) {
+            const T hdn = (k + 1 < ROWS) ? h1[k + 1] : nh1;
+            const T adn = (k + 1 < ROWS) ? a1[k + 1] : na1;
+            const T hdg = (k + 1 < ROWS) ? h2[k + 1] : nh2;
+            const T adg = (k + 1 < ROWS) ? a2[k + 1] : na2;
+            const T wh_dn = wdn * hdn, wh_rt = wrt * h1[k], wh_dg = wdg * hdg;
+            g -= (wh_dn * (pk - adn) + wh_rt * (pk - a1[k]) + wh_dg * (pk - adg)) * a.inv_gamma;
+            h = wh_dn + wh_rt + wh_dg;
+          }
+          // outside the grid, and (band) at unreachable cells, nothing flows
+          bool live = valid;
+          if (BAND) live = live && rk < INF;
+          g = live ? g : (T)0;
+          h = live ? h : (T)0;
+          xe[k] = live ? rk - ch : -INF;
+          xg[k] = g;
+          xh[k] = h;
+          xa[k] = valid ? pk - q : (T)0;
+
+          const int vn = valid ? vnat[k] : kOob;
+          if (SRC == SRC_COST) {
+            bdC.st(g, vn, so_n);
+            if (want_dq) bdQ.st(h, vn, so_n);
+          } else {
+            const T dsq = sq_raw > (T)0 ? g * rv : (T)0;
+            if (SRC == SRC_SQ) bdC.st(dsq, vn, so_n);
+            if (SRC == SRC_FEAT1) {
+              const T df = valid ? (T)2 * dsq * (xr[k] - yc[k]) : (T)0;
+              dxr[k] += df;
+              cy[k] -= df;
+            }
+            if (vgrad) {
+              T dvar = var_raw > a.eps ? (T)0.5 * (a.beta * h - g * c) * rv : (T)0;
+              dvar = valid ? dvar : (T)0;
+              dvr[k] += dvar;
+              cvy[k] += dvar;
+            }
+            // column d leaves the sweep at row 0: store its sums
+            const int vc = ((unsigned)d < (unsigned)M) ? vrow0[k] : kOob;
+            if (SRC == SRC_FEAT1) bdY.st(cy[k], vc, so_n);
+            if (vgrad) bdVY.st(cvy[k], vc, so_n);
+          }
+        }
+  #pragma unroll
+        for (int k = 0; k < ROWS; ++k) {
+          e2[k] = e1[k];
+          e1[k] = xe[k];
+          g2[k] = g1[k];
+          g1[k] = xg[k];
+          h2[k] = h1[k];
+          h1[k] = xh[k];
+          a2[k] = a1[k];
+          a1[k] = xa[k];
+        }
+        // ring reloads and the record for the next step only now (see the forward)
+        __builtin_amdgcn_sched_barrier(0);
+        fetch(d - PF, rr[u % PF], rp[u % PF], rc[u % PF], rq[u % PF]);
+        if (EDGE && COLS) {
+          ey_ring[u] = col_y(vcol - (u + kSlots) * ES);
+          evy_ring[u] = col_vy(vcol - (u + kSlots) * ES);
+        }
+        if (!EDGE) {
+          if (COLS)
+            nx = inbox[(u + 2) & 3];
+          else
+            nx.a = inbox[(u + 2) & 3].a;
+        }
+        if (COLS) {
+          my_out[u] = {{e1[0], g1[0], h1[0], a1[0]}, {yc[0], hyc[0], cy[0], cvy[0]}};
+        } else {
+          my_out[u].a = {e1[0], g1[0], h1[0], a1[0]};
+        }
+        lag_barrier();
+      }
+      vcol -= kSlots * ES;
+    }
+  };
+  if (last_wave)
+    sweep(std::true_type{});
+  else
+    sweep(std::false_type{});
 #pragma unroll
   for (int k = 0; k < ROWS; ++k) {
     const int i = row0 + k;
@@ -760,6 +793,15 @@ static void set_hyper(UdtwArgs<T>& a, double gamma, double beta, double eps, dou
   a.beta_ln2 = (T)(beta * 0.6931471805599453);
   a.eps = (T)eps;
   a.band = (T)band;
+  a.hv1 = (T)0;
+  a.hv0 = (T)0.5;
+}
+
+template <typename T>
+static void set_sigma(UdtwArgs<T>& a, int sigma) {
+  a.sigma = sigma != 0;
+  a.hv1 = (T)(a.sigma ? 0.5 : 0.0);
+  a.hv0 = (T)(a.sigma ? 0.0 : 0.5);
 }
 
 static int check_dims(const char* what, int B, int N, int M, double gamma) {
@@ -906,8 +948,8 @@ static int feat_fwd(const T* X, const T* Y, const T* vx, const T* vy, int B, int
   a.out_p = out_p;
   a.N = N;
   a.M = M;
-  a.sigma = sigma != 0;
   set_hyper(a, gamma, beta, eps, band);
+  set_sigma(a, sigma);
   if (D == 1) {
     a.X = X;
     a.Y = Y;
@@ -968,8 +1010,8 @@ static int feat_bwd(const T* X, const T* Y, const T* vx, const T* vy, const T* R
   a.M = M;
   if (gstride != 0 && gstride != 1) return fail(TW_EINVAL, "%s: grad_stride must be 0 or 1", what);
   a.gstride = gstride;
-  a.sigma = sigma != 0;
   set_hyper(a, gamma, beta, eps, band);
+  set_sigma(a, sigma);
   const bool sig_grads = sigma && dvx != nullptr;
   if (D == 1) {
     a.X = X;
