@@ -82,10 +82,14 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 struct Buf {
   __amdgpu_buffer_rsrc_t r;
+  // The size and flags words pass through an empty asm, so descriptors of
+  // equal size never share registers: a shared word would have to be copied
+  // into each descriptor's aligned register quad before every access.
   template <typename T>
   __device__ __forceinline__ void init(const T* p, long long n) {
-    r = __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)(n * (long long)sizeof(T)),
-                                          kRsrcWord3);
+    int bytes = (int)(n * (long long)sizeof(T)), flags = kRsrcWord3;
+    asm volatile("" : "+s"(bytes), "+s"(flags));
+    r = __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, bytes, flags);
   }
   __device__ __forceinline__ float ldf(int v, int s) const {
     return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, v, s, 0));

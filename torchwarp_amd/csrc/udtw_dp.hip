@@ -6,7 +6,7 @@
 // value per diagonal is the last owned row of the previous thread (forward)
 // or the first owned row of the next thread (backward): a DPP wave shift
 // inside a wavefront, an LDS mailbox between wavefronts. Wavefronts meet at
-// an LDS-only barrier once per diagonal.
+// an LDS-only barrier once per block of four diagonals.
 //
 // Forward (reference: udtw_cuda.cu:57-164 and :298-422, udtw/_torch_dp.py:14-42):
 //   R[i,j] = C[i,j] + softmin_g(R[i-1,j-1], R[i-1,j], R[i,j-1])
@@ -88,20 +88,24 @@ __device__ __forceinline__ T half_var(const UdtwArgs<T>& a, T v) {
 
 // ------------------------------------------------------------- pipeline
 //
-// Wavefront w of a workgroup runs kLag = 2 diagonals behind wavefront w-1
-// (forward; behind w+1 in the backward). At global step tau every wavefront
-// stores its boundary row into slot tau % 4 of its neighbour's mailbox and
-// reads the record stored two steps earlier (slot (tau + 2) % 4), which it
-// uses on the following step. lag_barrier() leaves only the newest LDS
-// operation in flight, so a record is complete one barrier after it is
-// stored and is read after the next barrier: no mailbox latency and no
-// barrier-side wait sit on the dependency chain. The store is one
+// The steps of a sweep are grouped in blocks of kSlots = 4; the wavefronts of
+// a workgroup meet at one barrier per block. Wavefront w runs kLag = 4
+// diagonals behind wavefront w-1 (forward; behind w+1 in the backward), so
+// at step tau it needs its neighbour's boundary record of step tau - 5.
+// Every wavefront stores its boundary record of step tau into slot tau % 4 of
+// half (tau / 4) % 2 of its neighbour's mailbox. After the barrier that ends
+// block k (every LDS operation complete), the neighbour reads the four
+// records of block k: steps 4k+5, 4k+6, 4k+7 of block k+1 use the first
+// three, the fourth is kept in a register for step 4k+8, the first step of
+// block k+2. A half is rewritten two blocks later, after the barrier that
+// follows those reads, so no record is overwritten before it is read and the
+// reads are issued a whole step before their first use. The store is one
 // instruction for the whole wavefront: the lane holding the boundary row
 // writes the mailbox slot, the other lanes a private dump area, so no
-// exec-mask branch is needed. The edge wavefront writes its own records (the
-// border row and the column entering the sweep). Four steps are unrolled per
-// loop trip so mailbox slots, prefetch registers and buffer offsets of a
-// step are compile-time constants.
+// exec-mask branch is needed. The edge wavefront makes its own records (the
+// border row and the column entering the sweep). A loop trip is one block,
+// so mailbox slots, prefetch registers and buffer offsets of a step are
+// compile-time constants.
 //
 // Column values (y and hy = half the column variance) travel with the sweep:
 // row i on diagonal d uses column j = d - i, which row i-1 used on diagonal
@@ -113,11 +117,23 @@ __device__ __forceinline__ T half_var(const UdtwArgs<T>& a, T v) {
 // Global accesses are raw buffer operations with a lane-constant voffset and
 // a wave-uniform, non-negative soffset. The hardware range check covers the
 // voffset only; lanes outside the grid pass an out-of-range voffset, so their
-// loads return 0 and their stores are dropped without branching.
+// loads return 0 and their stores are dropped without branching. The
+// soffsets of 64 consecutive steps are computed once, one step per lane, and
+// each step takes its own with v_readlane: no per-step scalar arithmetic.
 
-constexpr int kLag = 2;
-constexpr int kSlots = 4;   // mailbox ring depth; also the steps per loop trip
-constexpr int kDump = 64 + kSlots;
+constexpr int kLag = 4;
+constexpr int kSlots = 4;            // steps per block (and per loop trip)
+constexpr int kBox = 2 * kSlots;     // mailbox slots per wavefront boundary
+constexpr int kDump = 64 + kBox;
+constexpr int kWindow = 64;          // steps per soffset window (one per lane)
+
+// Barrier at the end of a block: every LDS operation of this wavefront is
+// complete (the block's mailbox stores and the reads of the previous block's
+// records), then the workgroup barrier. Outstanding global stores are not
+// waited for.
+__device__ __forceinline__ void block_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 template <typename T>
 struct alignas(4 * sizeof(T)) Rec4 {
@@ -128,32 +144,13 @@ struct alignas(4 * sizeof(T)) Rec8 {
   Rec4<T> a, b;
 };
 
-// Wave-uniform integer min / max on the scalar unit. Offsets built from them
-// stay in scalar registers; the compiler would otherwise fold nested min/max
-// into a vector min3 and carry the offset in a vector register. The operands
-// pass through readfirstlane so a vector copy of a uniform value never
-// reaches the scalar instruction.
-__device__ __forceinline__ int smin(int a, int b) {
-  int r;
-  asm("s_min_i32 %0, %1, %2"
-      : "=s"(r)
-      : "s"(__builtin_amdgcn_readfirstlane(a)), "s"(__builtin_amdgcn_readfirstlane(b))
-      : "scc");
-  return r;
-}
-__device__ __forceinline__ int smax(int a, int b) {
-  int r;
-  asm("s_max_i32 %0, %1, %2"
-      : "=s"(r)
-      : "s"(__builtin_amdgcn_readfirstlane(a)), "s"(__builtin_amdgcn_readfirstlane(b))
-      : "scc");
-  return r;
-}
-
-// soff(e+1) - soff(e) for soff(e) = (index of the first cell of diagonal e)
-// - (row of that cell) in the diagonal-major layout, N <= M; 0 outside the grid.
-__device__ __forceinline__ int diag_step(int e, int N, int M) {
-  return smax(0, smin(smin(e + 1, N), N + M - 2 - e));
+// soff(d) = (index of the first cell of diagonal d) - (row of that cell) in
+// the diagonal-major layout of an N x M grid, N <= M: cell (i, d - i) is
+// element soff(d) + i. Clamped to diagonal 0 below and Dn - 1 above.
+__device__ __forceinline__ int diag_soff(int d, int N, int M) {
+  d = d < 0 ? 0 : (d > N + M - 2 ? N + M - 2 : d);
+  const int lo = d - M + 1 > 0 ? d - M + 1 : 0;
+  return (int)(diag_offset(d, N, M) - lo);
 }
 
 template <int ROWS>
@@ -174,11 +171,12 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwA
   const long long NM = (long long)N * M;
   const int Dn = N + M - 1;
 
-  // box[v * kSlots + slot]: wavefront v's inbox (the row above its first
+  // box[v * kBox + slot]: wavefront v's inbox (the row above its first
   // row; box[nw] is the last wavefront's unread outbox), then the dump area.
   Rec4<T>* box = reinterpret_cast<Rec4<T>*>(smem_raw);
-  Rec4<T>* dump = box + (nw + 1) * kSlots;
-  for (int t = tid; t < (nw + 1) * kSlots; t += blockDim.x) box[t] = {INF, (T)0, (T)0, (T)0.5};
+  Rec4<T>* dump = box + (nw + 1) * kBox;
+  const Rec4<T> rec0 = {INF, (T)0, (T)0, (T)0.5};   // the record before the sweep
+  for (int t = tid; t < (nw + 1) * kBox; t += blockDim.x) box[t] = rec0;
 
   Buf bR, bP, bC, bQ, bY, bVY;
   bR.init(a.R + b * NM, NM);
@@ -192,8 +190,8 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwA
   auto col_y = [&](int vcol) -> T { return SRC == SRC_FEAT1 ? bY.ld<T>(vcol, 0) : (T)0; };
   auto col_vy = [&](int vcol) -> T { return COLS ? bVY.ld<T>(vcol, 0) : (T)1; };
 
-  Rec4<T>* const inbox = box + wave * kSlots;
-  Rec4<T>* const outbox = box + (wave + 1) * kSlots;
+  Rec4<T>* const inbox = box + wave * kBox;
+  Rec4<T>* const outbox = box + (wave + 1) * kBox;
   // the mailbox store of a step: lane 63 to the slot, the others to the dump
   Rec4<T>* const my_out = lane == 63 ? outbox : dump + lane;
   __syncthreads();
@@ -220,8 +218,8 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwA
   const int steps = (Dn + kLag * (nw - 1) + kSlots - 1) / kSlots * kSlots;
 
   T rc[PF][ROWS], rq[PF][ROWS];
-  auto fetch = [&](int d, T* c, T* q) {
-    const int so = smax(d, 0) * ES;
+  // C (and Q) of diagonal d at byte soffset so = max(d, 0) * ES
+  auto fetch = [&](int d, int so, T* c, T* q) {
 #pragma unroll
     for (int k = 0; k < ROWS; ++k) {
       const int vo = (unsigned)(d + jb[k]) < (unsigned)M ? vnat[k] : kOob;
@@ -231,7 +229,10 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwA
   };
   if (SRC != SRC_FEAT1) {
 #pragma unroll
-    for (int u = 0; u < PF; ++u) fetch(d_first + u, rc[u], rq[u]);
+    for (int u = 0; u < PF; ++u) {
+      const int d = d_first + u;
+      fetch(d, (d > 0 ? d : 0) * ES, rc[u], rq[u]);
+    }
   }
 
   // The sweep, instantiated for the edge wavefront (0: its row above is the
@@ -248,17 +249,31 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwA
         evy_ring[u] = col_vy(u * ES);
       }
     }
-    Rec4<T> nxt = {INF, (T)0, (T)0, (T)0.5};
-    if (!EDGE) nxt = inbox[1];
-    int soff = 0;  // soff of diagonal d, in elements
+    Rec4<T> carry = rec0;   // the record used by the first step of the next block
     // Drain the set-up loads here: the compiler derives each in-loop wait on
     // a ring register from every path into the loop, and the entry path
     // would otherwise force a near-full vmcnt wait on every trip.
     __builtin_amdgcn_s_waitcnt(0);
-    for (int t0 = 0; t0 < steps; t0 += kSlots) {
+    for (int tw = 0; tw < steps; tw += kWindow) {
+      // lane l: byte soffsets of step tw + l (R / P store, C / Q fetch)
+      const int dl = d_first + tw + lane;
+      const int so_st = diag_soff(dl, N, M) * ES;
+      const int so_ld = SRC != SRC_FEAT1 ? (dl + PF > 0 ? dl + PF : 0) * ES : 0;
+      const int tn = min(kWindow, steps - tw);
+    for (int t0 = 0; t0 < tn; t0 += kSlots) {
+      const int half = (t0 / kSlots) & 1;   // mailbox half of this block
+      Rec4<T> rec[kSlots];
+      if (!EDGE) {
+        const Rec4<T>* prev = inbox + (half ^ 1) * kSlots;
+        rec[0] = carry;
+#pragma unroll
+        for (int u = 1; u < kSlots; ++u) rec[u] = prev[u - 1];
+        carry = prev[kSlots - 1];
+      }
+      Rec4<T>* const out = my_out + half * kSlots;
 #pragma unroll
       for (int u = 0; u < kSlots; ++u) {
-        const int d = d_first + t0 + u;
+        const int d = d_first + tw + t0 + u;
         T cc[ROWS], cq[ROWS];
 #pragma unroll
         for (int k = 0; k < ROWS; ++k) {
@@ -271,7 +286,7 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwA
         if (EDGE)
           e = {INF, (T)0, ey_ring[u], COLS ? half_var(a, evy_ring[u]) : (T)0.5};
         else
-          e = nxt;
+          e = rec[u];
 
         nr2 = nr1;
         np2 = np1;
@@ -293,7 +308,7 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwA
           hyc[0] = nhy;
         }
 
-        const int so = soff * ES;
+        const int so = __builtin_amdgcn_readlane(so_st, t0 + u);
         T nr[ROWS], np[ROWS];
 #pragma unroll
         for (int k = 0; k < ROWS; ++k) {
@@ -344,25 +359,21 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwA
           p2[k] = p1[k];
           p1[k] = np[k];
         }
-        soff += diag_step(d, N, M);
-        // Read the record for the next step (stored two steps ago, complete
-        // since the last barrier) only now, after this step's shifts: the
-        // scheduling barrier keeps it there, so its destination registers
-        // never collide with the shifts' results.
-        // The ring reloads follow the same rule: issued after the last use
-        // of the slot they refill, so the slot's register is reused in place
-        // and the loop back edge needs no copies (nor the waits they imply).
+        // The ring reloads are issued after the last use of the slot they
+        // refill, so the slot's register is reused in place and the loop back
+        // edge needs no copies (nor the waits they imply).
         __builtin_amdgcn_sched_barrier(0);
-        if (SRC != SRC_FEAT1) fetch(d + PF, rc[u % PF], rq[u % PF]);
+        if (SRC != SRC_FEAT1)
+          fetch(d + PF, __builtin_amdgcn_readlane(so_ld, t0 + u), rc[u % PF], rq[u % PF]);
         if (EDGE && COLS) {
           ey_ring[u] = col_y(vcol + (u + kSlots) * ES);
           evy_ring[u] = col_vy(vcol + (u + kSlots) * ES);
         }
-        if (!EDGE) nxt = inbox[(u + 2) & 3];
-        my_out[u] = {r1[ROWS - 1], p1[ROWS - 1], yc[ROWS - 1], hyc[ROWS - 1]};
-        lag_barrier();
+        out[u] = {r1[ROWS - 1], p1[ROWS - 1], yc[ROWS - 1], hyc[ROWS - 1]};
       }
+      block_barrier();
       vcol += kSlots * ES;
+    }
     }
   };
   if (wave == 0)
@@ -397,15 +408,13 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
   // where every column enters the backward sweep.
   const int row0 = tid * ROWS - ((int)blockDim.x * ROWS - N);
 
-  // box[(v + 1) * kSlots + slot]: wavefront v's inbox, the row below its last
-  // row: (E, G, H, A) and (y, hy, dy sum, dvy sum); box[0..kSlots) is
+  // box[(v + 1) * kBox + slot]: wavefront v's inbox, the row below its last
+  // row: (E, G, H, A) and (y, hy, dy sum, dvy sum); box[0..kBox) is
   // wavefront 0's unread outbox. Then the dump area.
   Rec8<T>* box = reinterpret_cast<Rec8<T>*>(smem_raw);
-  Rec8<T>* dump = box + (nw + 1) * kSlots;
-  for (int t = tid; t < (nw + 1) * kSlots; t += blockDim.x) {
-    box[t].a = {-INF, (T)0, (T)0, (T)0};
-    box[t].b = {(T)0, (T)0.5, (T)0, (T)0};
-  }
+  Rec8<T>* dump = box + (nw + 1) * kBox;
+  const Rec8<T> rec0 = {{-INF, (T)0, (T)0, (T)0}, {(T)0, (T)0.5, (T)0, (T)0}};
+  for (int t = tid; t < (nw + 1) * kBox; t += blockDim.x) box[t] = rec0;
 
   Buf bR, bP, bC, bQ, bdC, bdQ, bY, bVY, bdY, bdVY;
   bR.init(a.R + b * NM, NM);
@@ -417,22 +426,25 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
   const bool want_dq = SRC == SRC_COST && PEN && a.dQ != nullptr;
   if (SRC == SRC_COST && PEN) {
     bQ.init(a.Q + b * NM, NM);
-    if (want_dq) bdQ.init(a.dQ + b * NM, NM);
+    // no penalty gradient wanted: its stores go to an empty buffer (dropped)
+    bdQ.init(want_dq ? a.dQ + b * NM : a.Q, want_dq ? NM : 0);
   }
   if (SRC == SRC_FEAT1) {
     bY.init(a.Y + (size_t)b * M, M);
     bdY.init(a.dY + (size_t)b * M, M);
   }
   if (COLS) bVY.init(a.VY + (size_t)b * M, M);
-  if (vgrad) bdVY.init(a.dVY + (size_t)b * M, M);
+  // without variance gradients the column sums are still formed (no branch in
+  // the sweep) and their stores go to an empty buffer, which drops them
+  if (COLS) bdVY.init(vgrad ? a.dVY + (size_t)b * M : a.VY, vgrad ? M : 0);
   // column operands of the edge wavefront at byte offset vcol (lane uniform);
   // columns before the first fail the range check and read 0
   auto col_y = [&](int vcol) -> T { return SRC == SRC_FEAT1 ? bY.ld<T>(vcol, 0) : (T)0; };
   auto col_vy = [&](int vcol) -> T { return COLS ? bVY.ld<T>(vcol, 0) : (T)1; };
 
   const bool last_wave = wave == nw - 1;
-  Rec8<T>* const inbox = box + (wave + 1) * kSlots;
-  Rec8<T>* const outbox = box + wave * kSlots;
+  Rec8<T>* const inbox = box + (wave + 1) * kBox;
+  Rec8<T>* const outbox = box + wave * kBox;
   Rec8<T>* const my_out = lane == 0 ? outbox : dump + lane;
   __syncthreads();
 
@@ -475,10 +487,9 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
   const int steps = (Dn + kLag * (nw - 1) + kSlots - 1) / kSlots * kSlots;
 
   T rr[PF][ROWS], rp[PF][ROWS], rc[PF][ROWS], rq[PF][ROWS];
-  int sfetch = (int)(NM - N);  // soff of the next diagonal to fetch (min(d, Dn-1))
-  auto fetch = [&](int d, T* r, T* p, T* c, T* q) {
-    const int so_d = sfetch * ES;
-    const int so_n = smax(d, 0) * ES;
+  // R, P of diagonal d at byte soffset so_d = soff(d) * ES (diagonal-major),
+  // C, Q at so_n = max(d, 0) * ES ([N, M])
+  auto fetch = [&](int d, int so_d, int so_n, T* r, T* p, T* c, T* q) {
 #pragma unroll
     for (int k = 0; k < ROWS; ++k) {
       const bool v = (unsigned)(d + jb[k]) < (unsigned)M;
@@ -491,10 +502,12 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
         if (SRC == SRC_COST && PEN) q[k] = bQ.ld<T>(vn, so_n);
       }
     }
-    sfetch -= diag_step(d - 1, N, M);
   };
 #pragma unroll
-  for (int u = 0; u < PF; ++u) fetch(d_first - u, rr[u], rp[u], rc[u], rq[u]);
+  for (int u = 0; u < PF; ++u) {
+    const int d = d_first - u;
+    fetch(d, diag_soff(d, N, M) * ES, (d > 0 ? d : 0) * ES, rr[u], rp[u], rc[u], rq[u]);
+  }
 
   // The sweep, instantiated for the edge wavefront (the last: its row below
   // is the virtual row N, its entering column comes from a register ring of
@@ -512,13 +525,34 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
         evy_ring[u] = col_vy(vcol - u * ES);
       }
     }
-    Rec8<T> nx = {{-INF, (T)0, (T)0, (T)0}, {(T)0, (T)0.5, (T)0, (T)0}};
-    if (!EDGE) nx = inbox[1];
+    Rec8<T> carry = rec0;   // the record used by the first step of the next block
     __builtin_amdgcn_s_waitcnt(0);   // drain the set-up loads (as in the forward)
-    for (int t0 = 0; t0 < steps; t0 += kSlots) {
+    for (int tw = 0; tw < steps; tw += kWindow) {
+      // lane l: byte soffsets of step tw + l (fetch of R / P and C / Q, and
+      // the stores of the step's own diagonal)
+      const int dl = d_first - tw - lane;
+      const int so_fd = diag_soff(dl - PF, N, M) * ES;
+      const int so_fn = SRC != SRC_FEAT1 ? (dl - PF > 0 ? dl - PF : 0) * ES : 0;
+      const int so_st = (dl > 0 ? dl : 0) * ES;
+      const int tn = min(kWindow, steps - tw);
+    for (int t0 = 0; t0 < tn; t0 += kSlots) {
+      const int half = (t0 / kSlots) & 1;   // mailbox half of this block
+      Rec8<T> rec[kSlots];
+      if (!EDGE) {
+        const Rec8<T>* prev = inbox + (half ^ 1) * kSlots;
+        rec[0] = carry;
+#pragma unroll
+        for (int u = 1; u < kSlots; ++u) {
+          rec[u].a = prev[u - 1].a;
+          if (COLS) rec[u].b = prev[u - 1].b;
+        }
+        carry.a = prev[kSlots - 1].a;
+        if (COLS) carry.b = prev[kSlots - 1].b;
+      }
+      Rec8<T>* const out = my_out + half * kSlots;
 #pragma unroll
       for (int u = 0; u < kSlots; ++u) {
-        const int d = d_first - t0 - u;
+        const int d = d_first - tw - t0 - u;
         T cr[ROWS], cp[ROWS], cc[ROWS], cq[ROWS];
   #pragma unroll
         for (int k = 0; k < ROWS; ++k) {
@@ -534,7 +568,7 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
           ex = {{-INF, (T)0, (T)0, (T)0},
                 {ey_ring[u], COLS ? half_var(a, evy_ring[u]) : (T)0.5, (T)0, (T)0}};
         else
-          ex = nx;
+          ex = rec[u];
 
         ne2 = ne1;
         ng2 = ng1;
@@ -551,7 +585,7 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
                        : shift_next(yc[0], EDGE ? uniform(ex.b.x) : ex.b.x);
           const T fhy = shift_next(hyc[0], EDGE ? uniform(ex.b.y) : ex.b.y);
           const T fcy = SRC != SRC_FEAT1 ? (T)0 : EDGE ? shift_next0(cy[0]) : shift_next(cy[0], ex.b.z);
-          const T fcvy = !vgrad ? (T)0 : EDGE ? shift_next0(cvy[0]) : shift_next(cvy[0], ex.b.w);
+          const T fcvy = EDGE ? shift_next0(cvy[0]) : shift_next(cvy[0], ex.b.w);
   #pragma unroll
           for (int k = 0; k + 1 < ROWS; ++k) {
             yc[k] = yc[k + 1];
@@ -565,7 +599,7 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
           cvy[ROWS - 1] = fcvy;
         }
 
-        const int so_n = smax(d, 0) * ES;
+        const int so_n = __builtin_amdgcn_readlane(so_st, t0 + u);
         T xe[ROWS], xg[ROWS], xh[ROWS], xa[ROWS];
   #pragma unroll
         for (int k = 0; k < ROWS; ++k) {
@@ -621,7 +655,7 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
           const int vn = valid ? vnat[k] : kOob;
           if (SRC == SRC_COST) {
             bdC.st(g, vn, so_n);
-            if (want_dq) bdQ.st(h, vn, so_n);
+            if (PEN) bdQ.st(h, vn, so_n);
           } else {
             const T dsq = sq_raw > (T)0 ? g * rv : (T)0;
             if (SRC == SRC_SQ) bdC.st(dsq, vn, so_n);
@@ -630,7 +664,7 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
               dxr[k] += df;
               cy[k] -= df;
             }
-            if (vgrad) {
+            {
               T dvar = var_raw > a.eps ? (T)0.5 * (a.beta * h - g * c) * rv : (T)0;
               dvar = valid ? dvar : (T)0;
               dvr[k] += dvar;
@@ -639,7 +673,7 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
             // column d leaves the sweep at row 0: store its sums
             const int vc = ((unsigned)d < (unsigned)M) ? vrow0[k] : kOob;
             if (SRC == SRC_FEAT1) bdY.st(cy[k], vc, so_n);
-            if (vgrad) bdVY.st(cvy[k], vc, so_n);
+            bdVY.st(cvy[k], vc, so_n);
           }
         }
   #pragma unroll
@@ -653,27 +687,24 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
           a2[k] = a1[k];
           a1[k] = xa[k];
         }
-        // ring reloads and the record for the next step only now (see the forward)
+        // ring reloads only now (see the forward)
         __builtin_amdgcn_sched_barrier(0);
-        fetch(d - PF, rr[u % PF], rp[u % PF], rc[u % PF], rq[u % PF]);
+        fetch(d - PF, __builtin_amdgcn_readlane(so_fd, t0 + u),
+              __builtin_amdgcn_readlane(so_fn, t0 + u), rr[u % PF], rp[u % PF], rc[u % PF],
+              rq[u % PF]);
         if (EDGE && COLS) {
           ey_ring[u] = col_y(vcol - (u + kSlots) * ES);
           evy_ring[u] = col_vy(vcol - (u + kSlots) * ES);
         }
-        if (!EDGE) {
-          if (COLS)
-            nx = inbox[(u + 2) & 3];
-          else
-            nx.a = inbox[(u + 2) & 3].a;
-        }
         if (COLS) {
-          my_out[u] = {{e1[0], g1[0], h1[0], a1[0]}, {yc[0], hyc[0], cy[0], cvy[0]}};
+          out[u] = {{e1[0], g1[0], h1[0], a1[0]}, {yc[0], hyc[0], cy[0], cvy[0]}};
         } else {
-          my_out[u].a = {e1[0], g1[0], h1[0], a1[0]};
+          out[u].a = {e1[0], g1[0], h1[0], a1[0]};
         }
-        lag_barrier();
       }
+      block_barrier();
       vcol -= kSlots * ES;
+    }
     }
   };
   if (last_wave)
@@ -721,7 +752,7 @@ static Shape pick_shape(int N) {
 // mailbox stores (records of 4 values forward, 8 backward).
 template <typename T>
 static size_t udtw_lds(bool backward, int nw) {
-  return (size_t)((nw + 1) * kSlots + kDump) * (backward ? 8 : 4) * sizeof(T);
+  return (size_t)((nw + 1) * kBox + kDump) * (backward ? 8 : 4) * sizeof(T);
 }
 
 // Prefetch depth (diagonals) of the register ring for a row count.
