@@ -37,9 +37,34 @@ COMMON = [
 ]
 
 
-def _compile(src):
-    obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC] + COMMON + ["-c", str(src), "-o", str(obj)]
+# Sources compiled once per set of defines (one object each): the uDTW sweep
+# launchers per (type, direction, cost source), so their kernels build in
+# parallel.
+VARIANTS = {
+    "udtw_sweep.hip": [
+        {"TW_SWEEP_T": t, "TW_SWEEP_BWD": bwd, "TW_SWEEP_SRC": src}
+        for t in ("float", "double") for bwd in ("0", "1") for src in ("0", "1", "2")
+    ],
+}
+
+
+def _units():
+    """(source, defines, object name) of every compilation unit."""
+    units = []
+    for src in sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp")):
+        for k, defs in enumerate(VARIANTS.get(src.name, [None])):
+            stem = src.stem if defs is None else "{}_{}".format(src.stem, k)
+            units.append((src, defs or {}, stem))
+    # longest first: the double-precision sweeps dominate the build
+    units.sort(key=lambda u: (u[1].get("TW_SWEEP_T") != "double", u[2]))
+    return units
+
+
+def _compile(unit):
+    src, defs, stem = unit
+    obj = BUILD / (stem + ".o")
+    cmd = [HIPCC] + COMMON + ["-D{}={}".format(k, v) for k, v in defs.items()]
+    cmd += ["-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
         cmd = [HIPCC, "-O2", "-fPIC", "-std=c++17", "-I" + str(ROOT / "include"),
                "-c", str(src), "-o", str(obj)]
@@ -57,10 +82,10 @@ def _compile(src):
 def build(verbose=False):
     """Compile every source and link the shared library; returns its path."""
     BUILD.mkdir(exist_ok=True)
-    srcs = sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp"))
-    jobs = min(len(srcs), int(os.environ.get("MAX_JOBS", "8")), 16)
+    units = _units()
+    jobs = min(len(units), int(os.environ.get("MAX_JOBS", "8")), 16)
     with ThreadPoolExecutor(max_workers=max(1, jobs)) as ex:
-        results = list(ex.map(_compile, srcs))
+        results = list(ex.map(_compile, units))
     for obj, msg in results:
         if verbose and msg:
             print(msg)

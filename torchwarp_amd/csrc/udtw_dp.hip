@@ -1,818 +1,17 @@
-// uDTW / soft-DTW dynamic program for gfx950: forward and fused backward.
-//
-// One workgroup per sequence pair. Thread t owns the ROWS contiguous grid
-// rows t*ROWS .. t*ROWS+ROWS-1 and sweeps the anti-diagonals d = i + j with
-// its rows' two previous diagonals held in registers. The only cross-thread
-// value per diagonal is the last owned row of the previous thread (forward)
-// or the first owned row of the next thread (backward): a DPP wave shift
-// inside a wavefront, an LDS mailbox between wavefronts. Wavefronts meet at
-// an LDS-only barrier once per block of four diagonals.
-//
-// Forward (reference: udtw_cuda.cu:57-164 and :298-422, udtw/_torch_dp.py:14-42):
-//   R[i,j] = C[i,j] + softmin_g(R[i-1,j-1], R[i-1,j], R[i,j-1])
-//   P[i,j] = Q[i,j] + sum_k softmax(-R_k/g)_k P_k
-// with R[-1,-1] = 0 and +inf elsewhere on the border, R = +inf / P = 0 for
-// unreachable cells and outside the Sakoe-Chiba band |i-j| <= band.
-// R is stored scaled (Rh = R log2(e)/g) in a diagonal-major layout (the
-// cells of diagonal d contiguous, by row), P unscaled in the same layout;
-// both are internal tensors carried from the forward to the backward.
-//
-// Backward (udtw_cuda.cu:166-278, :424-582; udtw/_torch_dp.py:45-75), for
-// L = gR R[N-1,M-1] + gP P[N-1,M-1] and successors s of cell k:
-//   w = 2^(Eh_s - Rh_k),  Eh = Rh - Ch
-//   Rbar_k = sum_s w (Rbar_s - Pbar_s (P_k - A_s) / g),  A = P - Q
-//   Pbar_k = sum_s w Pbar_s.
-//
-// Cost sources (template SRC):
-//   SRC_COST  C, Q given as [B,N,M]                   -> writes dC, dQ
-//   SRC_SQ    raw squared distance S = x2+y2-2x.y [B,N,M] and variances
-//             vx [B,N], vy [B,M]: C = max(S,0)/max((vx+vy)/2,eps),
-//             Q = beta ln max(...)                      -> writes dS, dvx, dvy
-//   SRC_FEAT1 one feature per step, x [B,N], y [B,M] and variances,
-//             C from (x-y)^2 in registers               -> writes dx, dy, dvx, dvy
-// Column sums (dy, dvy) travel up the rows with their column and are stored
-// when the column leaves the sweep, so their order of summation is fixed
-// (bitwise deterministic).
+// uDTW / soft-DTW host entry points for gfx950: argument checks, the
+// hyper-parameters of the sweep and the C ABI. The sweep kernels and their
+// launchers are in udtw_sweep.hpp.
 
-#include <limits.h>
-#include <type_traits>
-#include <stdlib.h>
-
-#include "tw_capi.hpp"
-#include "tw_common.hpp"
+#include "udtw_sweep.hpp"
 #include "../../include/torchwarp_hip.h"
 
 namespace tw {
 
-enum { SRC_COST = 0, SRC_SQ = 1, SRC_FEAT1 = 2 };
-
-template <typename T>
-struct UdtwArgs {
-  const T* C;    // SRC_COST cost / SRC_SQ raw squared distance, [B,N,M]
-  const T* Q;    // SRC_COST penalty [B,N,M] (PEN)
-  const T* X;    // SRC_FEAT1 [B,N]
-  const T* Y;    // SRC_FEAT1 [B,M]
-  const T* VX;   // SRC_SQ / SRC_FEAT1 [B,N]
-  const T* VY;   // [B,M]
-  T* R;          // [B, N*M] diagonal-major, scaled
-  T* P;          // [B, N*M] diagonal-major (PEN)
-  T* out_r;      // [B]
-  T* out_p;      // [B]
-  const T* gr;   // [B]
-  const T* gp;   // [B] (PEN)
-  T* dC;         // SRC_COST d cost / SRC_SQ d squared distance, [B,N,M]
-  T* dQ;         // SRC_COST d penalty (may be null)
-  T* dX;         // SRC_FEAT1 [B,N]
-  T* dY;         // SRC_FEAT1 [B,M]
-  T* dVX;        // SRC_SQ / SRC_FEAT1 [B,N] (may be null: no variance gradient)
-  T* dVY;        // [B,M]
-  int N, M;
-  T k;           // log2(e) / gamma
-  T inv_k;       // gamma ln 2
-  T inv_gamma;   // 1 / gamma
-  T beta;
-  T beta_ln2;    // beta ln 2
-  T eps;
-  T band;        // <= 0: no band
-  int sigma;     // VX / VY hold standard deviations: variances are their squares
-  T hv1, hv0;    // half variance of an input v: v (hv1 v + hv0)
-  int gstride;   // element stride of gr / gp (0: one value for every pair)
-};
-
-// Half of a variance input: 0.5 v, or 0.5 v^2 when the input is a standard
-// deviation, as v (hv1 v + hv0) with (hv1, hv0) = (0, 0.5) or (0.5, 0).
-template <typename T>
-__device__ __forceinline__ T half_var(const UdtwArgs<T>& a, T v) {
-  return v * (a.hv1 * v + a.hv0);
-}
-
-// ------------------------------------------------------------- pipeline
-//
-// The steps of a sweep are grouped in blocks of kSlots = 4; the wavefronts of
-// a workgroup meet at one barrier per block. Wavefront w runs kLag = 4
-// diagonals behind wavefront w-1 (forward; behind w+1 in the backward), so
-// at step tau it needs its neighbour's boundary record of step tau - 5.
-// Every wavefront stores its boundary record of step tau into slot tau % 4 of
-// half (tau / 4) % 2 of its neighbour's mailbox. After the barrier that ends
-// block k (every LDS operation complete), the neighbour reads the four
-// records of block k: steps 4k+5, 4k+6, 4k+7 of block k+1 use the first
-// three, the fourth is kept in a register for step 4k+8, the first step of
-// block k+2. A half is rewritten two blocks later, after the barrier that
-// follows those reads, so no record is overwritten before it is read and the
-// reads are issued a whole step before their first use. The store is one
-// instruction for the whole wavefront: the lane holding the boundary row
-// writes the mailbox slot, the other lanes a private dump area, so no
-// exec-mask branch is needed. The edge wavefront makes its own records (the
-// border row and the column entering the sweep). A loop trip is one block,
-// so mailbox slots, prefetch registers and buffer offsets of a step are
-// compile-time constants.
-//
-// Column values (y and hy = half the column variance) travel with the sweep:
-// row i on diagonal d uses column j = d - i, which row i-1 used on diagonal
-// d-1, so a row takes its column operands from the row above (forward) or
-// below (backward) with the DPP shift that moves R. The backward's column
-// gradient sums ride along the same way and are stored when their column
-// leaves the sweep at row 0, summed over rows in a fixed order.
-//
-// Global accesses are raw buffer operations with a lane-constant voffset and
-// a wave-uniform, non-negative soffset. The hardware range check covers the
-// voffset only; lanes outside the grid pass an out-of-range voffset, so their
-// loads return 0 and their stores are dropped without branching. The
-// soffsets of 64 consecutive steps are computed once, one step per lane, and
-// each step takes its own with v_readlane: no per-step scalar arithmetic.
-
-constexpr int kLag = 4;
-constexpr int kSlots = 4;            // steps per block (and per loop trip)
-constexpr int kBox = 2 * kSlots;     // mailbox slots per wavefront boundary
-constexpr int kDump = 64 + kBox;
-constexpr int kWindow = 64;          // steps per soffset window (one per lane)
-
-// Barrier at the end of a block: every LDS operation of this wavefront is
-// complete (the block's mailbox stores and the reads of the previous block's
-// records), then the workgroup barrier. Outstanding global stores are not
-// waited for.
-__device__ __forceinline__ void block_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-template <typename T>
-struct alignas(4 * sizeof(T)) Rec4 {
-  T x, y, z, w;
-};
-template <typename T>
-struct alignas(4 * sizeof(T)) Rec8 {
-  Rec4<T> a, b;
-};
-
-// soff(d) = (index of the first cell of diagonal d) - (row of that cell) in
-// the diagonal-major layout of an N x M grid, N <= M: cell (i, d - i) is
-// element soff(d) + i. Clamped to diagonal 0 below and Dn - 1 above.
-__device__ __forceinline__ int diag_soff(int d, int N, int M) {
-  d = d < 0 ? 0 : (d > N + M - 2 ? N + M - 2 : d);
-  const int lo = d - M + 1 > 0 ? d - M + 1 : 0;
-  return (int)(diag_offset(d, N, M) - lo);
-}
-
-template <int ROWS>
-struct MaxThreads {
-  static constexpr int value = ROWS >= 16 ? 1024 : 256;
-};
-
-template <typename T, int ROWS, int SRC, bool PEN, bool BAND, int PF>
-__global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwArgs<T> a) {
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  constexpr int ES = sizeof(T);
-  constexpr bool COLS = SRC != SRC_COST;
-  const int N = a.N, M = a.M;
-  const int b = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const T INF = inf_v<T>();
-  const long long NM = (long long)N * M;
-  const int Dn = N + M - 1;
-
-  // box[v * kBox + slot]: wavefront v's inbox (the row above its first
-  // row; box[nw] is the last wavefront's unread outbox), then the dump area.
-  Rec4<T>* box = reinterpret_cast<Rec4<T>*>(smem_raw);
-  Rec4<T>* dump = box + (nw + 1) * kBox;
-  const Rec4<T> rec0 = {INF, (T)0, (T)0, (T)0.5};   // the record before the sweep
-  for (int t = tid; t < (nw + 1) * kBox; t += blockDim.x) box[t] = rec0;
-
-  Buf bR, bP, bC, bQ, bY, bVY;
-  bR.init(a.R + b * NM, NM);
-  if (PEN) bP.init(a.P + b * NM, NM);
-  if (SRC != SRC_FEAT1) bC.init(a.C + b * NM, NM);
-  if (SRC == SRC_COST && PEN) bQ.init(a.Q + b * NM, NM);
-  if (SRC == SRC_FEAT1) bY.init(a.Y + (size_t)b * M, M);
-  if (COLS) bVY.init(a.VY + (size_t)b * M, M);
-  // column operands of the edge wavefront: loads at byte offset vcol (lane
-  // uniform); columns past the end fail the range check and read 0
-  auto col_y = [&](int vcol) -> T { return SRC == SRC_FEAT1 ? bY.ld<T>(vcol, 0) : (T)0; };
-  auto col_vy = [&](int vcol) -> T { return COLS ? bVY.ld<T>(vcol, 0) : (T)1; };
-
-  Rec4<T>* const inbox = box + wave * kBox;
-  Rec4<T>* const outbox = box + (wave + 1) * kBox;
-  // the mailbox store of a step: lane 63 to the slot, the others to the dump
-  Rec4<T>* const my_out = lane == 63 ? outbox : dump + lane;
-  __syncthreads();
-
-  const int row0 = tid * ROWS;
-  T xr[ROWS], hxr[ROWS], r1[ROWS], r2[ROWS], p1[ROWS], p2[ROWS], yc[ROWS], hyc[ROWS];
-  int vst[ROWS], vnat[ROWS], jb[ROWS];
-#pragma unroll
-  for (int k = 0; k < ROWS; ++k) {
-    const int i = row0 + k;
-    xr[k] = (SRC == SRC_FEAT1 && i < N) ? a.X[(size_t)b * N + i] : (T)0;
-    hxr[k] = (COLS && i < N) ? half_var(a, a.VX[(size_t)b * N + i]) : (T)0.5;
-    r1[k] = r2[k] = INF;
-    p1[k] = p2[k] = (T)0;
-    yc[k] = (T)0;
-    hyc[k] = (T)0.5;
-    vst[k] = i * ES;                          // row offset within a diagonal
-    vnat[k] = i < N ? i * (M - 1) * ES : 0;   // [N, M] offset of (i, d - i) minus d
-    jb[k] = i < N ? -i : INT_MIN / 2;         // column of row i on diagonal d is d + jb
-  }
-  T nr1 = (tid == 0) ? (T)0 : INF, nr2 = INF, np1 = (T)0, np2 = (T)0;
-
-  const int d_first = -kLag * wave;
-  const int steps = (Dn + kLag * (nw - 1) + kSlots - 1) / kSlots * kSlots;
-
-  T rc[PF][ROWS], rq[PF][ROWS];
-  // C (and Q) of diagonal d at byte soffset so = max(d, 0) * ES
-  auto fetch = [&](int d, int so, T* c, T* q) {
-#pragma unroll
-    for (int k = 0; k < ROWS; ++k) {
-      const int vo = (unsigned)(d + jb[k]) < (unsigned)M ? vnat[k] : kOob;
-      c[k] = bC.ld<T>(vo, so);
-      if (SRC == SRC_COST && PEN) q[k] = bQ.ld<T>(vo, so);
-    }
-  };
-  if (SRC != SRC_FEAT1) {
-#pragma unroll
-    for (int u = 0; u < PF; ++u) {
-      const int d = d_first + u;
-      fetch(d, (d > 0 ? d : 0) * ES, rc[u], rq[u]);
-    }
-  }
-
-  // The sweep, instantiated for the edge wavefront (0: its row above is the
-  // border, its entering column comes from a register ring of column loads)
-  // and for the others (row above and columns from the mailbox).
-  auto sweep = [&](auto edge_tag) {
-    constexpr bool EDGE = decltype(edge_tag)::value;
-    T ey_ring[kSlots], evy_ring[kSlots];   // EDGE: column d of ring slot d % kSlots
-    int vcol = 0;                          // EDGE: byte offset of column t0
-    if (EDGE && COLS) {
-#pragma unroll
-      for (int u = 0; u < kSlots; ++u) {
-        ey_ring[u] = col_y(u * ES);
-        evy_ring[u] = col_vy(u * ES);
-      }
-    }
-    Rec4<T> carry = rec0;   // the record used by the first step of the next block
-    // Drain the set-up loads here: the compiler derives each in-loop wait on
-    // a ring register from every path into the loop, and the entry path
-    // would otherwise force a near-full vmcnt wait on every trip.
-    __builtin_amdgcn_s_waitcnt(0);
-    for (int tw = 0; tw < steps; tw += kWindow) {
-      // lane l: byte soffsets of step tw + l (R / P store, C / Q fetch)
-      const int dl = d_first + tw + lane;
-      const int so_st = diag_soff(dl, N, M) * ES;
-      const int so_ld = SRC != SRC_FEAT1 ? (dl + PF > 0 ? dl + PF : 0) * ES : 0;
-      const int tn = min(kWindow, steps - tw);
-    for (int t0 = 0; t0 < tn; t0 += kSlots) {
-      const int half = (t0 / kSlots) & 1;   // mailbox half of this block
-      Rec4<T> rec[kSlots];
-      if (!EDGE) {
-        const Rec4<T>* prev = inbox + (half ^ 1) * kSlots;
-        rec[0] = carry;
-#pragma unroll
-        for (int u = 1; u < kSlots; ++u) rec[u] = prev[u - 1];
-        carry = prev[kSlots - 1];
-      }
-      Rec4<T>* const out = my_out + half * kSlots;
-#pragma unroll
-      for (int u = 0; u < kSlots; ++u) {
-        const int d = d_first + tw + t0 + u;
-        T cc[ROWS], cq[ROWS];
-#pragma unroll
-        for (int k = 0; k < ROWS; ++k) {
-          cc[k] = rc[u % PF][k];
-          cq[k] = rq[u % PF][k];
-        }
-        // the row above the first row on diagonal d-1, and the column
-        // entering the first row on diagonal d
-        Rec4<T> e;
-        if (EDGE)
-          e = {INF, (T)0, ey_ring[u], COLS ? half_var(a, evy_ring[u]) : (T)0.5};
-        else
-          e = rec[u];
-
-        nr2 = nr1;
-        np2 = np1;
-        nr1 = shift_prev(r1[ROWS - 1], e.x);
-        if (PEN) np1 = EDGE ? shift_prev0(p1[ROWS - 1]) : shift_prev(p1[ROWS - 1], e.y);
-        if (COLS) {
-          // the edge wavefront's column operands are wave-uniform: passing
-          // them through readfirstlane gives each shift a fresh copy, so the
-          // ring registers are never tied to (and overwritten by) a shift
-          const T ny = SRC != SRC_FEAT1 ? (T)0
-                       : shift_prev(yc[ROWS - 1], EDGE ? uniform(e.z) : e.z);
-          const T nhy = shift_prev(hyc[ROWS - 1], EDGE ? uniform(e.w) : e.w);
-#pragma unroll
-          for (int k = ROWS - 1; k > 0; --k) {
-            yc[k] = yc[k - 1];
-            hyc[k] = hyc[k - 1];
-          }
-          yc[0] = ny;
-          hyc[0] = nhy;
-        }
-
-        const int so = __builtin_amdgcn_readlane(so_st, t0 + u);
-        T nr[ROWS], np[ROWS];
-#pragma unroll
-        for (int k = 0; k < ROWS; ++k) {
-          const int j = d + jb[k];
-          const bool valid = (unsigned)j < (unsigned)M;
-          const T up = k ? r1[k - 1] : nr1;
-          const T dg = k ? r2[k - 1] : nr2;
-          const T lf = r1[k];
-          T ch, q = (T)0;
-          if (SRC == SRC_COST) {
-            ch = cc[k] * a.k;
-            if (PEN) q = cq[k];
-          } else {
-            T sq;
-            if (SRC == SRC_FEAT1) {
-              const T df = xr[k] - yc[k];
-              sq = df * df;
-            } else {
-              sq = cc[k] > (T)0 ? cc[k] : (T)0;
-            }
-            const T var = fmax(hxr[k] + hyc[k], a.eps);   // max((vx + vy) / 2, eps)
-            ch = sq * (rcp(var) * a.k);
-            if (PEN) q = a.beta_ln2 * lg2(var);
-          }
-          const T m = min3(dg, up, lf);
-          const T ed = ex2(m - dg), eu = ex2(m - up), el = ex2(m - lf);
-          const T s = ed + eu + el;
-          const T rv = ch + m - lg2(s);
-          bool ok = valid;
-          if (BAND) ok = ok && (m < INF) && (fabs((T)(2 * (row0 + k) - d)) <= a.band);
-          nr[k] = ok ? rv : INF;
-          if (PEN) {
-            const T pup = k ? p1[k - 1] : np1;
-            const T pdg = k ? p2[k - 1] : np2;
-            const T pv = q + (ed * pdg + eu * pup + el * p1[k]) * rcp(s);
-            np[k] = ok ? pv : (T)0;
-          } else {
-            np[k] = (T)0;
-          }
-          const int vo = valid ? vst[k] : kOob;
-          bR.st(nr[k], vo, so);
-          if (PEN) bP.st(np[k], vo, so);
-        }
-#pragma unroll
-        for (int k = 0; k < ROWS; ++k) {
-          r2[k] = r1[k];
-          r1[k] = nr[k];
-          p2[k] = p1[k];
-          p1[k] = np[k];
-        }
-        // The ring reloads are issued after the last use of the slot they
-        // refill, so the slot's register is reused in place and the loop back
-        // edge needs no copies (nor the waits they imply).
-        __builtin_amdgcn_sched_barrier(0);
-        if (SRC != SRC_FEAT1)
-          fetch(d + PF, __builtin_amdgcn_readlane(so_ld, t0 + u), rc[u % PF], rq[u % PF]);
-        if (EDGE && COLS) {
-          ey_ring[u] = col_y(vcol + (u + kSlots) * ES);
-          evy_ring[u] = col_vy(vcol + (u + kSlots) * ES);
-        }
-        out[u] = {r1[ROWS - 1], p1[ROWS - 1], yc[ROWS - 1], hyc[ROWS - 1]};
-      }
-      block_barrier();
-      vcol += kSlots * ES;
-    }
-    }
-  };
-  if (wave == 0)
-    sweep(std::true_type{});
-  else
-    sweep(std::false_type{});
-  // cell (N-1, M-1) is the last element of the diagonal-major R / P; the
-  // thread that stored it reads it back
-  if (row0 <= N - 1 && N - 1 < row0 + ROWS) {
-    const int so = (int)(NM - 1) * ES;
-    const T rl = bR.ld<T>(0, so);
-    a.out_r[b] = rl < INF ? rl * a.inv_k : INF;
-    a.out_p[b] = PEN ? bP.ld<T>(0, so) : (T)0;
-  }
-}
-
-template <typename T, int ROWS, int SRC, bool PEN, bool BAND, int PF>
-__global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwArgs<T> a) {
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  constexpr int ES = sizeof(T);
-  constexpr bool COLS = SRC != SRC_COST;
-  const int N = a.N, M = a.M;
-  const int b = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const T INF = inf_v<T>();
-  const long long NM = (long long)N * M;
-  const bool vgrad = COLS && a.dVX != nullptr;
-  const int Dn = N + M - 1;
-
-  // Rows are bottom-aligned: row N-1 is the last row of the last wavefront,
-  // where every column enters the backward sweep.
-  const int row0 = tid * ROWS - ((int)blockDim.x * ROWS - N);
-
-  // box[(v + 1) * kBox + slot]: wavefront v's inbox, the row below its last
-  // row: (E, G, H, A) and (y, hy, dy sum, dvy sum); box[0..kBox) is
-  // wavefront 0's unread outbox. Then the dump area.
-  Rec8<T>* box = reinterpret_cast<Rec8<T>*>(smem_raw);
-  Rec8<T>* dump = box + (nw + 1) * kBox;
-  const Rec8<T> rec0 = {{-INF, (T)0, (T)0, (T)0}, {(T)0, (T)0.5, (T)0, (T)0}};
-  for (int t = tid; t < (nw + 1) * kBox; t += blockDim.x) box[t] = rec0;
-
-  Buf bR, bP, bC, bQ, bdC, bdQ, bY, bVY, bdY, bdVY;
-  bR.init(a.R + b * NM, NM);
-  if (PEN) bP.init(a.P + b * NM, NM);
-  if (SRC != SRC_FEAT1) {
-    bC.init(a.C + b * NM, NM);
-    bdC.init(a.dC + b * NM, NM);
-  }
-  const bool want_dq = SRC == SRC_COST && PEN && a.dQ != nullptr;
-  if (SRC == SRC_COST && PEN) {
-    bQ.init(a.Q + b * NM, NM);
-    // no penalty gradient wanted: its stores go to an empty buffer (dropped)
-    bdQ.init(want_dq ? a.dQ + b * NM : a.Q, want_dq ? NM : 0);
-  }
-  if (SRC == SRC_FEAT1) {
-    bY.init(a.Y + (size_t)b * M, M);
-    bdY.init(a.dY + (size_t)b * M, M);
-  }
-  if (COLS) bVY.init(a.VY + (size_t)b * M, M);
-  // without variance gradients the column sums are still formed (no branch in
-  // the sweep) and their stores go to an empty buffer, which drops them
-  if (COLS) bdVY.init(vgrad ? a.dVY + (size_t)b * M : a.VY, vgrad ? M : 0);
-  // column operands of the edge wavefront at byte offset vcol (lane uniform);
-  // columns before the first fail the range check and read 0
-  auto col_y = [&](int vcol) -> T { return SRC == SRC_FEAT1 ? bY.ld<T>(vcol, 0) : (T)0; };
-  auto col_vy = [&](int vcol) -> T { return COLS ? bVY.ld<T>(vcol, 0) : (T)1; };
-
-  const bool last_wave = wave == nw - 1;
-  Rec8<T>* const inbox = box + (wave + 1) * kBox;
-  Rec8<T>* const outbox = box + wave * kBox;
-  Rec8<T>* const my_out = lane == 0 ? outbox : dump + lane;
-  __syncthreads();
-
-  T xr[ROWS], hxr[ROWS], dxr[ROWS], dvr[ROWS];
-  T e1[ROWS], e2[ROWS], g1[ROWS], g2[ROWS], h1[ROWS], h2[ROWS], a1[ROWS], a2[ROWS];
-  T yc[ROWS], hyc[ROWS], cy[ROWS], cvy[ROWS];
-  int vst[ROWS], vnat[ROWS], jb[ROWS], vrow0[ROWS];
-#pragma unroll
-  for (int k = 0; k < ROWS; ++k) {
-    const int i = row0 + k;
-    const bool in = i >= 0 && i < N;
-    xr[k] = (SRC == SRC_FEAT1 && in) ? a.X[(size_t)b * N + i] : (T)0;
-    hxr[k] = (COLS && in) ? half_var(a, a.VX[(size_t)b * N + i]) : (T)0.5;
-    dxr[k] = dvr[k] = (T)0;
-    e1[k] = e2[k] = -INF;
-    g1[k] = g2[k] = h1[k] = h2[k] = a1[k] = a2[k] = (T)0;
-    yc[k] = cy[k] = cvy[k] = (T)0;
-    hyc[k] = (T)0.5;
-    vst[k] = in ? i * ES : 0;
-    vnat[k] = in ? i * (M - 1) * ES : 0;
-    jb[k] = in ? -i : INT_MIN / 2;
-    vrow0[k] = i == 0 ? 0 : kOob;   // the row that stores finished columns
-  }
-  // Row below the last row on the two previous diagonals. The virtual cell
-  // (N, M) on diagonal Dn+1 is given E = Rh(N-1, M-1), A = P(N-1, M-1) and the
-  // incoming gradients, so the recursion yields grad_dist / grad_pen at
-  // (N-1, M-1) without a special case.
-  T ne1 = -INF, ne2 = -INF, ng1 = 0, ng2 = 0, nh1 = 0, nh2 = 0, na1 = 0, na2 = 0;
-  if (last_wave && lane == 63) {
-    const int so = (int)(NM - 1) * ES;
-    ne1 = bR.ld<T>(0, so);
-    ng1 = a.gr[(size_t)b * a.gstride];
-    if (PEN) {
-      nh1 = a.gp[(size_t)b * a.gstride];
-      na1 = bP.ld<T>(0, so);
-    }
-  }
-
-  const int d_first = Dn - 1 + kLag * (nw - 1 - wave);
-  const int steps = (Dn + kLag * (nw - 1) + kSlots - 1) / kSlots * kSlots;
-
-  T rr[PF][ROWS], rp[PF][ROWS], rc[PF][ROWS], rq[PF][ROWS];
-  // R, P of diagonal d at byte soffset so_d = soff(d) * ES (diagonal-major),
-  // C, Q at so_n = max(d, 0) * ES ([N, M])
-  auto fetch = [&](int d, int so_d, int so_n, T* r, T* p, T* c, T* q) {
-#pragma unroll
-    for (int k = 0; k < ROWS; ++k) {
-      const bool v = (unsigned)(d + jb[k]) < (unsigned)M;
-      const int vd = v ? vst[k] : kOob;
-      r[k] = bR.ld<T>(vd, so_d);
-      if (PEN) p[k] = bP.ld<T>(vd, so_d);
-      if (SRC != SRC_FEAT1) {
-        const int vn = v ? vnat[k] : kOob;
-        c[k] = bC.ld<T>(vn, so_n);
-        if (SRC == SRC_COST && PEN) q[k] = bQ.ld<T>(vn, so_n);
-      }
-    }
-  };
-#pragma unroll
-  for (int u = 0; u < PF; ++u) {
-    const int d = d_first - u;
-    fetch(d, diag_soff(d, N, M) * ES, (d > 0 ? d : 0) * ES, rr[u], rp[u], rc[u], rq[u]);
-  }
-
-  // The sweep, instantiated for the edge wavefront (the last: its row below
-  // is the virtual row N, its entering column comes from a register ring of
-  // column loads) and for the others (row below and columns from the mailbox).
-  auto sweep = [&](auto edge_tag) {
-    constexpr bool EDGE = decltype(edge_tag)::value;
-    // EDGE: ring slot u of a trip holds column M-1-t0-u, the one entering row
-    // N-1 on that step's diagonal
-    T ey_ring[kSlots], evy_ring[kSlots];
-    int vcol = (M - 1) * ES;   // EDGE: byte offset of column M-1-t0
-    if (EDGE && COLS) {
-#pragma unroll
-      for (int u = 0; u < kSlots; ++u) {
-        ey_ring[u] = col_y(vcol - u * ES);
-        evy_ring[u] = col_vy(vcol - u * ES);
-      }
-    }
-    Rec8<T> carry = rec0;   // the record used by the first step of the next block
-    __builtin_amdgcn_s_waitcnt(0);   // drain the set-up loads (as in the forward)
-    for (int tw = 0; tw < steps; tw += kWindow) {
-      // lane l: byte soffsets of step tw + l (fetch of R / P and C / Q, and
-      // the stores of the step's own diagonal)
-      const int dl = d_first - tw - lane;
-      const int so_fd = diag_soff(dl - PF, N, M) * ES;
-      const int so_fn = SRC != SRC_FEAT1 ? (dl - PF > 0 ? dl - PF : 0) * ES : 0;
-      const int so_st = (dl > 0 ? dl : 0) * ES;
-      const int tn = min(kWindow, steps - tw);
-    for (int t0 = 0; t0 < tn; t0 += kSlots) {
-      const int half = (t0 / kSlots) & 1;   // mailbox half of this block
-      Rec8<T> rec[kSlots];
-      if (!EDGE) {
-        const Rec8<T>* prev = inbox + (half ^ 1) * kSlots;
-        rec[0] = carry;
-#pragma unroll
-        for (int u = 1; u < kSlots; ++u) {
-          rec[u].a = prev[u - 1].a;
-          if (COLS) rec[u].b = prev[u - 1].b;
-        }
-        carry.a = prev[kSlots - 1].a;
-        if (COLS) carry.b = prev[kSlots - 1].b;
-      }
-      Rec8<T>* const out = my_out + half * kSlots;
-#pragma unroll
-      for (int u = 0; u < kSlots; ++u) {
-        const int d = d_first - tw - t0 - u;
-        T cr[ROWS], cp[ROWS], cc[ROWS], cq[ROWS];
-  #pragma unroll
-        for (int k = 0; k < ROWS; ++k) {
-          cr[k] = rr[u % PF][k];
-          cp[k] = rp[u % PF][k];
-          cc[k] = rc[u % PF][k];
-          cq[k] = rq[u % PF][k];
-        }
-        // the row below the last row on diagonal d+1, and the column entering
-        // the last row on diagonal d
-        Rec8<T> ex;
-        if (EDGE)
-          ex = {{-INF, (T)0, (T)0, (T)0},
-                {ey_ring[u], COLS ? half_var(a, evy_ring[u]) : (T)0.5, (T)0, (T)0}};
-        else
-          ex = rec[u];
-
-        ne2 = ne1;
-        ng2 = ng1;
-        nh2 = nh1;
-        na2 = na1;
-        ne1 = shift_next(e1[0], ex.a.x);
-        ng1 = EDGE ? shift_next0(g1[0]) : shift_next(g1[0], ex.a.y);
-        if (PEN) {
-          nh1 = EDGE ? shift_next0(h1[0]) : shift_next(h1[0], ex.a.z);
-          na1 = EDGE ? shift_next0(a1[0]) : shift_next(a1[0], ex.a.w);
-        }
-        if (COLS) {
-          const T fy = SRC != SRC_FEAT1 ? (T)0
-                       : shift_next(yc[0], EDGE ? uniform(ex.b.x) : ex.b.x);
-          const T fhy = shift_next(hyc[0], EDGE ? uniform(ex.b.y) : ex.b.y);
-          const T fcy = SRC != SRC_FEAT1 ? (T)0 : EDGE ? shift_next0(cy[0]) : shift_next(cy[0], ex.b.z);
-          const T fcvy = EDGE ? shift_next0(cvy[0]) : shift_next(cvy[0], ex.b.w);
-  #pragma unroll
-          for (int k = 0; k + 1 < ROWS; ++k) {
-            yc[k] = yc[k + 1];
-            hyc[k] = hyc[k + 1];
-            cy[k] = cy[k + 1];
-            cvy[k] = cvy[k + 1];
-          }
-          yc[ROWS - 1] = fy;
-          hyc[ROWS - 1] = fhy;
-          cy[ROWS - 1] = fcy;
-          cvy[ROWS - 1] = fcvy;
-        }
-
-        const int so_n = __builtin_amdgcn_readlane(so_st, t0 + u);
-        T xe[ROWS], xg[ROWS], xh[ROWS], xa[ROWS];
-  #pragma unroll
-        for (int k = 0; k < ROWS; ++k) {
-          const bool valid = (unsigned)(d + jb[k]) < (unsigned)M;
-          const T rk = valid ? cr[k] : INF;
-          const T pk = cp[k];
-          T ch, q = (T)0, c = (T)0, rv = (T)1, sq_raw = (T)0, var_raw = (T)1;
-          if (SRC == SRC_COST) {
-            ch = cc[k] * a.k;
-            if (PEN) q = cq[k];
-          } else {
-            if (SRC == SRC_FEAT1) {
-              const T df = xr[k] - yc[k];
-              sq_raw = df * df;
-            } else {
-              sq_raw = cc[k];
-            }
-            const T sq = sq_raw > (T)0 ? sq_raw : (T)0;
-            var_raw = hxr[k] + hyc[k];
-            const T var = fmax(var_raw, a.eps);
-            rv = rcp(var);
-            c = sq * rv;
-            ch = c * a.k;
-            if (PEN) q = a.beta_ln2 * lg2(var);
-          }
-          // successors: down (i+1, j) and right (i, j+1) on d+1, diagonal (i+1, j+1) on d+2
-          const T edn = (k + 1 < ROWS) ? e1[k + 1] : ne1;
-          const T gdn = (k + 1 < ROWS) ? g1[k + 1] : ng1;
-          const T edg = (k + 1 < ROWS) ? e2[k + 1] : ne2;
-          const T gdg = (k + 1 < ROWS) ? g2[k + 1] : ng2;
-          const T wdn = ex2(edn - rk), wrt = ex2(e1[k] - rk), wdg = ex2(edg - rk);
-          T g = wdn * gdn + wrt * g1[k] + wdg * gdg;
-          T h = (T)0;
-          if (PEN) {
-            const T hdn = (k + 1 < ROWS) ? h1[k + 1] : nh1;
-            const T adn = (k + 1 < ROWS) ? a1[k + 1] : na1;
-            const T hdg = (k + 1 < ROWS) ? h2[k + 1] : nh2;
-            const T adg = (k + 1 < ROWS) ? a2[k + 1] : na2;
-            const T wh_dn = wdn * hdn, wh_rt = wrt * h1[k], wh_dg = wdg * hdg;
-            g -= (wh_dn * (pk - adn) + wh_rt * (pk - a1[k]) + wh_dg * (pk - adg)) * a.inv_gamma;
-            h = wh_dn + wh_rt + wh_dg;
-          }
-          // outside the grid, and (band) at unreachable cells, nothing flows
-          bool live = valid;
-          if (BAND) live = live && rk < INF;
-          g = live ? g : (T)0;
-          h = live ? h : (T)0;
-          xe[k] = live ? rk - ch : -INF;
-          xg[k] = g;
-          xh[k] = h;
-          xa[k] = valid ? pk - q : (T)0;
-
-          const int vn = valid ? vnat[k] : kOob;
-          if (SRC == SRC_COST) {
-            bdC.st(g, vn, so_n);
-            if (PEN) bdQ.st(h, vn, so_n);
-          } else {
-            const T dsq = sq_raw > (T)0 ? g * rv : (T)0;
-            if (SRC == SRC_SQ) bdC.st(dsq, vn, so_n);
-            if (SRC == SRC_FEAT1) {
-              const T df = valid ? (T)2 * dsq * (xr[k] - yc[k]) : (T)0;
-              dxr[k] += df;
-              cy[k] -= df;
-            }
-            {
-              T dvar = var_raw > a.eps ? (T)0.5 * (a.beta * h - g * c) * rv : (T)0;
-              dvar = valid ? dvar : (T)0;
-              dvr[k] += dvar;
-              cvy[k] += dvar;
-            }
-            // column d leaves the sweep at row 0: store its sums
-            const int vc = ((unsigned)d < (unsigned)M) ? vrow0[k] : kOob;
-            if (SRC == SRC_FEAT1) bdY.st(cy[k], vc, so_n);
-            bdVY.st(cvy[k], vc, so_n);
-          }
-        }
-  #pragma unroll
-        for (int k = 0; k < ROWS; ++k) {
-          e2[k] = e1[k];
-          e1[k] = xe[k];
-          g2[k] = g1[k];
-          g1[k] = xg[k];
-          h2[k] = h1[k];
-          h1[k] = xh[k];
-          a2[k] = a1[k];
-          a1[k] = xa[k];
-        }
-        // ring reloads only now (see the forward)
-        __builtin_amdgcn_sched_barrier(0);
-        fetch(d - PF, __builtin_amdgcn_readlane(so_fd, t0 + u),
-              __builtin_amdgcn_readlane(so_fn, t0 + u), rr[u % PF], rp[u % PF], rc[u % PF],
-              rq[u % PF]);
-        if (EDGE && COLS) {
-          ey_ring[u] = col_y(vcol - (u + kSlots) * ES);
-          evy_ring[u] = col_vy(vcol - (u + kSlots) * ES);
-        }
-        if (COLS) {
-          out[u] = {{e1[0], g1[0], h1[0], a1[0]}, {yc[0], hyc[0], cy[0], cvy[0]}};
-        } else {
-          out[u].a = {e1[0], g1[0], h1[0], a1[0]};
-        }
-      }
-      block_barrier();
-      vcol -= kSlots * ES;
-    }
-    }
-  };
-  if (last_wave)
-    sweep(std::true_type{});
-  else
-    sweep(std::false_type{});
-#pragma unroll
-  for (int k = 0; k < ROWS; ++k) {
-    const int i = row0 + k;
-    if (i >= 0 && i < N) {
-      if (SRC == SRC_FEAT1) a.dX[(size_t)b * N + i] = dxr[k];
-      if (vgrad) a.dVX[(size_t)b * N + i] = dvr[k];
-    }
-  }
-}
-
-// ---------------------------------------------------------------- launching
-
-struct Shape {
-  int rows;
-  int threads;
-};
-
-// Rows per thread and threads per pair for a grid with N rows (N <= M).
-// Up to 4 wavefronts (one per SIMD of a CU), more rows per thread beyond.
-static Shape pick_shape(int N) {
-  int rows = 1;
-  while (rows < 16 && (N + rows - 1) / rows > 256) rows *= 2;
-  // tuning override: TORCHWARP_UDTW_ROWS = 1, 2, 4, 8 or 16 rows per thread,
-  // taken when the kernel's thread limit for that row count allows it
-  static const int forced = [] {
-    const char* e = getenv("TORCHWARP_UDTW_ROWS");
-    return e ? atoi(e) : 0;
-  }();
-  if ((forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16) &&
-      (N + forced - 1) / forced <= (forced >= 16 ? 1024 : 256))
-    rows = forced;
-  int threads = (N + rows - 1) / rows;
-  if (threads > 1024) return {0, 0};
-  threads = ((threads + 63) / 64) * 64;
-  return {rows, threads};
-}
-
-// LDS of one workgroup: the mailbox rings and the dump area of the
-// mailbox stores (records of 4 values forward, 8 backward).
-template <typename T>
-static size_t udtw_lds(bool backward, int nw) {
-  return (size_t)((nw + 1) * kBox + kDump) * (backward ? 8 : 4) * sizeof(T);
-}
-
-// Prefetch depth (diagonals) of the register ring for a row count.
-template <int ROWS>
-struct PrefetchDepth {
-  static constexpr int value = ROWS == 1 ? 4 : (ROWS == 2 ? 2 : 1);
-};
-
-template <typename T, int SRC, bool PEN, bool BAND>
-static int launch_udtw(bool backward, const UdtwArgs<T>& a, int B, hipStream_t stream,
-                       const char* what) {
-  if (B == 0) return TW_OK;
-  const Shape sh = pick_shape(a.N);
-  if (sh.rows == 0) {
-    return fail(TW_ESIZE, "%s: the shorter sequence has %d steps; this build handles up to 16384",
-                what, a.N);
-  }
-  if ((long long)a.N * a.M * (long long)sizeof(T) >= (1LL << 31)) {
-    return fail(TW_ESIZE, "%s: one pair's N*M matrix must stay below 2 GiB", what);
-  }
-  const int nw = sh.threads / 64;
-  const size_t lds = udtw_lds<T>(backward, nw);
-  if (lds > (size_t)max_lds_bytes()) {
-    return fail(TW_ESIZE, "%s: %zu bytes of LDS needed, %d available", what, lds,
-                max_lds_bytes());
-  }
-  dim3 grid(B), block(sh.threads);
-#define TW_UDTW_CASE(R_)                                                                     \
-  case R_:                                                                                   \
-    if (backward)                                                                            \
-      hipLaunchKernelGGL(                                                                    \
-          (udtw_bwd_kernel<T, R_, SRC, PEN, BAND, PrefetchDepth<R_>::value>), grid, block,   \
-          lds, stream, a);                                                                   \
-    else                                                                                     \
-      hipLaunchKernelGGL(                                                                    \
-          (udtw_fwd_kernel<T, R_, SRC, PEN, BAND, PrefetchDepth<R_>::value>), grid, block,   \
-          lds, stream, a);                                                                   \
-    break;
-  switch (sh.rows) {
-    TW_UDTW_CASE(1)
-    TW_UDTW_CASE(2)
-    TW_UDTW_CASE(4)
-    TW_UDTW_CASE(8)
-    TW_UDTW_CASE(16)
-    default:
-      return fail(TW_EINVAL, "%s: internal: bad row count", what);
-  }
-#undef TW_UDTW_CASE
-  return check_launch(what);
-}
-
 template <typename T, int SRC>
 static int launch_pen(bool pen, bool backward, const UdtwArgs<T>& a, int B, hipStream_t s,
                       const char* what) {
-  const bool band = a.band > (T)0;
-  if (pen)
-    return band ? launch_udtw<T, SRC, true, true>(backward, a, B, s, what)
-                : launch_udtw<T, SRC, true, false>(backward, a, B, s, what);
-  return band ? launch_udtw<T, SRC, false, true>(backward, a, B, s, what)
-              : launch_udtw<T, SRC, false, false>(backward, a, B, s, what);
+  return backward ? launch_sweep<T, SRC, true>(pen, a, B, s, what)
+                  : launch_sweep<T, SRC, false>(pen, a, B, s, what);
 }
 
 template <typename T>
