@@ -27,6 +27,7 @@ import torch
 HBM_PEAK_GBS = 8000.0
 METRIC = ("DP cells/sec & pairs/sec fwd+bwd (uDTW B=256 N=M=140; JEANIE K=25), "
           "% HBM roofline")
+SETTLE_S = 0.25    # minimum untimed warm-up per config (seconds)
 LAST_TIMES = {}   # label -> mean ms of every kernel timed by the last _hip_call_times
 CONFIGS = ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5a", "cfg5b")
 
@@ -260,8 +261,15 @@ def run_config(name, steps, warmup):
     dev = torch.device("cuda", 0)
     inputs = make_inputs(name, dev)
     f = step_fn(name, inputs)
-    for _ in range(warmup):
+    # W warmup steps, continued until at least SETTLE_S seconds have passed so
+    # the GPU's clocks have left their idle state before the timed steps
+    t_w = time.perf_counter()
+    n = 0
+    while n < warmup or time.perf_counter() - t_w < SETTLE_S:
         f()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize(dev)
     torch.cuda.synchronize(dev)
     t0 = time.perf_counter()
     for _ in range(steps):

@@ -193,27 +193,6 @@ static int feat_fwd(const T* X, const T* Y, const T* vx, const T* vy, int B, int
   return launch_pen<T, SRC_SQ>(pen, false, a, B, s, what);
 }
 
-// d sigma = 2 sigma d var, in place over the variance gradients of both sides
-template <typename T>
-__global__ void __launch_bounds__(256) sigma_grad_kernel(const T* __restrict__ sx,
-                                                         const T* __restrict__ sy, T* dsx, T* dsy,
-                                                         long long nx, long long ny) {
-  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < nx)
-    dsx[i] *= (T)2 * sx[i];
-  else if (i < nx + ny)
-    dsy[i - nx] *= (T)2 * sy[i - nx];
-}
-
-template <typename T>
-static int sigma_grads(const T* sx, const T* sy, T* dsx, T* dsy, long long nx, long long ny,
-                       hipStream_t s, const char* what) {
-  const long long n = nx + ny;
-  hipLaunchKernelGGL((sigma_grad_kernel<T>), dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-                     sx, sy, dsx, dsy, nx, ny);
-  return check_launch(what);
-}
-
 template <typename T>
 static int feat_bwd(const T* X, const T* Y, const T* vx, const T* vy, const T* R, const T* P,
                     const T* gr, const T* gp, int B, int N, int M, int D, double gamma,
@@ -242,15 +221,12 @@ static int feat_bwd(const T* X, const T* Y, const T* vx, const T* vy, const T* R
   a.gstride = gstride;
   set_hyper(a, gamma, beta, eps, band);
   set_sigma(a, sigma);
-  const bool sig_grads = sigma && dvx != nullptr;
   if (D == 1) {
     a.X = X;
     a.Y = Y;
     a.dX = dX;
     a.dY = dY;
-    if (int e = launch_pen<T, SRC_FEAT1>(pen, true, a, B, s, what)) return e;
-    return sig_grads ? sigma_grads<T>(vx, vy, dvx, dvy, (long long)B * N, (long long)B * M, s, what)
-                     : TW_OK;
+    return launch_pen<T, SRC_FEAT1>(pen, true, a, B, s, what);
   }
   const size_t need = (size_t)B * N * M * sizeof(T);
   if (!ws || ws_bytes < need)
@@ -261,9 +237,7 @@ static int feat_bwd(const T* X, const T* Y, const T* vx, const T* vy, const T* R
   a.C = ws;
   a.dC = ws;
   if (int e = launch_pen<T, SRC_SQ>(pen, true, a, B, s, what)) return e;
-  if (int e = sqdist_raw_bwd<T>(X, Y, ws, B, N, M, D, dX, dY, s, what)) return e;
-  return sig_grads ? sigma_grads<T>(vx, vy, dvx, dvy, (long long)B * N, (long long)B * M, s, what)
-                   : TW_OK;
+  return sqdist_raw_bwd<T>(X, Y, ws, B, N, M, D, dX, dY, s, what);
 }
 
 }  // namespace tw

@@ -810,12 +810,17 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
     sweep(std::true_type{});
   else
     sweep(std::false_type{});
+  // Variance gradients are d/dv of the variance inputs; when those are
+  // standard deviations s (v = s^2) the gradient is d/ds = 2 s d/dv.
 #pragma unroll
   for (int k = 0; k < ROWS; ++k) {
     const int i = row0 + k;
     if (i >= 0 && i < N) {
       if (SRC == SRC_FEAT1) a.dX[(size_t)b * N + i] = dxr[k];
-      if (vgrad) a.dVX[(size_t)b * N + i] = dvr[k];
+      if (vgrad) {
+        const T sx = a.VX[(size_t)b * N + i];
+        a.dVX[(size_t)b * N + i] = a.sigma ? (T)2 * sx * dvr[k] : dvr[k];
+      }
     }
   }
   if (LC) {
@@ -828,7 +833,19 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
         svy += acc[v * ncol + cpad + j].hy;
       }
       if (SRC == SRC_FEAT1) a.dY[(size_t)b * M + j] = sy;
-      if (vgrad) a.dVY[(size_t)b * M + j] = svy;
+      if (vgrad) {
+        const T sy_in = a.VY[(size_t)b * M + j];
+        a.dVY[(size_t)b * M + j] = a.sigma ? (T)2 * sy_in * svy : svy;
+      }
+    }
+  } else if (FLOW && a.sigma && vgrad) {
+    // the sweep stored d/dv of every column; once all of its stores are
+    // complete and visible, scale them to d/ds
+    __threadfence();
+    __syncthreads();
+    for (int j = tid; j < M; j += blockDim.x) {
+      const size_t o = (size_t)b * M + j;
+      a.dVY[o] = (T)2 * a.VY[o] * a.dVY[o];
     }
   }
 }
