@@ -1,6 +1,6 @@
 """Benchmark of the torchwarp alignment hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--config cfg2] [--all] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--config cfg2] [--all] [--no-cpu] [--eager]
     python bench.py --copy-probe      # HBM counter calibration: 5 copies of 256 MiB
 
 A "step" is one forward + loss + backward of the configured alignment loss on
@@ -8,6 +8,12 @@ synthetic inputs already resident in HBM (inputs are
 drawn from a CPU ``torch.Generator().manual_seed(0)`` in config order, then
 moved to the GPU). The headline workload is configs[1]: uDTW fp32 fwd+bwd,
 B=256, N=M=140, D=1 -- metric "DP cells/s" (N*M*B per step / step time).
+
+The step goes through the public API. It is captured once as a HIP graph and
+the timed steps are graph replays, so the figure is the GPU's, not the host's:
+an eager step costs 0.1-0.2 ms of Python and autograd-engine work on the host,
+as much as the kernels. The eager step is timed beside it
+(``config.eager_ms_per_step``); ``--eager`` makes it the headline.
 
 One JSON line is printed with ``roofline`` for the dominant kernel (algorithmic
 bytes per launch / its mean duration, timed with HIP events on the stream the
@@ -29,6 +35,7 @@ METRIC = ("DP cells/sec & pairs/sec fwd+bwd (uDTW B=256 N=M=140; JEANIE K=25), "
           "% HBM roofline")
 SETTLE_S = 0.25    # minimum untimed warm-up per config (seconds)
 LAST_TIMES = {}   # label -> mean ms of every kernel timed by the last _hip_call_times
+EAGER_MS = {}     # config -> ms per eagerly run step (run_config with mode "eager"/"both")
 CONFIGS = ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5a", "cfg5b")
 
 
@@ -257,12 +264,32 @@ def cpu_baseline(name, budget_s=10.0):
 
 # -------------------------------------------------------------------- main
 
-def run_config(name, steps, warmup):
-    dev = torch.device("cuda", 0)
-    inputs = make_inputs(name, dev)
-    f = step_fn(name, inputs)
-    # W warmup steps, continued until at least SETTLE_S seconds have passed so
-    # the GPU's clocks have left their idle state before the timed steps
+def graphed(f, dev):
+    """The step ``f`` captured once as a HIP graph (torch.cuda.graph); returns
+    its replay. A replay launches every kernel of the eager step -- forward,
+    loss, backward -- on the same device-resident inputs, with the host's
+    per-step Python and autograd-engine work taken out of the loop. The
+    library allocates nothing, synchronises nothing and records no memset,
+    so the step captures as is (tests/test_gpu_graph.py checks replays
+    against eager steps)."""
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            f()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        f()
+    torch.cuda.synchronize(dev)
+    return g.replay
+
+
+def _time_steps(f, dev, steps, warmup):
+    """ms per step of ``f`` over exactly ``steps`` steps, bracketed by
+    synchronisations, after ``warmup`` untimed steps (continued until at least
+    SETTLE_S seconds have passed, so the GPU's clocks have left their idle
+    state before the timed steps)."""
     t_w = time.perf_counter()
     n = 0
     while n < warmup or time.perf_counter() - t_w < SETTLE_S:
@@ -275,7 +302,19 @@ def run_config(name, steps, warmup):
     for _ in range(steps):
         f()
     torch.cuda.synchronize(dev)
-    ms = (time.perf_counter() - t0) * 1e3 / steps
+    return (time.perf_counter() - t0) * 1e3 / steps
+
+
+def run_config(name, steps, warmup, mode="graph"):
+    """Time one config: ``mode`` "graph" replays the captured step, "eager"
+    runs it through Python and the autograd engine every time, "both" times
+    both (the graph figure is returned, the eager one in ``EAGER_MS``)."""
+    dev = torch.device("cuda", 0)
+    inputs = make_inputs(name, dev)
+    f = step_fn(name, inputs)
+    if mode in ("eager", "both"):
+        EAGER_MS[name] = _time_steps(f, dev, steps, warmup)
+    ms = EAGER_MS[name] if mode == "eager" else _time_steps(graphed(f, dev), dev, steps, warmup)
     w = work(name)
     return inputs, ms, w["cells"] / (ms * 1e-3), w["pairs"] / (ms * 1e-3)
 
@@ -288,6 +327,8 @@ def main():
     ap.add_argument("--config", default="cfg2", choices=CONFIGS)
     ap.add_argument("--all", action="store_true", help="also time every config (stderr)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--eager", action="store_true",
+                    help="time eager steps only (default: graph replays, eager timed beside)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run 5 device copies of 256 MiB (calibrates FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -307,7 +348,8 @@ def main():
         sys.exit(2)
 
     name = args.config
-    inputs, ms, cells_s, pairs_s = run_config(name, args.steps, args.warmup)
+    mode = "eager" if args.eager else "both"
+    inputs, ms, cells_s, pairs_s = run_config(name, args.steps, args.warmup, mode)
     kt = _hip_call_times(name, inputs, max(args.steps, 10))
     roof = None
     if kt is not None:
@@ -330,17 +372,20 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {"workload": name, "pairs_per_s": round(pairs_s, 1), "cells": work(name)["cells"],
-                   "pairs": work(name)["pairs"]},
+                   "pairs": work(name)["pairs"],
+                   "timing": ("eager steps" if args.eager else
+                              "HIP-graph replays of the public-API step (forward, loss, backward)"),
+                   "eager_ms_per_step": round(EAGER_MS[name], 5)},
         "roofline": roof,
         "cpu_baseline": None if args.no_cpu else cpu_baseline(name),
     }
     print(json.dumps(line), flush=True)
     if args.all:
         for other in CONFIGS:
-            inp, oms, oc, op = run_config(other, max(5, args.steps // 3), 2)
+            inp, oms, oc, op = run_config(other, max(10, args.steps), 2, mode)
             kt = _hip_call_times(other, inp, 10)
             rec = {"config": other, "ms_per_step": round(oms, 4), "cells_per_s": round(oc, 1),
-                   "pairs_per_s": round(op, 1)}
+                   "pairs_per_s": round(op, 1), "eager_ms_per_step": round(EAGER_MS[other], 4)}
             if kt is not None:
                 rec.update(kernel=kt[0], kernel_ms=round(kt[1], 5),
                            hbm_frac=round(kt[2] / (kt[1] * 1e-3) / 1e9 / HBM_PEAK_GBS, 5))

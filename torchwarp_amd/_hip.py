@@ -140,6 +140,19 @@ def udtw_workspace_elems(B, N, M, D):
     return library().tw_udtw_feat_workspace_bytes(B, N, M, D, 1)
 
 
+def dense(dtype, *tensors, contiguous=True):
+    """The tensors in ``dtype`` (and contiguous), converting only those that
+    need it."""
+    out = []
+    for t in tensors:
+        if t.dtype != dtype:
+            t = t.to(dtype)
+        if contiguous and not t.is_contiguous():
+            t = t.contiguous()
+        out.append(t)
+    return out
+
+
 def per_pair(*grads):
     """Per-pair gradient tensors [B] and their common element stride: a stride-0
     expansion (a mean's backward) is passed as is, anything else contiguous."""

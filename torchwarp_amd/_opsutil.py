@@ -10,6 +10,7 @@ autograd-native restatement.
 
 import torch
 from torch import Tensor
+from torch.autograd import forward_ad as _fwad
 
 
 def register_vmap(op, n_tensors):
@@ -93,13 +94,25 @@ def direct(op):
     return call
 
 
-def pick(cls, compiled):
+def _records_nothing(args):
+    """True when ``Function.apply`` would record no graph: grad mode off, no
+    forward-mode dual level entered, and a plain eager call (as for
+    :func:`plain_eager`). The backward of a first-order ``backward()`` runs
+    this way, so its VJP Function then reduces to its forward."""
+    if torch.is_grad_enabled() or _fwad._current_level >= 0:
+        return False
+    return plain_eager(args)
+
+
+def pick(cls, compiled, forward=None):
     """``cls.apply``, with the compiled twin while torch.compile traces.
 
     With all arguments given positionally and no functorch transform active,
     ``Function.apply`` only adds a per-call ``inspect.signature`` binding of
     default arguments before the C++ apply; the plain path calls the C++
-    apply directly (dead functorch wrappers are still unwrapped).
+    apply directly (dead functorch wrappers are still unwrapped). When
+    ``forward`` (the Function's forward) is given and the call records
+    nothing (:func:`_records_nothing`), it is called directly.
     """
     base_apply = super(torch.autograd.Function, cls).apply
     unwrap = torch._functorch.utils.unwrap_if_dead
@@ -109,5 +122,7 @@ def pick(cls, compiled):
             return compiled.apply(*args)
         if torch._C._are_functorch_transforms_active():
             return cls.apply(*args)
-        return base_apply(*(unwrap(a) if isinstance(a, Tensor) else a for a in args))
+        if forward is not None and _records_nothing(args):
+            return forward(*args)
+        return base_apply(*[unwrap(a) if isinstance(a, Tensor) else a for a in args])
     return apply

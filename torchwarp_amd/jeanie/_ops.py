@@ -143,8 +143,8 @@ class PairBackward(torch.autograd.Function):
         return tuple(jvp_of(PairBackward._first(ctx.metric), (A, Bm, g), tangents))
 
 
-pair_apply = pick(Pair, without_jvp(Pair))
-pair_backward_apply = pick(PairBackward, without_jvp(PairBackward))
+pair_apply = pick(Pair, without_jvp(Pair), Pair.forward)
+pair_backward_apply = pick(PairBackward, without_jvp(PairBackward), PairBackward.forward)
 
 
 # ----------------------------------------------------------- JEANIE, cost
@@ -270,8 +270,8 @@ class DPBackward(torch.autograd.Function):
         return jvp_of(_first_order_dp(*ctx.args, ctx.with_R), saved, tangents)[0]
 
 
-dp_apply = pick(DP, without_jvp(DP))
-dp_backward_apply = pick(DPBackward, without_jvp(DPBackward))
+dp_apply = pick(DP, without_jvp(DP), DP.forward)
+dp_backward_apply = pick(DPBackward, without_jvp(DPBackward), DPBackward.forward)
 
 
 # ------------------------------------------------------- JEANIE, features
@@ -412,8 +412,9 @@ class FeaturesBackward(torch.autograd.Function):
         return jvp_of(_first_order_features(*ctx.args, ctx.with_R), saved, tangents)
 
 
-features_apply = pick(Features, without_jvp(Features))
-features_backward_apply = pick(FeaturesBackward, without_jvp(FeaturesBackward))
+features_apply = pick(Features, without_jvp(Features), Features.forward)
+features_backward_apply = pick(FeaturesBackward, without_jvp(FeaturesBackward),
+                               FeaturesBackward.forward)
 
 
 # ------------------------------------------------------------------- FVM
@@ -529,5 +530,5 @@ class FVMBackward(torch.autograd.Function):
                       (zeros_if_none(t_cost, cost), zeros_if_none(t_go, g_out)))
 
 
-fvm_apply = pick(FVM, without_jvp(FVM))
-fvm_backward_apply = pick(FVMBackward, without_jvp(FVMBackward))
+fvm_apply = pick(FVM, without_jvp(FVM), FVM.forward)
+fvm_backward_apply = pick(FVMBackward, without_jvp(FVMBackward), FVMBackward.forward)

@@ -99,8 +99,7 @@ def fused(X: Tensor, Y: Tensor, vx: Tensor, vy: Tensor, gamma: float, beta: floa
     _hip.require(X, backend, "uDTW")
     B, N, D = X.shape
     M = Y.shape[1]
-    X, Y = X.contiguous(), Y.to(X.dtype).contiguous()
-    vx, vy = vx.to(X.dtype).contiguous(), vy.to(X.dtype).contiguous()
+    X, Y, vx, vy = _hip.dense(X.dtype, X, Y, vx, vy)
     pen = beta != 0.0
     R = X.new_empty(B, N * M)
     P = X.new_empty(B, N * M) if pen else X.new_empty(0)
@@ -127,14 +126,13 @@ def fused_backward(X: Tensor, Y: Tensor, vx: Tensor, vy: Tensor, R: Tensor, P: T
     _hip.require(X, backend, "uDTW")
     B, N, D = X.shape
     M = Y.shape[1]
-    X, Y = X.contiguous(), Y.to(X.dtype).contiguous()
-    vx, vy = vx.to(X.dtype).contiguous(), vy.to(X.dtype).contiguous()
+    X, Y, vx, vy = _hip.dense(X.dtype, X, Y, vx, vy)
     pen = beta != 0.0
     dX, dY = torch.empty_like(X), torch.empty_like(Y)
     dvx, dvy = torch.empty_like(vx), torch.empty_like(vy)
     ws = _feat_ws(X, N, M)
-    grads, gs = _hip.per_pair(*((grad_r.to(X.dtype), grad_p.to(X.dtype)) if pen
-                                else (grad_r.to(X.dtype),)))
+    grads, gs = _hip.per_pair(*(_hip.dense(X.dtype, grad_r, grad_p, contiguous=False) if pen
+                                else _hip.dense(X.dtype, grad_r, contiguous=False)))
     _hip.call("tw_udtw_feat_bwd", X.dtype, X, Y, vx, vy, R, P if pen else None, grads[0],
               grads[1] if pen else None, B, N, M, D, gamma, beta, eps, bandwidth, int(sigma), gs,
               dX, dY, dvx, dvy, ws, 0 if ws is None else ws.numel() * ws.element_size())
@@ -343,7 +341,7 @@ class FusedBackward(torch.autograd.Function):
         return tuple(jvp_of(FusedBackward._first(ctx), primals, tangents))
 
 
-dp_apply = pick(DP, without_jvp(DP))
-dp_backward_apply = pick(DPBackward, without_jvp(DPBackward))
-fused_apply = pick(Fused, without_jvp(Fused))
-fused_backward_apply = pick(FusedBackward, without_jvp(FusedBackward))
+dp_apply = pick(DP, without_jvp(DP), DP.forward)
+dp_backward_apply = pick(DPBackward, without_jvp(DPBackward), DPBackward.forward)
+fused_apply = pick(Fused, without_jvp(Fused), Fused.forward)
+fused_backward_apply = pick(FusedBackward, without_jvp(FusedBackward), FusedBackward.forward)

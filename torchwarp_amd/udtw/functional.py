@@ -13,6 +13,7 @@ from typing import NamedTuple
 
 import torch
 
+from .. import _hip
 from . import _ops
 
 _BACKENDS = ("auto", "cuda", "torch")
@@ -130,12 +131,11 @@ def _udtw_fused(X, Y, sigma_x, sigma_y, beta, gamma, bandwidth, eps, backend):
     if X.shape[1] > Y.shape[1]:  # symmetric problem; keep N <= M
         X, Y, sigma_x, sigma_y = Y, X, sigma_y, sigma_x
     dtype = X.dtype if X.dtype in (torch.float32, torch.float64) else torch.float32
-    X, Y = X.to(dtype), Y.to(dtype)
+    # the kernels square the standard deviations themselves (and return d sigma)
+    X, Y, sx, sy = _hip.dense(dtype, X, Y, sigma_x, sigma_y, contiguous=False)
     if Y is X:
         # d(X, X): torch.compile cannot trace a Function receiving one tensor twice
         Y = X.view_as(X)
-    # the kernels square the standard deviations themselves (and return d sigma)
-    sx, sy = sigma_x.to(dtype), sigma_y.to(dtype)
     if sy is sx:
         sy = sx.view_as(sx)
     band = 0.0 if bandwidth is None else float(bandwidth)
