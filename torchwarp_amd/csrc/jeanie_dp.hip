@@ -20,32 +20,12 @@
 // when they do not fit, the kernel reads them back from the R output in
 // global memory (full-fence barrier per diagonal).
 
-#include "tw_capi.hpp"
-#include "tw_common.hpp"
+#include <stdlib.h>
+
+#include "jeanie.hpp"
 #include "../../include/torchwarp_hip.h"
 
 namespace tw {
-
-template <typename T>
-struct JeanieArgs {
-  const T* C;
-  const T* R;   // backward input
-  T* Rw;        // forward output
-  T* out;
-  const T* gout;
-  const T* gR;
-  T* dC;
-  int K1, K2, K, Tn, Un, s1, s2;
-  int swap;
-  T k;       // log2(e) / gamma
-  T inv_k;   // gamma ln 2
-};
-
-template <typename T>
-__device__ __forceinline__ size_t jidx(const JeanieArgs<T>& a, int n, int t, int u) {
-  const size_t plane = (size_t)a.Tn * a.Un;
-  return (size_t)n * plane + (a.swap ? (size_t)u * a.Tn + t : (size_t)t * a.Un + u);
-}
 
 template <typename T, bool LDSBUF>
 __global__ void __launch_bounds__(1024) jeanie_fwd_kernel(JeanieArgs<T> a) {
@@ -531,6 +511,17 @@ static J2Shape jeanie2_shape(int K, int Tn, int s1, int s2) {
   return sh;
 }
 
+// The wavefront-per-pair kernels serve every shape they support unless
+// TORCHWARP_JEANIE_V2=1 selects the workgroup-per-pair kernels (for
+// comparisons).
+static bool j3_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("TORCHWARP_JEANIE_V2");
+    return !(e && e[0] == '1');
+  }();
+  return on;
+}
+
 static int jeanie_threads(int cells) {
   int t = ((cells + 63) / 64) * 64;
   return t < 64 ? 64 : (t > 1024 ? 1024 : t);
@@ -573,6 +564,10 @@ int jeanie_cost_fwd(const T* C, int B, int K1, int K2, int Tn, int Un, int swap,
   a.Rw = R;
   a.out = out;
   jeanie_fill(a, K1, K2, Tn, Un, s1, s2, swap, gamma);
+  if (j3_enabled()) {
+    const int e = jeanie3_fwd<T>(a, B, s, what);
+    if (e != kJ3Unsupported) return e;
+  }
   const J2Shape sh = jeanie2_shape(a.K, Tn, a.s1, a.s2);
   if (sh.threads) {
     const size_t ring = (size_t)2 * sh.threads * sizeof(T);
@@ -612,6 +607,10 @@ int jeanie_cost_bwd(const T* C, const T* R, const T* gout, const T* gR, int B, i
   a.gR = gR;
   a.dC = dC;
   jeanie_fill(a, K1, K2, Tn, Un, s1, s2, swap, gamma);
+  if (j3_enabled()) {
+    const int e = jeanie3_bwd<T>(a, B, s, what);
+    if (e != kJ3Unsupported) return e;
+  }
   const J2Shape sh = jeanie2_shape(a.K, Tn, a.s1, a.s2);
   if (sh.threads) {
     const size_t ring = (size_t)4 * sh.threads * sizeof(T);

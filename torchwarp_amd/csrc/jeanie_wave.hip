@@ -1,0 +1,451 @@
+// JEANIE temporal-viewpoint DP for gfx950 with one wavefront per pair:
+// forward and backward on the cost path (reference: jeanie_cuda.cu:144-295,
+// jeanie/_torch_dp.py:14-75, jeanie/functional.py:28-61).
+//
+// The window softmin is evaluated separably in the base-2 scaled domain
+// (Rh = R log2(e)/g); a softmin over a union of disjoint sets is the softmin
+// of their softmins, so with viewpoints n = n1 K2 + n2:
+//   S2[n1,n2] = softmin_{|o|<=s2} R[n1, n2+o]
+//   Rw[n1,n2] = softmin_{|o|<=s1} S2[n1+o, n2]
+//   R[n,t,u]  = C[n,t,u] + softmin(Rw[n,t-1,u], Rw[n,t,u-1], Rw[n,t-1,u-1])
+// and R[n,0,0] = C[n,0,0]. The backward runs the three stages in reverse
+// (successor weights -> RWbar -> S2bar -> Rbar), recomputing S2 and Rw from R.
+//
+// Mapping. A wavefront owns one pair and walks it in row pairs: its 32-lane
+// halves own rows t = 2r and 2r + 1, lane n of a half owns viewpoint n
+// (K <= 32). At step v of a row pair, half h computes column u = v - h, one
+// column behind the other half (U + 1 steps per row pair). Per cell:
+//  * the window softmins gather neighbouring viewpoints of the same cell:
+//    stride 1 by DPP wave shifts, stride K2 by ds_bpermute;
+//  * the temporal predecessors are Rw values of the lane's own viewpoint:
+//    "left" is its own last step; half 1's "up" is half 0's last step, handed
+//    over by v_permlane32_swap at the end of every step; half 0's "up" is the
+//    row above the pair, which half 1 produced during the previous row pair:
+//    half 0 receives it in the same swap and parks it in an LDS row buffer
+//    (two buffers, by row-pair parity) until the next row pair reads it;
+//  * the cost (and in the backward R and dL/dR) of a row pair is loaded into
+//    a register ring during the previous row pair, and each result is
+//    stored as soon as it is known.
+// Nothing crosses wavefronts, so there is no barrier: a wavefront's LDS
+// operations complete in order. The backward runs the same sweep on the
+// grid flipped in t and u, so its "predecessors" are the cell's successors.
+//
+// Work per pair: ceil(T/2) (U + 1) steps of one cell per lane, against
+// T + U - 1 diagonal steps of the workgroup-per-pair kernels (jeanie_dp.hip)
+// that keep a lane per (t, n) busy only while row t is on the diagonal.
+
+#include "jeanie.hpp"
+
+namespace tw {
+
+
+__device__ __forceinline__ float med3(float a, float b, float c) {
+  return __builtin_amdgcn_fmed3f(a, b, c);
+}
+__device__ __forceinline__ double med3(double a, double b, double c) {
+  return fmax(fmin(a, b), fmin(fmax(a, b), c));
+}
+
+// base-2 softmin of three values: the smallest one contributes exp2(0) = 1
+template <typename T>
+__device__ __forceinline__ T softmin3h(T a, T b, T c) {
+  const T m = fmin(a, fmin(b, c));
+  const T md = med3(a, b, c);
+  const T mx = fmax(a, fmax(b, c));
+  return m - lg2((T)1 + ex2(m - md) + ex2(m - mx));
+}
+
+// lane l + o (|o| <= 2) of v along the stride-1 viewpoint axis (DPP wave shifts)
+template <typename T>
+__device__ __forceinline__ T nb1(T v, int o) {
+  const T INF = inf_v<T>();
+  if (o == -1) return shift_prev(v, INF);
+  if (o == 1) return shift_next(v, INF);
+  if (o == -2) return shift_prev(shift_prev(v, INF), INF);
+  return shift_next(shift_next(v, INF), INF);
+}
+
+// the value of lane idx/4 (ds_bpermute byte index)
+__device__ __forceinline__ float bperm(float v, int idx) {
+  return __int_as_float(__builtin_amdgcn_ds_bpermute(idx, __float_as_int(v)));
+}
+__device__ __forceinline__ double bperm(double v, int idx) {
+  const long long b = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_ds_bpermute(idx, (int)b);
+  const int hi = __builtin_amdgcn_ds_bpermute(idx, (int)(b >> 32));
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+// The halves of a wavefront exchanged: lanes 0-31 take lanes 32-63 and back
+// (v_permlane32_swap of a register with itself).
+__device__ __forceinline__ float swap_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(__lane_id() < 32 ? r[1] : r[0]);
+}
+__device__ __forceinline__ double swap_halves(double v) {
+  const long long b = __double_as_longlong(v);
+  const unsigned lo = (unsigned)b, hi = (unsigned)(b >> 32);
+  const auto rl = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+  const auto rh = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+  const bool low = __lane_id() < 32;
+  const unsigned long long l = low ? rl[1] : rl[0], h = low ? rh[1] : rh[0];
+  return __longlong_as_double((long long)((h << 32) | l));
+}
+
+// Per-lane window of a viewpoint: which neighbours o = -2..2 exist along each
+// axis, and the ds_bpermute byte indices of the stride-K2 neighbours.
+struct J3Win {
+  bool a1[5], a2[5];   // axis 1 (stride K2) / axis 2 (stride 1) neighbour o - 2 in the window
+  int idx1[5];
+  __device__ void init(int lane, int n1, int n2, int K1, int K2, int s1, int s2) {
+#pragma unroll
+    for (int q = 0; q < 5; ++q) {
+      const int o = q - 2;
+      a1[q] = (o >= -s1 && o <= s1 && n1 + o >= 0 && n1 + o < K1);
+      a2[q] = (o >= -s2 && o <= s2 && n2 + o >= 0 && n2 + o < K2);
+      idx1[q] = ((lane + o * K2) & 63) << 2;
+    }
+  }
+};
+
+// softmin over the window of axis 2 (stride 1), then of axis 1 (stride K2)
+// (Cross-lane moves run in every lane and are masked afterwards: a lane that
+// skipped one would hand its neighbour a stale value.)
+template <typename T, int SMAX>
+__device__ __forceinline__ T win2(T v, const J3Win& w, int s2) {
+  const T INF = inf_v<T>();
+  if (s2 == 0) return v;
+  if (SMAX == 1) {
+    const T lo = nb1(v, -1), hi = nb1(v, 1);
+    return softmin3h(w.a2[1] ? lo : INF, v, w.a2[3] ? hi : INF);
+  }
+  T x[5];
+#pragma unroll
+  for (int q = 0; q < 5; ++q) x[q] = q == 2 ? v : nb1(v, q - 2);
+  T m = INF;
+#pragma unroll
+  for (int q = 0; q < 5; ++q) {
+    x[q] = (q == 2 || w.a2[q]) ? x[q] : INF;
+    m = fmin(m, x[q]);
+  }
+  T s = 0;
+#pragma unroll
+  for (int q = 0; q < 5; ++q) s += ex2(m - x[q]);
+  return m - lg2(s);
+}
+template <typename T, int SMAX>
+__device__ __forceinline__ T win1(T v, const J3Win& w, int s1) {
+  const T INF = inf_v<T>();
+  if (s1 == 0) return v;
+  if (SMAX == 1) {
+    const T lo = bperm(v, w.idx1[1]), hi = bperm(v, w.idx1[3]);
+    return softmin3h(w.a1[1] ? lo : INF, v, w.a1[3] ? hi : INF);
+  }
+  T x[5];
+#pragma unroll
+  for (int q = 0; q < 5; ++q) x[q] = q == 2 ? v : bperm(v, w.idx1[q]);
+  T m = INF;
+#pragma unroll
+  for (int q = 0; q < 5; ++q) {
+    x[q] = (q == 2 || w.a1[q]) ? x[q] : INF;
+    m = fmin(m, x[q]);
+  }
+  T s = 0;
+#pragma unroll
+  for (int q = 0; q < 5; ++q) s += ex2(m - x[q]);
+  return m - lg2(s);
+}
+
+// Adjoints of the window stages: sum over the window's neighbours q of
+// g[q] 2^(hq[q] - x) (the window is symmetric, so the lanes whose window holds
+// this lane are its window neighbours).
+template <typename T, int SMAX>
+__device__ __forceinline__ T win1_adj(T g, T hq, T x, const J3Win& w, int s1) {
+  if (s1 == 0) return g;
+  T acc = g * ex2(hq - x);
+#pragma unroll
+  for (int q = 0; q < 5; ++q) {
+    if (q == 2 || (SMAX == 1 && (q == 0 || q == 4))) continue;
+    const T gq = bperm(g, w.idx1[q]), hh = bperm(hq, w.idx1[q]);
+    acc += w.a1[q] ? gq * ex2(hh - x) : (T)0;
+  }
+  return acc;
+}
+template <typename T, int SMAX>
+__device__ __forceinline__ T win2_adj(T g, T hq, T x, const J3Win& w, int s2) {
+  if (s2 == 0) return g;
+  T acc = g * ex2(hq - x);
+#pragma unroll
+  for (int q = 0; q < 5; ++q) {
+    if (q == 2 || (SMAX == 1 && (q == 0 || q == 4))) continue;
+    const T gq = nb1(g, q - 2), hh = nb1(hq, q - 2);
+    acc += w.a2[q] ? gq * ex2(hh - x) : (T)0;
+  }
+  return acc;
+}
+
+// Lane geometry of the sweep. Row pair r puts half h on row 2r + h, and step
+// v of the row pair on column v - h (of the grid flipped in t and u for the
+// backward). UC >= U is the compile-time row length: a row pair takes UC + 1
+// steps, so the steps of a row pair unroll with constant columns; columns
+// >= U lie outside the grid.
+template <typename T>
+struct J3Lane {
+  int lb, ts, us, rlim, Un, h;
+  bool vn, flip;
+  __device__ void init(int n, int h_, const JeanieArgs<T>& a, bool flip_) {
+    const int es = (int)sizeof(T);
+    h = h_;
+    Un = a.Un;
+    flip = flip_;
+    vn = n < a.K;
+    ts = (a.swap ? 1 : a.Un) * es;
+    us = (a.swap ? a.Tn : 1) * es;
+    rlim = (a.Tn - h + 1) >> 1;   // row pairs whose row 2r + h < T
+    const int pl = n * a.Tn * a.Un * es;
+    // byte offset of the cell at step 0 of row pair 0
+    lb = flip ? pl + (a.Tn - 1 - h) * ts + (a.Un - 1 + h) * us : pl + h * (ts - us);
+  }
+  // byte offset of column 0 of row pair r (or kOob when the lane's row is outside)
+  __device__ __forceinline__ int base(int r) const {
+    return (vn && r < rlim) ? (flip ? lb - 2 * r * ts : lb + 2 * r * ts) : kOob;
+  }
+  // this lane's cell at step v is inside the grid (given its row is)
+  __device__ __forceinline__ bool col_ok(int v) const {
+    return h == 0 ? v < Un : (v >= 1 && v <= Un);
+  }
+  // byte offset of the cell at step v from the row pair's base (kOob stays kOob)
+  __device__ __forceinline__ int at(int vb, int v) const {
+    return vb == kOob ? kOob : (flip ? vb - v * us : vb + v * us);
+  }
+};
+
+template <typename T, int SMAX, int UC>
+__global__ void __launch_bounds__(64) jeanie3_fwd_kernel(JeanieArgs<T> a) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  constexpr int SPR = UC + 1;
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x, h = lane >> 5, n = lane & 31;
+  const int K = a.K, Tn = a.Tn, Un = a.Un;
+  const bool vn = n < K;
+  const int n1 = vn ? n / a.K2 : 0, n2 = vn ? n - n1 * a.K2 : 0;
+  const T INF = inf_v<T>();
+  const int plane = Tn * Un, nrp = (Tn + 1) / 2, hl = (Tn - 1) & 1;
+
+  J3Win w;
+  w.init(lane, n1, n2, a.K1, a.K2, a.s1, a.s2);
+  J3Lane<T> g;
+  g.init(n, h, a, false);
+  Buf bC, bR;
+  bC.init(a.C + (size_t)b * K * plane, (long long)K * plane);
+  bR.init(a.Rw + (size_t)b * K * plane, (long long)K * plane);
+
+  // LDS: row buffers [2][SPR][32] holding Rw of the row above a row pair
+  // (entries of columns >= U stay +inf), then a scratch row for half 1's stores
+  T* rows = reinterpret_cast<T*>(smem_raw);
+  for (int e = lane; e < 3 * SPR * 32; e += 64) rows[e] = INF;
+
+  // register ring: the cost of one row pair, loaded during the previous one
+  T cr[SPR];
+  {
+    const int vb = g.base(0);
+#pragma unroll
+    for (int v = 0; v < SPR; ++v) cr[v] = bC.ld<T>(g.at(vb, v), 0);
+  }
+  T left = INF, pup = INF, xch = INF, lup = INF, rlast = INF;
+  for (int r = 0; r < nrp; ++r) {
+    const int vb = g.base(r), vbn = g.base(r + 1);
+    T* const rd = rows + (r & 1) * SPR * 32 + n;
+    T* const rdn = rows + ((r + 1) & 1) * SPR * 32 + n;
+    T* const wr = h == 0 ? rdn : rows + 2 * SPR * 32 + n;
+#pragma unroll
+    for (int v = 0; v < SPR; ++v) {
+      const bool valid = vb != kOob && g.col_ok(v);
+      const T ch = cr[v] * a.k;
+      // temporal predecessors: up (t-1, u), left (t, u-1), diagonal (t-1, u-1)
+      const T up = h ? xch : lup;
+      const T dg = v == 0 ? ((r == 0 && h == 0) ? (T)0 : INF) : pup;
+      lup = v < UC ? rd[(v + 1) * 32] : rdn[0];   // half 0's next "up"
+      T rh = ch + softmin3h(up, left, dg);
+      rh = valid ? rh : INF;
+      const T s2h = win2<T, SMAX>(rh, w, a.s2);
+      T rw = win1<T, SMAX>(s2h, w, a.s1);
+      rw = valid ? rw : INF;
+      bR.st(rh * a.inv_k, valid ? g.at(vb, v) : kOob, 0);
+      if (r == nrp - 1 && v == Un - 1 + hl) rlast = rh;   // cell (T-1, U-1) in half hl
+      left = rw;
+      pup = up;
+      xch = swap_halves(rw);
+      // half 0 parks the row below it (half 1's Rw at column v - 1) for the next row pair
+      if (v >= 1) wr[(v - 1) * 32] = xch;
+      cr[v] = bC.ld<T>(g.at(vbn, v), 0);
+    }
+  }
+  // out = softmin over the viewpoints of R[., T-1, U-1] (half hl holds the cell)
+  T m = vn ? rlast : INF;
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) m = fmin(m, __shfl_xor(m, o));
+  T s = (vn && m < INF) ? ex2(m - rlast) : (T)0;
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) s += __shfl_xor(s, o);
+  if (h == hl && n == 0) a.out[b] = (m - lg2(s)) * a.inv_k;
+}
+
+template <typename T>
+struct alignas(2 * sizeof(T)) FG {
+  T f, g;   // F = Rh - Ch and G = Rbar of a cell
+};
+
+template <typename T, int SMAX, int UC>
+__global__ void __launch_bounds__(64) jeanie3_bwd_kernel(JeanieArgs<T> a) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  constexpr int SPR = UC + 1;
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x, h = lane >> 5, n = lane & 31;
+  const int K = a.K, Tn = a.Tn, Un = a.Un;
+  const bool vn = n < K;
+  const int n1 = vn ? n / a.K2 : 0, n2 = vn ? n - n1 * a.K2 : 0;
+  const T INF = inf_v<T>();
+  const int plane = Tn * Un, nrp = (Tn + 1) / 2;
+  const T gout = a.gout[b];
+  const bool has_gr = a.gR != nullptr;
+
+  J3Win w;
+  w.init(lane, n1, n2, a.K1, a.K2, a.s1, a.s2);
+  J3Lane<T> g;
+  g.init(n, h, a, true);
+  const size_t pb = (size_t)b * K * plane;
+  Buf bC, bR, bG, bD;
+  bC.init(a.C + pb, (long long)K * plane);
+  bR.init(a.R + pb, (long long)K * plane);
+  bG.init(has_gr ? a.gR + pb : a.C, has_gr ? (long long)K * plane : 0);   // empty: loads read 0
+  bD.init(a.dC + pb, (long long)K * plane);
+
+  // LDS: row buffers [2][SPR][32] of (F, G) of the row below a row pair (the
+  // row above in the flipped grid; columns >= U stay (-inf, 0)), then a
+  // scratch row for half 1's stores
+  FG<T>* rows = reinterpret_cast<FG<T>*>(smem_raw);
+  for (int e = lane; e < 3 * SPR * 32; e += 64) rows[e] = {-INF, (T)0};
+
+  T rr[SPR], rc[SPR], rg[SPR];
+  {
+    const int vb = g.base(0);
+#pragma unroll
+    for (int v = 0; v < SPR; ++v) {
+      const int o = g.at(vb, v);
+      rr[v] = bR.ld<T>(o, 0);
+      rc[v] = bC.ld<T>(o, 0);
+      rg[v] = bG.ld<T>(o, 0);
+    }
+  }
+  const FG<T> none = {-INF, (T)0};
+  FG<T> left = none, pup = none, xch = none, lup = none;
+  for (int r = 0; r < nrp; ++r) {
+    const int vb = g.base(r), vbn = g.base(r + 1);
+    FG<T>* const rd = rows + (r & 1) * SPR * 32 + n;
+    FG<T>* const rdn = rows + ((r + 1) & 1) * SPR * 32 + n;
+    FG<T>* const wr = h == 0 ? rdn : rows + 2 * SPR * 32 + n;
+#pragma unroll
+    for (int v = 0; v < SPR; ++v) {
+      const bool valid = vb != kOob && g.col_ok(v);
+      const T rh = valid ? rr[v] * a.k : INF;
+      const T ch = rc[v] * a.k;
+      // successors (t+1, u), (t, u+1), (t+1, u+1) of the cell
+      const FG<T> up = h ? xch : lup;
+      const FG<T> dg = v == 0 ? none : pup;
+      lup = v < UC ? rd[(v + 1) * 32] : rdn[0];
+      const T s2h = win2<T, SMAX>(rh, w, a.s2);
+      const T rwh = win1<T, SMAX>(s2h, w, a.s1);
+      T wbar = up.g * ex2(up.f - rwh) + left.g * ex2(left.f - rwh) + dg.g * ex2(dg.f - rwh);
+      wbar = valid ? wbar : (T)0;
+      const T s2bar = win1_adj<T, SMAX>(wbar, valid ? rwh : (T)0, s2h, w, a.s1);
+      T rbar = win2_adj<T, SMAX>(valid ? s2bar : (T)0, valid ? s2h : (T)0, rh, w, a.s2);
+      if (v == 0 && r == 0) {
+        // the last cell (T-1, U-1) (half 0): seed with grad_out * softmax_n(-R/g)
+        T m = valid ? rh : INF;
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) m = fmin(m, __shfl_xor(m, o));
+        T s = valid ? ex2(m - rh) : (T)0;
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) s += __shfl_xor(s, o);
+        rbar += gout * ex2(m - lg2(s) - rh);
+      }
+      if (has_gr) rbar += rg[v];
+      rbar = valid ? rbar : (T)0;
+      const FG<T> cur = {valid ? rh - ch : -INF, rbar};
+      bD.st(rbar, valid ? g.at(vb, v) : kOob, 0);
+      left = cur;
+      pup = up;
+      xch = {swap_halves(cur.f), swap_halves(cur.g)};
+      if (v >= 1) wr[(v - 1) * 32] = xch;
+      const int o = g.at(vbn, v);
+      rr[v] = bR.ld<T>(o, 0);
+      rc[v] = bC.ld<T>(o, 0);
+      rg[v] = bG.ld<T>(o, 0);
+    }
+  }
+}
+
+// Row length the kernels are compiled for: the smallest of 8, 16, 32 that
+// holds U (16 in float64), 0 beyond. Longer rows would not unroll into
+// registers; they use the workgroup-per-pair kernels.
+template <typename T>
+static int j3_uc(int Un) {
+  constexpr int umax = sizeof(T) == 4 ? 32 : 16;
+  return Un <= 8 ? 8 : (Un <= 16 ? 16 : (Un <= umax ? umax : 0));
+}
+
+template <typename T>
+static size_t j3_lds(int uc, bool bwd) {
+  return (size_t)3 * (uc + 1) * 32 * sizeof(T) * (bwd ? 2 : 1);
+}
+
+template <typename T, int SMAX, int UC>
+static void j3_launch(bool bwd, const JeanieArgs<T>& a, int B, hipStream_t s) {
+  const size_t lds = j3_lds<T>(UC, bwd);
+  if (bwd)
+    hipLaunchKernelGGL((jeanie3_bwd_kernel<T, SMAX, UC>), dim3(B), dim3(64), lds, s, a);
+  else
+    hipLaunchKernelGGL((jeanie3_fwd_kernel<T, SMAX, UC>), dim3(B), dim3(64), lds, s, a);
+}
+
+template <typename T, int SMAX>
+static void j3_launch_uc(bool bwd, int uc, const JeanieArgs<T>& a, int B, hipStream_t s) {
+  switch (uc) {
+    case 8: j3_launch<T, SMAX, 8>(bwd, a, B, s); break;
+    case 16: j3_launch<T, SMAX, 16>(bwd, a, B, s); break;
+    default:
+      if constexpr (sizeof(T) == 4) j3_launch<T, SMAX, 32>(bwd, a, B, s);
+      break;
+  }
+}
+
+template <typename T>
+static int j3_run(bool bwd, const JeanieArgs<T>& a, int B, hipStream_t s, const char* what) {
+  const int uc = j3_uc<T>(a.Un);
+  if (a.K > 32 || uc == 0 || a.s1 > 2 || a.s2 > 2) return kJ3Unsupported;
+  if (B == 0) return TW_OK;
+  if (a.s1 > 1 || a.s2 > 1)
+    j3_launch_uc<T, 2>(bwd, uc, a, B, s);
+  else
+    j3_launch_uc<T, 1>(bwd, uc, a, B, s);
+  return check_launch(what);
+}
+
+template <typename T>
+int jeanie3_fwd(const JeanieArgs<T>& a, int B, hipStream_t s, const char* what) {
+  return j3_run<T>(false, a, B, s, what);
+}
+
+template <typename T>
+int jeanie3_bwd(const JeanieArgs<T>& a, int B, hipStream_t s, const char* what) {
+  return j3_run<T>(true, a, B, s, what);
+}
+
+template int jeanie3_fwd<float>(const JeanieArgs<float>&, int, hipStream_t, const char*);
+template int jeanie3_fwd<double>(const JeanieArgs<double>&, int, hipStream_t, const char*);
+template int jeanie3_bwd<float>(const JeanieArgs<float>&, int, hipStream_t, const char*);
+template int jeanie3_bwd<double>(const JeanieArgs<double>&, int, hipStream_t, const char*);
+
+}  // namespace tw

@@ -892,10 +892,13 @@ static size_t udtw_lds(bool backward, int nw, bool lc, int N, int M) {
   return n;
 }
 
-// Prefetch depth (diagonals) of the register ring for a row count.
+// Prefetch depth (diagonals) of the register ring for a row count: loads
+// are issued this many diagonals before their use, enough to cover an HBM
+// miss when a diagonal step takes a few hundred nanoseconds. It divides the
+// block of kSlots steps, so ring slots stay compile-time constants.
 template <int ROWS>
 struct PrefetchDepth {
-  static constexpr int value = ROWS == 1 ? 4 : (ROWS == 2 ? 2 : 1);
+  static constexpr int value = ROWS <= 4 ? 4 : (ROWS == 8 ? 2 : 1);
 };
 
 template <typename T, int SRC, bool PEN, bool BAND>
