@@ -26,6 +26,11 @@ SHAPES = [  # (P, R, C, D)
     (2, 9, 8, 7),
     (4, 72, 8, 256),
     (1, 40, 80, 16),
+    # more than 64 columns: the tiled backward passes, ragged tiles
+    (2, 130, 70, 5),
+    (1, 65, 129, 33),
+    (2, 200, 100, 64),
+    (3, 100, 90, 3),
 ]
 
 

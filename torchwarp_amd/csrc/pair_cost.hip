@@ -15,7 +15,9 @@
 // (v_mfma_f32_16x16x4f32, a 16 x 16*TN output strip per wavefront); fp64 and
 // other D on a plain FMA kernel. Backward: when a pair's dS fits in LDS and
 // C <= 64, one fused kernel per pair streams A and B once (threads along D,
-// dB partial sums in registers); otherwise two FMA kernels (dA, dB).
+// dB partial sums in registers); otherwise, for D <= 64, two tiled passes
+// that each read dS once (dA by row blocks, dB by column blocks), and two
+// FMA kernels beyond.
 
 #include "tw_capi.hpp"
 #include "tw_common.hpp"
@@ -103,6 +105,72 @@ __global__ void __launch_bounds__(256) pair_bwd_b_fma(const T* __restrict__ A,
   dB[((size_t)p * C + c) * D + d] = (T)2 * (cs * Bm[((size_t)p * C + c) * D + d] - acc);
 }
 
+
+// Tiled backward for D <= 64, one pass over dS per output: a workgroup owns
+// 64 rows (dA, COLS false) or 64 columns (dB, COLS true) of a pair and
+// streams the other axis in 64-wide tiles. Each dS tile is read with
+// coalesced 256-byte rows and staged in LDS as [owned][streamed] next to the
+// matching 64 x D block of the other operand; four threads share an owned
+// index and each accumulates DPT of its D outputs, summing in a fixed order.
+template <typename T, int MET, bool COLS, int DPT>
+__global__ void __launch_bounds__(256) pair_bwd_tiled(const T* __restrict__ A,
+                                                      const T* __restrict__ Bm,
+                                                      const T* __restrict__ cost,
+                                                      const T* __restrict__ dcost,
+                                                      T* __restrict__ dOut, int R, int C, int D) {
+  constexpr int TL = 64;
+  __shared__ T ds[TL][TL + 1];
+  __shared__ T op[TL][4 * DPT + 1];
+  const int p = blockIdx.y, tid = threadIdx.x;
+  const int own0 = blockIdx.x * TL;
+  const int nown = COLS ? C : R, nstr = COLS ? R : C;
+  const size_t prc = (size_t)p * R * C;
+  const T* other = COLS ? A + (size_t)p * R * D : Bm + (size_t)p * C * D;
+  const T* self = COLS ? Bm + (size_t)p * C * D : A + (size_t)p * R * D;
+  const int oi = tid >> 2, dg = tid & 3;
+  T acc[DPT];
+#pragma unroll
+  for (int k = 0; k < DPT; ++k) acc[k] = 0;
+  T sum = 0;
+  for (int s0 = 0; s0 < nstr; s0 += TL) {
+    __syncthreads();
+    const int r0 = COLS ? s0 : own0, c0 = COLS ? own0 : s0;
+#pragma unroll 4
+    for (int e = tid; e < TL * TL; e += 256) {
+      const int rr = e >> 6, cc = e & 63;
+      const int r = r0 + rr, c = c0 + cc;
+      T v = 0;
+      if (r < R && c < C) {
+        const size_t o = prc + (size_t)r * C + c;
+        v = cost_adjoint<T, MET>(dcost[o], MET == MET_RAW ? (T)0 : cost[o]);
+      }
+      if (COLS)
+        ds[cc][rr] = v;
+      else
+        ds[rr][cc] = v;
+    }
+    for (int e = tid; e < TL * 4 * DPT; e += 256) {
+      const int si = e / (4 * DPT), d = e - si * (4 * DPT);
+      op[si][d] = (s0 + si < nstr && d < D) ? other[(size_t)(s0 + si) * D + d] : (T)0;
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int si = 0; si < TL; ++si) {
+      const T v = ds[oi][si];
+      sum += v;
+#pragma unroll
+      for (int k = 0; k < DPT; ++k) acc[k] += v * op[si][dg * DPT + k];
+    }
+  }
+  const int o = own0 + oi;
+  if (o < nown) {
+#pragma unroll
+    for (int k = 0; k < DPT; ++k) {
+      const int d = dg * DPT + k;
+      if (d < D) dOut[((size_t)p * nown + o) * D + d] = (T)2 * (sum * self[(size_t)o * D + d] - acc[k]);
+    }
+  }
+}
 
 // ----------------------------------------------------------- MFMA forward
 //
@@ -330,6 +398,34 @@ int pair_cost_bwd(const T* A, const T* Bm, const T* cost, const T* dcost, int P,
     else { TW_PAIR_SMALL_C(MET_EUC) }
 #undef TW_PAIR_SMALL_C
 #undef TW_PAIR_SMALL
+    return check_launch(what);
+  }
+  // (a float64 pass with 64 features would need 66 KB of static LDS)
+  if (D <= (sizeof(T) == 4 ? 64 : 32)) {
+    const int dpt = D <= 4 ? 1 : (D <= 8 ? 2 : (D <= 16 ? 4 : (D <= 32 ? 8 : 16)));
+    const dim3 ga((R + 63) / 64, P), gb((C + 63) / 64, P), block(256);
+#define TW_PAIR_TILED(MET_, DPT_)                                                               \
+  hipLaunchKernelGGL((pair_bwd_tiled<T, MET_, false, DPT_>), ga, block, 0, s, A, Bm, cost,      \
+                     dcost, dA, R, C, D);                                                       \
+  hipLaunchKernelGGL((pair_bwd_tiled<T, MET_, true, DPT_>), gb, block, 0, s, A, Bm, cost, dcost, \
+                     dB, R, C, D);
+#define TW_PAIR_TILED_D(MET_)                      \
+  switch (dpt) {                                   \
+    case 1: TW_PAIR_TILED(MET_, 1) break;          \
+    case 2: TW_PAIR_TILED(MET_, 2) break;          \
+    case 4: TW_PAIR_TILED(MET_, 4) break;          \
+    case 8: TW_PAIR_TILED(MET_, 8) break;          \
+    default:                                       \
+      if constexpr (sizeof(T) == 4) {             \
+        TW_PAIR_TILED(MET_, 16)                    \
+      }                                            \
+      break;                                       \
+  }
+    if (metric == MET_RAW) { TW_PAIR_TILED_D(MET_RAW) }
+    else if (metric == MET_SQ) { TW_PAIR_TILED_D(MET_SQ) }
+    else { TW_PAIR_TILED_D(MET_EUC) }
+#undef TW_PAIR_TILED_D
+#undef TW_PAIR_TILED
     return check_launch(what);
   }
   dim3 ga(blocks_for((long long)R * D), P), gb(blocks_for((long long)C * D), P), block(256);
