@@ -642,7 +642,9 @@ int jeanie_cost_bwd(const T* C, const T* R, const T* gout, const T* gR, int B, i
 // written in the DP orientation ([U,T] when `swap`), and its adjoint
 //   dC[n,t,u] = exp((temporal[t,u] - C[n,t,u])/g) * dtemporal[t,u].
 
-template <typename T>
+// KU > 0: all K <= KU viewpoints of a cell are loaded at once (unrolled,
+// every load in flight together); KU = 0: a loop for larger K.
+template <typename T, int KU>
 __global__ void __launch_bounds__(256) fvm_softmin_fwd(const T* __restrict__ C, T* __restrict__ tmp,
                                                        int K, int Tn, int Un, int swap, T k,
                                                        T inv_k) {
@@ -651,16 +653,26 @@ __global__ void __launch_bounds__(256) fvm_softmin_fwd(const T* __restrict__ C, 
   const int plane = Tn * Un;
   if (cell >= plane) return;
   const T* c = C + (size_t)b * K * plane + cell;
-  T m = inf_v<T>();
-  for (int n = 0; n < K; ++n) m = fmin(m, c[(size_t)n * plane]);
-  T s = 0;
-  for (int n = 0; n < K; ++n) s += ex2((m - c[(size_t)n * plane]) * k);
+  const T INF = inf_v<T>();
+  T m = INF, s = 0;
+  if (KU > 0) {
+    T v[KU > 0 ? KU : 1];
+#pragma unroll
+    for (int n = 0; n < KU; ++n) v[n] = n < K ? c[(size_t)n * plane] : INF;
+#pragma unroll
+    for (int n = 0; n < KU; ++n) m = fmin(m, v[n]);
+#pragma unroll
+    for (int n = 0; n < KU; ++n) s += n < K ? ex2((m - v[n]) * k) : (T)0;
+  } else {
+    for (int n = 0; n < K; ++n) m = fmin(m, c[(size_t)n * plane]);
+    for (int n = 0; n < K; ++n) s += ex2((m - c[(size_t)n * plane]) * k);
+  }
   const int t = cell / Un, u = cell - t * Un;
   const int o = swap ? u * Tn + t : cell;
   tmp[(size_t)b * plane + o] = m - inv_k * lg2(s);
 }
 
-template <typename T>
+template <typename T, int KU>
 __global__ void __launch_bounds__(256) fvm_softmin_bwd(const T* __restrict__ C,
                                                        const T* __restrict__ tmp,
                                                        const T* __restrict__ dtmp,
@@ -675,7 +687,16 @@ __global__ void __launch_bounds__(256) fvm_softmin_bwd(const T* __restrict__ C,
   const T tv = tmp[(size_t)b * plane + o], g = dtmp[(size_t)b * plane + o];
   const T* c = C + (size_t)b * K * plane + cell;
   T* dc = dC + (size_t)b * K * plane + cell;
-  for (int n = 0; n < K; ++n) dc[(size_t)n * plane] = ex2((tv - c[(size_t)n * plane]) * k) * g;
+  if (KU > 0) {
+    T v[KU > 0 ? KU : 1];
+#pragma unroll
+    for (int n = 0; n < KU; ++n) v[n] = n < K ? c[(size_t)n * plane] : (T)0;
+#pragma unroll
+    for (int n = 0; n < KU; ++n)
+      if (n < K) dc[(size_t)n * plane] = ex2((tv - v[n]) * k) * g;
+  } else {
+    for (int n = 0; n < K; ++n) dc[(size_t)n * plane] = ex2((tv - c[(size_t)n * plane]) * k) * g;
+  }
 }
 
 template <typename T>
@@ -696,8 +717,12 @@ int fvm_fwd(const T* C, int B, int K, int Tn, int Un, double gamma, T* tmp, T* R
   const int swap = Tn > Un;
   const T k = (T)(1.4426950408889634 / gamma), inv_k = (T)(gamma * 0.6931471805599453);
   dim3 grid((Tn * Un + 255) / 256, B);
-  hipLaunchKernelGGL((fvm_softmin_fwd<T>), grid, dim3(256), 0, s, C, tmp, K, Tn, Un, swap, k,
-                     inv_k);
+  if (K <= 32)
+    hipLaunchKernelGGL((fvm_softmin_fwd<T, 32>), grid, dim3(256), 0, s, C, tmp, K, Tn, Un, swap,
+                       k, inv_k);
+  else
+    hipLaunchKernelGGL((fvm_softmin_fwd<T, 0>), grid, dim3(256), 0, s, C, tmp, K, Tn, Un, swap,
+                       k, inv_k);
   if (int e = check_launch(what)) return e;
   const int N = swap ? Un : Tn, M = swap ? Tn : Un;
   return udtw_cost_fwd_any<T>(tmp, nullptr, B, N, M, gamma, 0.0, R, nullptr, out, pen_scratch,
@@ -718,8 +743,12 @@ int fvm_bwd(const T* C, const T* tmp, const T* R, const T* gout, int B, int K, i
     return e;
   const T k = (T)(1.4426950408889634 / gamma);
   dim3 grid((Tn * Un + 255) / 256, B);
-  hipLaunchKernelGGL((fvm_softmin_bwd<T>), grid, dim3(256), 0, s, C, tmp, ws, dC, K, Tn, Un,
-                     swap, k);
+  if (K <= 32)
+    hipLaunchKernelGGL((fvm_softmin_bwd<T, 32>), grid, dim3(256), 0, s, C, tmp, ws, dC, K, Tn, Un,
+                       swap, k);
+  else
+    hipLaunchKernelGGL((fvm_softmin_bwd<T, 0>), grid, dim3(256), 0, s, C, tmp, ws, dC, K, Tn, Un,
+                       swap, k);
   return check_launch(what);
 }
 
