@@ -18,6 +18,11 @@
 // dB partial sums in registers); otherwise, for D <= 64, two tiled passes
 // that each read dS once (dA by row blocks, dB by column blocks), and two
 // FMA kernels beyond.
+//
+// The uDTW feature path (sqdist_raw / sqdist_raw_bwd) keeps S and dS by
+// anti-diagonals (plane_index), the layout in which the sweeps' per-diagonal
+// accesses are coalesced; the tiled backward then reads each 64 x 64 tile
+// along its anti-diagonals, whose cells are contiguous.
 
 #include "tw_capi.hpp"
 #include "tw_common.hpp"
@@ -41,9 +46,19 @@ __device__ __forceinline__ T cost_adjoint(T dcost, T cost) {
   return MET == MET_EUC ? (T)0.5 * dcost / cost : dcost;
 }
 
+// Element (r, c) of a pair's R x C plane (R <= C): row-major, or with DG by
+// anti-diagonals (the cells of diagonal r + c contiguous, by row), the layout
+// the uDTW sweeps read and write coalesced.
+template <bool DG>
+__device__ __forceinline__ long long plane_index(int r, int c, int R, int C) {
+  if (!DG) return (long long)r * C + c;
+  const int d = r + c, lo = d - C + 1 > 0 ? d - C + 1 : 0;
+  return diag_offset(d, R, C) + (r - lo);
+}
+
 // ------------------------------------------------------------ FMA kernels
 
-template <typename T, int MET>
+template <typename T, int MET, bool DG>
 __global__ void __launch_bounds__(256) pair_fwd_fma(const T* __restrict__ A,
                                                     const T* __restrict__ Bm, T* __restrict__ out,
                                                     int R, int C, int D) {
@@ -60,11 +75,11 @@ __global__ void __launch_bounds__(256) pair_fwd_fma(const T* __restrict__ A,
     bq += y * y;
     ab += x * y;
   }
-  out[(size_t)p * R * C + idx] = finish_cost<T, MET>(aa + bq - (T)2 * ab);
+  out[(size_t)p * R * C + plane_index<DG>(r, c, R, C)] = finish_cost<T, MET>(aa + bq - (T)2 * ab);
 }
 
 // dA[r, d] = 2 (sum_c dS[r,c] a[r,d] - sum_c dS[r,c] b[c,d])
-template <typename T, int MET>
+template <typename T, int MET, bool DG>
 __global__ void __launch_bounds__(256) pair_bwd_a_fma(const T* __restrict__ A,
                                                       const T* __restrict__ Bm,
                                                       const T* __restrict__ cost,
@@ -74,10 +89,11 @@ __global__ void __launch_bounds__(256) pair_bwd_a_fma(const T* __restrict__ A,
   const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (long long)R * D) return;
   const int r = (int)(idx / D), d = (int)(idx % D);
-  const size_t prc = (size_t)p * R * C + (size_t)r * C;
+  const size_t pp = (size_t)p * R * C;
   T rs = 0, acc = 0;
   for (int c = 0; c < C; ++c) {
-    const T ds = cost_adjoint<T, MET>(dcost[prc + c], MET == MET_RAW ? (T)0 : cost[prc + c]);
+    const size_t o = pp + plane_index<DG>(r, c, R, C);
+    const T ds = cost_adjoint<T, MET>(dcost[o], MET == MET_RAW ? (T)0 : cost[o]);
     rs += ds;
     acc += ds * Bm[((size_t)p * C + c) * D + d];
   }
@@ -85,7 +101,7 @@ __global__ void __launch_bounds__(256) pair_bwd_a_fma(const T* __restrict__ A,
 }
 
 // dB[c, d] = 2 (sum_r dS[r,c] b[c,d] - sum_r dS[r,c] a[r,d])
-template <typename T, int MET>
+template <typename T, int MET, bool DG>
 __global__ void __launch_bounds__(256) pair_bwd_b_fma(const T* __restrict__ A,
                                                       const T* __restrict__ Bm,
                                                       const T* __restrict__ cost,
@@ -97,7 +113,7 @@ __global__ void __launch_bounds__(256) pair_bwd_b_fma(const T* __restrict__ A,
   const int c = (int)(idx / D), d = (int)(idx % D);
   T cs = 0, acc = 0;
   for (int r = 0; r < R; ++r) {
-    const size_t o = (size_t)p * R * C + (size_t)r * C + c;
+    const size_t o = (size_t)p * R * C + plane_index<DG>(r, c, R, C);
     const T ds = cost_adjoint<T, MET>(dcost[o], MET == MET_RAW ? (T)0 : cost[o]);
     cs += ds;
     acc += ds * A[((size_t)p * R + r) * D + d];
@@ -112,7 +128,7 @@ __global__ void __launch_bounds__(256) pair_bwd_b_fma(const T* __restrict__ A,
 // coalesced 256-byte rows and staged in LDS as [owned][streamed] next to the
 // matching 64 x D block of the other operand; four threads share an owned
 // index and each accumulates DPT of its D outputs, summing in a fixed order.
-template <typename T, int MET, bool COLS, int DPT>
+template <typename T, int MET, bool COLS, int DPT, bool DG>
 __global__ void __launch_bounds__(256) pair_bwd_tiled(const T* __restrict__ A,
                                                       const T* __restrict__ Bm,
                                                       const T* __restrict__ cost,
@@ -135,19 +151,40 @@ __global__ void __launch_bounds__(256) pair_bwd_tiled(const T* __restrict__ A,
   for (int s0 = 0; s0 < nstr; s0 += TL) {
     __syncthreads();
     const int r0 = COLS ? s0 : own0, c0 = COLS ? own0 : s0;
-#pragma unroll 4
-    for (int e = tid; e < TL * TL; e += 256) {
-      const int rr = e >> 6, cc = e & 63;
-      const int r = r0 + rr, c = c0 + cc;
-      T v = 0;
-      if (r < R && c < C) {
-        const size_t o = prc + (size_t)r * C + c;
-        v = cost_adjoint<T, MET>(dcost[o], MET == MET_RAW ? (T)0 : cost[o]);
+    if (DG) {
+      // by the tile's 127 anti-diagonals, four per pass: the cells of one are
+      // contiguous in the diagonal-major plane
+      for (int dd0 = 0; dd0 < 2 * TL - 1; dd0 += 4) {
+        const int dd = dd0 + (tid >> 6);
+        const int rr = (dd < TL ? 0 : dd - TL + 1) + (tid & 63), cc = dd - rr;
+        if (dd < 2 * TL - 1 && rr < TL && cc >= 0) {
+          const int r = r0 + rr, c = c0 + cc;
+          T v = 0;
+          if (r < R && c < C) {
+            const size_t o = prc + plane_index<true>(r, c, R, C);
+            v = cost_adjoint<T, MET>(dcost[o], MET == MET_RAW ? (T)0 : cost[o]);
+          }
+          if (COLS)
+            ds[cc][rr] = v;
+          else
+            ds[rr][cc] = v;
+        }
       }
-      if (COLS)
-        ds[cc][rr] = v;
-      else
-        ds[rr][cc] = v;
+    } else {
+#pragma unroll 4
+      for (int e = tid; e < TL * TL; e += 256) {
+        const int rr = e >> 6, cc = e & 63;
+        const int r = r0 + rr, c = c0 + cc;
+        T v = 0;
+        if (r < R && c < C) {
+          const size_t o = prc + (size_t)r * C + c;
+          v = cost_adjoint<T, MET>(dcost[o], MET == MET_RAW ? (T)0 : cost[o]);
+        }
+        if (COLS)
+          ds[cc][rr] = v;
+        else
+          ds[rr][cc] = v;
+      }
     }
     for (int e = tid; e < TL * 4 * DPT; e += 256) {
       const int si = e / (4 * DPT), d = e - si * (4 * DPT);
@@ -192,7 +229,7 @@ __device__ __forceinline__ f32x4 ld4(const Buf& b, int v, int s) {
                __uint_as_float(w.w)};
 }
 
-template <int MET, int TN>
+template <int MET, int TN, bool DG>
 __global__ void __launch_bounds__(256) pair_fwd_mfma(const float* __restrict__ A,
                                                      const float* __restrict__ Bm,
                                                      float* __restrict__ out, int R, int C,
@@ -253,7 +290,8 @@ __global__ void __launch_bounds__(256) pair_fwd_mfma(const float* __restrict__ A
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
       const int c = c0 + 16 * t + li;
-      if (r < R && c < C) o[(size_t)r * C + c] = finish_cost<float, MET>(nr + nb[t] - 2.f * acc[t][i]);
+      if (r < R && c < C)
+        o[plane_index<DG>(r, c, R, C)] = finish_cost<float, MET>(nr + nb[t] - 2.f * acc[t][i]);
     }
   }
 }
@@ -266,7 +304,7 @@ __global__ void __launch_bounds__(256) pair_fwd_mfma(const float* __restrict__ A
 // once: dA[r, d] = 2 (rs[r] a - sum_c dS[r,c] B[c,d]), dB partial
 // += dS[r, c] a, a = A[r, d]. A and B are read once and dA, dB written once.
 
-template <typename T, int MET, int CMAX>
+template <typename T, int MET, int CMAX, bool DG>
 __global__ void __launch_bounds__(256) pair_bwd_small(const T* __restrict__ A,
                                                       const T* __restrict__ Bm,
                                                       const T* __restrict__ cost,
@@ -283,7 +321,7 @@ __global__ void __launch_bounds__(256) pair_bwd_small(const T* __restrict__ A,
     const int r = e / CMAX, c = e % CMAX;
     T v = (T)0;
     if (c < C) {
-      const size_t o = prc + (size_t)r * C + c;
+      const size_t o = prc + plane_index<DG>(r, c, R, C);
       v = cost_adjoint<T, MET>(dcost[o], MET == MET_RAW ? (T)0 : cost[o]);
     }
     dS[e] = v;
@@ -331,10 +369,14 @@ __global__ void __launch_bounds__(256) pair_bwd_small(const T* __restrict__ A,
 
 static inline unsigned blocks_for(long long n) { return (unsigned)((n + 255) / 256); }
 
-template <typename T>
-int pair_cost_fwd(const T* A, const T* Bm, int P, int R, int C, int D, int metric, T* out,
-                  hipStream_t s, const char* what) {
+// DG: the cost plane is stored by anti-diagonals (plane_index; raw metric,
+// R <= C), as the uDTW sweeps read it.
+template <typename T, bool DG>
+static int pair_cost_fwd_impl(const T* A, const T* Bm, int P, int R, int C, int D, int metric,
+                              T* out, hipStream_t s, const char* what) {
   if (P < 0 || R <= 0 || C <= 0 || D <= 0) return fail(TW_EINVAL, "%s: bad sizes", what);
+  if (DG && (metric != MET_RAW || R > C))
+    return fail(TW_EINVAL, "%s: internal: diagonal planes are raw with R <= C", what);
   if (!A || !Bm || !out) return fail(TW_EINVAL, "%s: null pointer", what);
   if (P == 0) return TW_OK;
   if (P > 65535) return fail(TW_ESIZE, "%s: at most 65535 pairs per call", what);
@@ -351,31 +393,39 @@ int pair_cost_fwd(const T* A, const T* Bm, int P, int R, int C, int D, int metri
     const float* Bf = reinterpret_cast<const float*>(Bm);
     float* of = reinterpret_cast<float*>(out);
 #define TW_PAIR_MFMA(MET_, TN_) \
-  hipLaunchKernelGGL((pair_fwd_mfma<MET_, TN_>), grid, block, 0, s, Af, Bf, of, R, C, D)
+  hipLaunchKernelGGL((pair_fwd_mfma<MET_, TN_, DG>), grid, block, 0, s, Af, Bf, of, R, C, D)
 #define TW_PAIR_MFMA_TN(MET_)          \
   if (TN == 4) TW_PAIR_MFMA(MET_, 4);  \
   else if (TN == 2) TW_PAIR_MFMA(MET_, 2); \
   else TW_PAIR_MFMA(MET_, 1);
     if (metric == MET_RAW) { TW_PAIR_MFMA_TN(MET_RAW) }
-    else if (metric == MET_SQ) { TW_PAIR_MFMA_TN(MET_SQ) }
-    else { TW_PAIR_MFMA_TN(MET_EUC) }
+    else if constexpr (!DG) {
+      if (metric == MET_SQ) { TW_PAIR_MFMA_TN(MET_SQ) }
+      else { TW_PAIR_MFMA_TN(MET_EUC) }
+    }
 #undef TW_PAIR_MFMA_TN
 #undef TW_PAIR_MFMA
     return check_launch(what);
   }
   dim3 grid(blocks_for((long long)R * C), P), block(256);
-  switch (metric) {
-    case MET_RAW: hipLaunchKernelGGL((pair_fwd_fma<T, MET_RAW>), grid, block, 0, s, A, Bm, out, R, C, D); break;
-    case MET_SQ: hipLaunchKernelGGL((pair_fwd_fma<T, MET_SQ>), grid, block, 0, s, A, Bm, out, R, C, D); break;
-    default: hipLaunchKernelGGL((pair_fwd_fma<T, MET_EUC>), grid, block, 0, s, A, Bm, out, R, C, D); break;
+  if (metric == MET_RAW) {
+    hipLaunchKernelGGL((pair_fwd_fma<T, MET_RAW, DG>), grid, block, 0, s, A, Bm, out, R, C, D);
+  } else if constexpr (!DG) {
+    if (metric == MET_SQ)
+      hipLaunchKernelGGL((pair_fwd_fma<T, MET_SQ, false>), grid, block, 0, s, A, Bm, out, R, C, D);
+    else
+      hipLaunchKernelGGL((pair_fwd_fma<T, MET_EUC, false>), grid, block, 0, s, A, Bm, out, R, C, D);
   }
   return check_launch(what);
 }
 
-template <typename T>
-int pair_cost_bwd(const T* A, const T* Bm, const T* cost, const T* dcost, int P, int R, int C,
-                  int D, int metric, T* dA, T* dB, hipStream_t s, const char* what) {
+template <typename T, bool DG>
+static int pair_cost_bwd_impl(const T* A, const T* Bm, const T* cost, const T* dcost, int P,
+                              int R, int C, int D, int metric, T* dA, T* dB, hipStream_t s,
+                              const char* what) {
   if (P < 0 || R <= 0 || C <= 0 || D <= 0) return fail(TW_EINVAL, "%s: bad sizes", what);
+  if (DG && (metric != MET_RAW || R > C))
+    return fail(TW_EINVAL, "%s: internal: diagonal planes are raw with R <= C", what);
   if (!A || !Bm || !dcost || !dA || !dB) return fail(TW_EINVAL, "%s: null pointer", what);
   if (metric != MET_RAW && !cost) return fail(TW_EINVAL, "%s: metric needs the cost", what);
   if (P == 0) return TW_OK;
@@ -386,7 +436,7 @@ int pair_cost_bwd(const T* A, const T* Bm, const T* cost, const T* dcost, int P,
   const size_t lds = ((size_t)R * cmax + R + cmax) * sizeof(T);
   if (cmax && lds <= 48 * 1024) {
 #define TW_PAIR_SMALL(MET_, CM_)                                                            \
-  hipLaunchKernelGGL((pair_bwd_small<T, MET_, CM_>), dim3(P), dim3(256), lds, s, A, Bm, cost, \
+  hipLaunchKernelGGL((pair_bwd_small<T, MET_, CM_, DG>), dim3(P), dim3(256), lds, s, A, Bm, cost, \
                      dcost, dA, dB, R, C, D)
 #define TW_PAIR_SMALL_C(MET_)                  \
   if (cmax == 8) TW_PAIR_SMALL(MET_, 8);        \
@@ -394,8 +444,10 @@ int pair_cost_bwd(const T* A, const T* Bm, const T* cost, const T* dcost, int P,
   else if (cmax == 32) TW_PAIR_SMALL(MET_, 32); \
   else TW_PAIR_SMALL(MET_, 64);
     if (metric == MET_RAW) { TW_PAIR_SMALL_C(MET_RAW) }
-    else if (metric == MET_SQ) { TW_PAIR_SMALL_C(MET_SQ) }
-    else { TW_PAIR_SMALL_C(MET_EUC) }
+    else if constexpr (!DG) {
+      if (metric == MET_SQ) { TW_PAIR_SMALL_C(MET_SQ) }
+      else { TW_PAIR_SMALL_C(MET_EUC) }
+    }
 #undef TW_PAIR_SMALL_C
 #undef TW_PAIR_SMALL
     return check_launch(what);
@@ -405,9 +457,10 @@ int pair_cost_bwd(const T* A, const T* Bm, const T* cost, const T* dcost, int P,
     const int dpt = D <= 4 ? 1 : (D <= 8 ? 2 : (D <= 16 ? 4 : (D <= 32 ? 8 : 16)));
     const dim3 ga((R + 63) / 64, P), gb((C + 63) / 64, P), block(256);
 #define TW_PAIR_TILED(MET_, DPT_)                                                               \
-  hipLaunchKernelGGL((pair_bwd_tiled<T, MET_, false, DPT_>), ga, block, 0, s, A, Bm, cost,      \
+  hipLaunchKernelGGL((pair_bwd_tiled<T, MET_, false, DPT_, DG>), ga, block, 0, s, A, Bm, cost,  \
                      dcost, dA, R, C, D);                                                       \
-  hipLaunchKernelGGL((pair_bwd_tiled<T, MET_, true, DPT_>), gb, block, 0, s, A, Bm, cost, dcost, \
+  hipLaunchKernelGGL((pair_bwd_tiled<T, MET_, true, DPT_, DG>), gb, block, 0, s, A, Bm, cost,   \
+                     dcost, \
                      dB, R, C, D);
 #define TW_PAIR_TILED_D(MET_)                      \
   switch (dpt) {                                   \
@@ -422,38 +475,53 @@ int pair_cost_bwd(const T* A, const T* Bm, const T* cost, const T* dcost, int P,
       break;                                       \
   }
     if (metric == MET_RAW) { TW_PAIR_TILED_D(MET_RAW) }
-    else if (metric == MET_SQ) { TW_PAIR_TILED_D(MET_SQ) }
-    else { TW_PAIR_TILED_D(MET_EUC) }
+    else if constexpr (!DG) {
+      if (metric == MET_SQ) { TW_PAIR_TILED_D(MET_SQ) }
+      else { TW_PAIR_TILED_D(MET_EUC) }
+    }
 #undef TW_PAIR_TILED_D
 #undef TW_PAIR_TILED
     return check_launch(what);
   }
   dim3 ga(blocks_for((long long)R * D), P), gb(blocks_for((long long)C * D), P), block(256);
 #define TW_PAIR_BWD(MET_)                                                                     \
-  hipLaunchKernelGGL((pair_bwd_a_fma<T, MET_>), ga, block, 0, s, A, Bm, cost, dcost, dA, R,   \
-                     C, D);                                                                   \
-  hipLaunchKernelGGL((pair_bwd_b_fma<T, MET_>), gb, block, 0, s, A, Bm, cost, dcost, dB, R,   \
-                     C, D);
-  switch (metric) {
-    case MET_RAW: TW_PAIR_BWD(MET_RAW) break;
-    case MET_SQ: TW_PAIR_BWD(MET_SQ) break;
-    case MET_EUC: TW_PAIR_BWD(MET_EUC) break;
-    default: return fail(TW_EINVAL, "%s: unknown metric %d", what, metric);
+  hipLaunchKernelGGL((pair_bwd_a_fma<T, MET_, DG>), ga, block, 0, s, A, Bm, cost, dcost, dA, \
+                     R, C, D);                                                                \
+  hipLaunchKernelGGL((pair_bwd_b_fma<T, MET_, DG>), gb, block, 0, s, A, Bm, cost, dcost, dB, \
+                     R, C, D);
+  if (metric == MET_RAW) {
+    TW_PAIR_BWD(MET_RAW)
+  } else if constexpr (!DG) {
+    if (metric == MET_SQ) { TW_PAIR_BWD(MET_SQ) }
+    else { TW_PAIR_BWD(MET_EUC) }
   }
 #undef TW_PAIR_BWD
   return check_launch(what);
 }
 
+// Row-major cost planes (the public pairwise-cost entry points, JEANIE).
+template <typename T>
+int pair_cost_fwd(const T* A, const T* Bm, int P, int R, int C, int D, int metric, T* out,
+                  hipStream_t s, const char* what) {
+  return pair_cost_fwd_impl<T, false>(A, Bm, P, R, C, D, metric, out, s, what);
+}
+
+template <typename T>
+int pair_cost_bwd(const T* A, const T* Bm, const T* cost, const T* dcost, int P, int R, int C,
+                  int D, int metric, T* dA, T* dB, hipStream_t s, const char* what) {
+  return pair_cost_bwd_impl<T, false>(A, Bm, cost, dcost, P, R, C, D, metric, dA, dB, s, what);
+}
+
 template <typename T>
 int sqdist_raw(const T* X, const T* Y, int P, int R, int C, int D, T* out, hipStream_t s,
                const char* what) {
-  return pair_cost_fwd<T>(X, Y, P, R, C, D, MET_RAW, out, s, what);
+  return pair_cost_fwd_impl<T, true>(X, Y, P, R, C, D, MET_RAW, out, s, what);
 }
 
 template <typename T>
 int sqdist_raw_bwd(const T* X, const T* Y, const T* dS, int P, int R, int C, int D, T* dX, T* dY,
                    hipStream_t s, const char* what) {
-  return pair_cost_bwd<T>(X, Y, nullptr, dS, P, R, C, D, MET_RAW, dX, dY, s, what);
+  return pair_cost_bwd_impl<T, true>(X, Y, nullptr, dS, P, R, C, D, MET_RAW, dX, dY, s, what);
 }
 
 template int sqdist_raw<float>(const float*, const float*, int, int, int, int, float*,

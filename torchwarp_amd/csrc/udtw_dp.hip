@@ -148,7 +148,9 @@ int tw_udtw_cost_bwd_f64(const double* cost, const double* pen, const double* R,
 
 }  // extern "C"
 
-// Features path: defined with the pairwise-distance kernels it uses for D > 1.
+// Features path: defined with the pairwise-distance kernels it uses for D > 1,
+// which keep the squared distances (and their adjoint) in the sweeps'
+// diagonal-major layout.
 namespace tw {
 
 template <typename T>

@@ -25,9 +25,10 @@
 //
 // Cost sources (template SRC):
 //   SRC_COST  C, Q given as [B,N,M]                   -> writes dC, dQ
-//   SRC_SQ    raw squared distance S = x2+y2-2x.y [B,N,M] and variances
+//   SRC_SQ    raw squared distance S = x2+y2-2x.y [B, N*M] diagonal-major
+//             (as R, so every diagonal's access is coalesced) and variances
 //             vx [B,N], vy [B,M]: C = max(S,0)/max((vx+vy)/2,eps),
-//             Q = beta ln max(...)                      -> writes dS, dvx, dvy
+//             Q = beta ln max(...)                      -> writes dS (same layout), dvx, dvy
 //   SRC_FEAT1 one feature per step, x [B,N], y [B,M] and variances,
 //             C from (x-y)^2 in registers               -> writes dx, dy, dvx, dvy
 // Column sums (dy, dvy) travel up the rows with their column and are stored
@@ -166,15 +167,24 @@ __host__ __device__ __forceinline__ int col_pad(int N, int nw) {
   return 64 * nw + N + kLag * nw + 8;
 }
 
-template <int ROWS>
+// Threads per workgroup a kernel is compiled for. The forward with one row
+// per thread and the columns travelling by DPP (no LDS columns) serves long
+// sequences with up to 16 wavefronts (8 in float64), so a SIMD holds several
+// of the pair's wavefronts and hides their waits (cfg3 forward: 2.20 -> 1.95
+// ms against 4 rows per thread). The backward, with twice the live state
+// per row, is faster with 4 rows per thread and one wavefront per SIMD
+// (3.49 against 3.86 ms), so it keeps 256 threads.
+template <typename T, int ROWS, bool LC, bool BWD>
 struct MaxThreads {
-  static constexpr int value = ROWS >= 16 ? 1024 : 256;
+  static constexpr int value =
+      ROWS >= 16 ? 1024
+                 : ((ROWS == 1 && !LC && !BWD) ? (sizeof(T) == 4 ? 1024 : 512) : 256);
 };
 
 // LC (one row per thread): the column operands come from LDS (ColRec);
 // otherwise they travel down the rows with the DPP shifts that move R.
 template <typename T, int ROWS, int SRC, bool PEN, bool BAND, int PF, bool LC>
-__global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwArgs<T> a) {
+__global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_fwd_kernel(UdtwArgs<T> a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   constexpr int ES = sizeof(T);
   constexpr bool COLS = SRC != SRC_COST;
@@ -248,11 +258,14 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwA
   const int steps = (Dn + kLag * (nw - 1) + kSlots - 1) / kSlots * kSlots;
 
   T rc[PF][ROWS], rq[PF][ROWS];
-  // C (and Q) of diagonal d at byte soffset so = max(d, 0) * ES
+  // C (and Q) of diagonal d at byte soffset so: max(d, 0) * ES in the [N, M]
+  // layout, soff(d) * ES in the diagonal-major one (SRC_SQ)
+  constexpr bool DG = SRC == SRC_SQ;
+  auto fetch_so = [&](int d) { return DG ? diag_soff(d, N, M) * ES : (d > 0 ? d : 0) * ES; };
   auto fetch = [&](int d, int so, T* c, T* q) {
 #pragma unroll
     for (int k = 0; k < ROWS; ++k) {
-      const int vo = (unsigned)(d + jb[k]) < (unsigned)M ? vnat[k] : kOob;
+      const int vo = (unsigned)(d + jb[k]) < (unsigned)M ? (DG ? vst[k] : vnat[k]) : kOob;
       c[k] = bC.ld<T>(vo, so);
       if (SRC == SRC_COST && PEN) q[k] = bQ.ld<T>(vo, so);
     }
@@ -261,7 +274,7 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwA
 #pragma unroll
     for (int u = 0; u < PF; ++u) {
       const int d = d_first + u;
-      fetch(d, (d > 0 ? d : 0) * ES, rc[u], rq[u]);
+      fetch(d, fetch_so(d), rc[u], rq[u]);
     }
   }
 
@@ -293,7 +306,7 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwA
       // lane l: byte soffsets of step tw + l (R / P store, C / Q fetch)
       const int dl = d_first + tw + lane;
       const int so_st = diag_soff(dl, N, M) * ES;
-      const int so_ld = SRC != SRC_FEAT1 ? (dl + PF > 0 ? dl + PF : 0) * ES : 0;
+      const int so_ld = SRC != SRC_FEAT1 ? fetch_so(dl + PF) : 0;
       const int tn = min(kWindow, steps - tw);
     for (int t0 = 0; t0 < tn; t0 += kSlots) {
       const int half = (t0 / kSlots) & 1;   // mailbox half of this block
@@ -445,7 +458,7 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_fwd_kernel(UdtwA
 // in a fixed order at the end. Otherwise both travel along the rows with DPP
 // shifts.
 template <typename T, int ROWS, int SRC, bool PEN, bool BAND, int PF, bool LC>
-__global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwArgs<T> a) {
+__global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_bwd_kernel(UdtwArgs<T> a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   constexpr int ES = sizeof(T);
   constexpr bool COLS = SRC != SRC_COST;
@@ -568,7 +581,9 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
       const int vd = v ? vst[k] : kOob;
       r[k] = bR.ld<T>(vd, so_d);
       if (PEN) p[k] = bP.ld<T>(vd, so_d);
-      if (SRC != SRC_FEAT1) {
+      if (SRC == SRC_SQ) {
+        c[k] = bC.ld<T>(vd, so_d);   // diagonal-major, as R
+      } else if (SRC != SRC_FEAT1) {
         const int vn = v ? vnat[k] : kOob;
         c[k] = bC.ld<T>(vn, so_n);
         if (SRC == SRC_COST && PEN) q[k] = bQ.ld<T>(vn, so_n);
@@ -610,8 +625,10 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
       // the stores of the step's own diagonal)
       const int dl = d_first - tw - lane;
       const int so_fd = diag_soff(dl - PF, N, M) * ES;
-      const int so_fn = SRC != SRC_FEAT1 ? (dl - PF > 0 ? dl - PF : 0) * ES : 0;
+      const int so_fn = SRC == SRC_COST ? (dl - PF > 0 ? dl - PF : 0) * ES : 0;
       const int so_st = (dl > 0 ? dl : 0) * ES;
+      // SRC_SQ: the diagonal-major soffset of the step's own diagonal (dS store)
+      const int so_sd = SRC == SRC_SQ ? diag_soff(dl, N, M) * ES : 0;
       const int tn = min(kWindow, steps - tw);
     for (int t0 = 0; t0 < tn; t0 += kSlots) {
       const int half = (t0 / kSlots) & 1;   // mailbox half of this block
@@ -753,7 +770,8 @@ __global__ void __launch_bounds__(MaxThreads<ROWS>::value) udtw_bwd_kernel(UdtwA
             if (PEN) bdQ.st(h, vn, so_n);
           } else {
             const T dsq = sq_raw > (T)0 ? g * rv : (T)0;
-            if (SRC == SRC_SQ) bdC.st(dsq, vn, so_n);
+            if (SRC == SRC_SQ)
+              bdC.st(dsq, valid ? vst[k] : kOob, __builtin_amdgcn_readlane(so_sd, t0 + u));
             T df = (T)0;
             if (SRC == SRC_FEAT1) {
               df = valid ? (T)2 * dsq * (xr[k] - yc[k]) : (T)0;
@@ -857,19 +875,26 @@ struct Shape {
   int threads;
 };
 
-// Rows per thread and threads per pair for a grid with N rows (N <= M).
-// Up to 4 wavefronts (one per SIMD of a CU), more rows per thread beyond.
-static Shape pick_shape(int N) {
+// Rows per thread and threads per pair for a grid with N rows (N <= M): one
+// row per thread up to the one-row kernels' thread limit (forward 1024, or
+// 512 in float64; backward 256), more rows per thread beyond (up to 16, 256
+// threads; 1024 threads at 16 rows).
+template <typename T>
+static Shape pick_shape(int N, bool backward) {
+  const int one_row_max =
+      backward ? MaxThreads<T, 1, false, true>::value : MaxThreads<T, 1, false, false>::value;
   int rows = 1;
-  while (rows < 16 && (N + rows - 1) / rows > 256) rows *= 2;
+  if (N > one_row_max)
+    while (rows < 16 && (N + rows - 1) / rows > 256) rows *= 2;
   // tuning override: TORCHWARP_UDTW_ROWS = 1, 2, 4, 8 or 16 rows per thread,
   // taken when the kernel's thread limit for that row count allows it
   static const int forced = [] {
     const char* e = getenv("TORCHWARP_UDTW_ROWS");
     return e ? atoi(e) : 0;
   }();
+  const int fmax = forced == 1 ? one_row_max : (forced >= 16 ? 1024 : 256);
   if ((forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16) &&
-      (N + forced - 1) / forced <= (forced >= 16 ? 1024 : 256))
+      (N + forced - 1) / forced <= fmax)
     rows = forced;
   int threads = (N + rows - 1) / rows;
   if (threads > 1024) return {0, 0};
@@ -905,7 +930,7 @@ template <typename T, int SRC, bool PEN, bool BAND>
 static int launch_udtw(bool backward, const UdtwArgs<T>& a, int B, hipStream_t stream,
                        const char* what) {
   if (B == 0) return TW_OK;
-  const Shape sh = pick_shape(a.N);
+  const Shape sh = pick_shape<T>(a.N, backward);
   if (sh.rows == 0) {
     return fail(TW_ESIZE, "%s: the shorter sequence has %d steps; this build handles up to 16384",
                 what, a.N);
@@ -919,7 +944,7 @@ static int launch_udtw(bool backward, const UdtwArgs<T>& a, int B, hipStream_t s
   // they fit in a quarter of it (several workgroups per CU stay resident)
   if constexpr (SRC != SRC_COST) {
     const size_t lc_lds = udtw_lds<T>(backward, nw, true, a.N, a.M);
-    if (sh.rows == 1 && lc_lds <= (size_t)max_lds_bytes() / 4) {
+    if (sh.rows == 1 && sh.threads <= 256 && lc_lds <= (size_t)max_lds_bytes() / 4) {
       if (backward)
         hipLaunchKernelGGL((udtw_bwd_kernel<T, 1, SRC, PEN, BAND, PrefetchDepth<1>::value, true>),
                            grid, block, lc_lds, stream, a);
