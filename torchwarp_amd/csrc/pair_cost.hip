@@ -135,7 +135,10 @@ __global__ void __launch_bounds__(256) pair_bwd_tiled(const T* __restrict__ A,
                                                       const T* __restrict__ dcost,
                                                       T* __restrict__ dOut, int R, int C, int D) {
   constexpr int TL = 64;
-  __shared__ T ds[TL][TL + 1];
+  // row pitch: TL + 1 keeps row-wise and column-wise accesses conflict-free;
+  // the diagonal loads (DG) need TL + 2 (a diagonal's cells then fall in
+  // distinct banks)
+  __shared__ T ds[TL][TL + (DG ? 2 : 1)];
   __shared__ T op[TL][4 * DPT + 1];
   const int p = blockIdx.y, tid = threadIdx.x;
   const int own0 = blockIdx.x * TL;
@@ -152,22 +155,33 @@ __global__ void __launch_bounds__(256) pair_bwd_tiled(const T* __restrict__ A,
     __syncthreads();
     const int r0 = COLS ? s0 : own0, c0 = COLS ? own0 : s0;
     if (DG) {
-      // by the tile's 127 anti-diagonals, four per pass: the cells of one are
-      // contiguous in the diagonal-major plane
-      for (int dd0 = 0; dd0 < 2 * TL - 1; dd0 += 4) {
-        const int dd = dd0 + (tid >> 6);
-        const int rr = (dd < TL ? 0 : dd - TL + 1) + (tid & 63), cc = dd - rr;
+      // by the tile's 127 anti-diagonals, four per pass (one per wavefront):
+      // the cells of one are contiguous in the diagonal-major plane, so the
+      // wavefront-uniform start of its run is computed once; all 32 loads
+      // are issued before the LDS stores
+      const int wv = __builtin_amdgcn_readfirstlane(tid >> 6), ln = tid & 63;
+      T v[(2 * TL) / 4];
+#pragma unroll
+      for (int it = 0; it < (2 * TL) / 4; ++it) {
+        const int dd = 4 * it + wv;
+        const int rr = (dd < TL ? 0 : dd - TL + 1) + ln, cc = dd - rr;
+        const int r = r0 + rr, c = c0 + cc, d = r0 + c0 + dd;
+        const long long run = diag_offset(d, R, C) - (d - C + 1 > 0 ? d - C + 1 : 0);
+        v[it] = 0;
+        if (dd < 2 * TL - 1 && rr < TL && cc >= 0 && r < R && c < C) {
+          const size_t o = prc + (size_t)(run + r);
+          v[it] = cost_adjoint<T, MET>(dcost[o], MET == MET_RAW ? (T)0 : cost[o]);
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < (2 * TL) / 4; ++it) {
+        const int dd = 4 * it + wv;
+        const int rr = (dd < TL ? 0 : dd - TL + 1) + ln, cc = dd - rr;
         if (dd < 2 * TL - 1 && rr < TL && cc >= 0) {
-          const int r = r0 + rr, c = c0 + cc;
-          T v = 0;
-          if (r < R && c < C) {
-            const size_t o = prc + plane_index<true>(r, c, R, C);
-            v = cost_adjoint<T, MET>(dcost[o], MET == MET_RAW ? (T)0 : cost[o]);
-          }
           if (COLS)
-            ds[cc][rr] = v;
+            ds[cc][rr] = v[it];
           else
-            ds[rr][cc] = v;
+            ds[rr][cc] = v[it];
         }
       }
     } else {
@@ -283,16 +297,38 @@ __global__ void __launch_bounds__(256) pair_fwd_mfma(const float* __restrict__ A
     nb[t] += __shfl_xor(nb[t], 32);
   }
   float* o = out + (size_t)p * R * C;
+  if (!DG) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = r0 + 4 * g + i;
+      const float nr = __shfl(na, 4 * g + i);   // lane 4g+i holds row 4g+i's norm
+#pragma unroll
+      for (int t = 0; t < TN; ++t) {
+        const int c = c0 + 16 * t + li;
+        if (r < R && c < C) o[(size_t)r * C + c] = finish_cost<float, MET>(nr + nb[t] - 2.f * acc[t][i]);
+      }
+    }
+    return;
+  }
+  // Diagonal-major plane: the wavefront's 16 x 16 TN strip goes through LDS
+  // and leaves by anti-diagonals, four per store (one per 16 lanes), each a
+  // contiguous run of up to 16 cells. Only this wavefront touches its tile,
+  // and its LDS operations complete in order.
+  constexpr int W = 16 * TN, PITCH = W + 2;   // pitch W + 2: a diagonal's cells in distinct banks
+  __shared__ float tile[4][16][PITCH];
+  float(*tl)[PITCH] = tile[threadIdx.x >> 6];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int r = r0 + 4 * g + i;
-    const float nr = __shfl(na, 4 * g + i);   // lane 4g+i holds row 4g+i's norm
+    const float nr = __shfl(na, 4 * g + i);
 #pragma unroll
-    for (int t = 0; t < TN; ++t) {
-      const int c = c0 + 16 * t + li;
-      if (r < R && c < C)
-        o[plane_index<DG>(r, c, R, C)] = finish_cost<float, MET>(nr + nb[t] - 2.f * acc[t][i]);
-    }
+    for (int t = 0; t < TN; ++t)
+      tl[4 * g + i][16 * t + li] = finish_cost<float, MET>(nr + nb[t] - 2.f * acc[t][i]);
+  }
+  for (int dd0 = 0; dd0 < 16 + W - 1; dd0 += 4) {
+    const int dd = dd0 + g, rr = li, cc = dd - rr;
+    const int r = r0 + rr, c = c0 + cc;
+    if (dd < 16 + W - 1 && cc >= 0 && cc < W && r < R && c < C)
+      o[plane_index<true>(r, c, R, C)] = tl[rr][cc];
   }
 }
 
