@@ -167,18 +167,16 @@ __host__ __device__ __forceinline__ int col_pad(int N, int nw) {
   return 64 * nw + N + kLag * nw + 8;
 }
 
-// Threads per workgroup a kernel is compiled for. The forward with one row
-// per thread and the columns travelling by DPP (no LDS columns) serves long
-// sequences with up to 16 wavefronts (8 in float64), so a SIMD holds several
-// of the pair's wavefronts and hides their waits (cfg3 forward: 2.20 -> 1.95
-// ms against 4 rows per thread). The backward, with twice the live state
-// per row, is faster with 4 rows per thread and one wavefront per SIMD
-// (3.49 against 3.86 ms), so it keeps 256 threads.
+// Threads per workgroup a kernel is compiled for. One row per thread with
+// the columns travelling by DPP (no LDS columns) serves long sequences with
+// up to 16 wavefronts (8 in float64, whose backward needs ~180 VGPRs), so a
+// SIMD holds several of the pair's wavefronts and hides their waits: at
+// N = M = 1024 the sweeps take 0.93 / 1.76 ms against 1.28 / 2.24 ms with
+// 4 rows per thread and one wavefront per SIMD.
 template <typename T, int ROWS, bool LC, bool BWD>
 struct MaxThreads {
   static constexpr int value =
-      ROWS >= 16 ? 1024
-                 : ((ROWS == 1 && !LC && !BWD) ? (sizeof(T) == 4 ? 1024 : 512) : 256);
+      ROWS >= 16 ? 1024 : ((ROWS == 1 && !LC) ? (sizeof(T) == 4 ? 1024 : 512) : 256);
 };
 
 // LC (one row per thread): the column operands come from LDS (ColRec);
@@ -876,9 +874,9 @@ struct Shape {
 };
 
 // Rows per thread and threads per pair for a grid with N rows (N <= M): one
-// row per thread up to the one-row kernels' thread limit (forward 1024, or
-// 512 in float64; backward 256), more rows per thread beyond (up to 16, 256
-// threads; 1024 threads at 16 rows).
+// row per thread up to the one-row kernels' thread limit (1024, or 512 in
+// float64), more rows per thread beyond (up to 16, 256 threads; 1024
+// threads at 16 rows).
 template <typename T>
 static Shape pick_shape(int N, bool backward) {
   const int one_row_max =
