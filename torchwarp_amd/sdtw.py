@@ -6,7 +6,7 @@ import torch
 import torch.nn as nn
 
 from .udtw import _ops as _udtw_ops
-from .udtw.functional import _BACKENDS, _check_band_reached, udtw, udtw_from_cost
+from .udtw.functional import _BACKENDS, _batchable, _check_band_reached, udtw, udtw_from_cost
 
 
 def softmin(x: torch.Tensor, gamma: float, dim: Optional[int] = None) -> torch.Tensor:
@@ -84,6 +84,11 @@ def soft_dtw(X: torch.Tensor, Y: torch.Tensor, *, gamma: float = 1.0, normalize:
         return udtw_from_cost(cost, torch.zeros_like(cost), gamma=gamma, bandwidth=bandwidth,
                               backend=backend).distance
 
+    if normalize and dist_func is None and _batchable(X, Y):
+        # one launch over 3B pairs when N == M (see udtw; a user dist_func
+        # keeps three calls, since it sees the whole batch)
+        d_xy, d_xx, d_yy = run(torch.cat((X, X, Y)), torch.cat((Y, X, Y))).split(X.shape[0])
+        return d_xy - 0.5 * (d_xx + d_yy)
     d = run(X, Y)
     if not normalize:
         return d

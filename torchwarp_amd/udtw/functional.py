@@ -82,6 +82,14 @@ def pairwise_matrices(X, Y, sigma_x, sigma_y, beta=1.0, eps=1e-8, *, method="gem
     return weighted_cost, weighted_penalty, variance
 
 
+def _batchable(*tensors):
+    """The normalized terms can run as one batch: equal lengths (dim 1), one
+    dtype and one device, and a non-empty batch."""
+    X = tensors[0]
+    return (X.shape[0] > 0 and all(t.shape[1] == X.shape[1] for t in tensors)
+            and all(t.dtype == X.dtype and t.device == X.device for t in tensors))
+
+
 def _check_band_reached(distance, band):
     # data-dependent; skipped while torch.compile traces (then +inf shows instead)
     if band > 0 and not torch.compiler.is_compiling():
@@ -182,6 +190,15 @@ def udtw(X, Y, sigma_x, sigma_y, *, beta=1.0, gamma=1.0, normalize=False, bandwi
         cost, pen, _ = pairwise_matrices(A, Bq, sa, sb, beta, eps, method=method)
         return udtw_from_cost(cost, pen, gamma=gamma, bandwidth=bandwidth, backend=backend)
 
+    if normalize and _batchable(X, Y, sigma_x, sigma_y):
+        # d(X,Y), d(X,X) and d(Y,Y) share one grid shape when N == M: one
+        # launch over 3B pairs (each pair is computed independently, so the
+        # values are those of three separate calls)
+        B = X.shape[0]
+        d, p = run(torch.cat((X, X, Y)), torch.cat((Y, X, Y)),
+                   torch.cat((sigma_x, sigma_x, sigma_y)), torch.cat((sigma_y, sigma_x, sigma_y)))
+        (d_xy, d_xx, d_yy), (p_xy, p_xx, p_yy) = d.split(B), p.split(B)
+        return UDTWOutput(d_xy - 0.5 * (d_xx + d_yy), p_xy - 0.5 * (p_xx + p_yy))
     d_xy, p_xy = run(X, Y, sigma_x, sigma_y)
     if not normalize:
         return UDTWOutput(d_xy, p_xy)
