@@ -1,0 +1,78 @@
+"""uDTW launch layouts for longer and ragged sequences against the float64 oracle.
+
+The launcher gives one row per thread up to 1024 rows (512 in float64), with
+the column operands in LDS up to 256 rows and travelling by DPP beyond, then
+several rows per thread. For D > 1 the squared distances and their adjoint
+sit diagonal-major between the pair-cost kernels and the sweeps. These
+shapes put each layout (N just past 256, 512 and 1024; N > M, which the API
+swaps; D = 1 and D > 1; the precomputed-cost path) under the forward and
+the backward.
+"""
+
+import pytest
+import torch
+
+from oracle import udtw as OU
+import torchwarp_amd as tw
+import torchwarp_amd.functional as TF
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a ROCm GPU")]
+
+SHAPES = [  # (B, N, M, D, gamma)
+    (2, 300, 310, 1, 1.0),
+    (2, 290, 270, 4, 1.0),     # N > M: the API swaps the sequences
+    (1, 600, 640, 8, 1.0),     # one row per thread in float32, two in float64
+    (1, 1100, 1030, 1, 1.0),   # beyond 1024 rows: several rows per thread
+]
+
+
+def _maxnorm(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return ((a - b).abs().max() / b.abs().max()).item()
+
+
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "B{}N{}M{}D{}".format(*s[:4]))
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_udtw_features_layouts(shape, dtype):
+    B, N, M, D, gamma = shape
+    g = torch.Generator().manual_seed(5)
+    X = torch.randn(B, N, D, generator=g, dtype=torch.float64) / D ** 0.5
+    Y = torch.randn(B, M, D, generator=g, dtype=torch.float64) / D ** 0.5
+    sx = 0.5 + torch.rand(B, N, 1, generator=g, dtype=torch.float64)
+    sy = 0.5 + torch.rand(B, M, 1, generator=g, dtype=torch.float64)
+    xs = [t.to("cuda", dtype).requires_grad_(True) for t in (X, Y, sx, sy)]
+    d, p = tw.UDTW(gamma=gamma, beta=1.0)(*xs)
+    (d + p).sum().backward()
+    ref = [t.clone().requires_grad_(True) for t in (X, Y, sx, sy)]
+    rd, rp = OU.udtw(*ref, gamma=gamma, beta=1.0)
+    (rd + rp).sum().backward()
+    got = [d, p] + [t.grad for t in xs]
+    want = [rd, rp] + [t.grad for t in ref]
+    errs = [_maxnorm(a, b) for a, b in zip(got, want)]
+    if dtype == torch.float64:
+        assert max(errs) < 1e-9, errs
+    else:
+        assert max(errs[:2]) < 1e-5, errs
+        assert max(errs[2:]) < 2e-3, errs
+
+
+@pytest.mark.parametrize("NM", [(300, 330), (700, 650)])
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_udtw_cost_layouts(NM, dtype):
+    N, M = NM
+    g = torch.Generator().manual_seed(6)
+    C = torch.rand(2, N, M, generator=g, dtype=torch.float64)
+    Q = 0.2 * torch.rand(2, N, M, generator=g, dtype=torch.float64)
+    c, q = C.to("cuda", dtype).requires_grad_(True), Q.to("cuda", dtype).requires_grad_(True)
+    d, p = TF.udtw_from_cost(c, q, gamma=0.5)
+    (d + 3 * p).sum().backward()
+    rc, rq = C.clone().requires_grad_(True), Q.clone().requires_grad_(True)
+    rd, rp = OU.udtw_from_cost(rc, rq, gamma=0.5)
+    (rd + 3 * rp).sum().backward()
+    errs = [_maxnorm(a, b) for a, b in zip([d, p, c.grad, q.grad], [rd, rp, rc.grad, rq.grad])]
+    if dtype == torch.float64:
+        assert max(errs) < 1e-9, errs
+    else:
+        assert max(errs[:2]) < 1e-5, errs
+        assert max(errs[2:]) < 2e-3, errs
