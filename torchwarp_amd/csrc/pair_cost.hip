@@ -15,9 +15,10 @@
 // (v_mfma_f32_16x16x4f32, a 16 x 16*TN output strip per wavefront); fp64 and
 // other D on a plain FMA kernel. Backward: when a pair's dS fits in LDS and
 // C <= 64, one fused kernel per pair streams A and B once (threads along D,
-// dB partial sums in registers); otherwise, for D <= 64, two tiled passes
-// that each read dS once (dA by row blocks, dB by column blocks), and two
-// FMA kernels beyond.
+// dB partial sums in registers); otherwise, for D <= 64 (32 in fp64), two
+// tiled passes that each read dS once (dA by row blocks, dB by column
+// blocks), contracting on the matrix cores in fp32, and two FMA kernels
+// beyond.
 //
 // The uDTW feature path (sqdist_raw / sqdist_raw_bwd) keeps S and dS by
 // anti-diagonals (plane_index), the layout in which the sweeps' per-diagonal
@@ -122,7 +123,7 @@ __global__ void __launch_bounds__(256) pair_bwd_b_fma(const T* __restrict__ A,
 }
 
 
-// Tiled backward for D <= 64, one pass over dS per output: a workgroup owns
+// Tiled fp64 backward for D <= 32, one pass over dS per output: a workgroup owns
 // 64 rows (dA, COLS false) or 64 columns (dB, COLS true) of a pair and
 // streams the other axis in 64-wide tiles. Each dS tile is read with
 // coalesced 256-byte rows and staged in LDS as [owned][streamed] next to the
@@ -332,6 +333,167 @@ __global__ void __launch_bounds__(256) pair_fwd_mfma(const float* __restrict__ A
   }
 }
 
+// ---------------------------------------------------------- MFMA backward
+//
+// fp32, D <= 64: the tiled backward's two passes (dA by 64-row blocks, dB by
+// 64-column blocks, each reading dS once) with the contraction on the matrix
+// cores. A workgroup owns 64 indices of one side; per 64-wide tile of the
+// streamed side it stages dS as ds[owned][streamed] and the other operand
+// transposed, opT[d][streamed], both with rows of 68 floats (16-byte aligned
+// for the float4 reads; the diagonal stores of the DG loader step 67 banks
+// per lane, so they do not conflict). Wavefront w owns rows 16w..16w+15 and
+// accumulates its 16 x 16NB block of dS . other with v_mfma_f32_16x16x4f32,
+// lane l reading the float4s ds[16w + l % 16][k0 + 4 (l / 16)] and
+// opT[16n + l % 16][k0 + 4 (l / 16)] (the k-permuted operand layout of the
+// forward). The row sums of dS come from the same float4s. The next tile's
+// dS is loaded into registers before the MFMAs of this one. Workgroups are
+// numbered so that the tiles of one pair run on one XCD (the hardware
+// assigns workgroup i to XCD i % 8): the runs of a diagonal-major tile share
+// their end cache lines with the neighbouring tiles.
+template <int MET, bool COLS, int NB, bool DG>
+__global__ void __launch_bounds__(256) pair_bwd_mfma(const float* __restrict__ A,
+                                                     const float* __restrict__ Bm,
+                                                     const float* __restrict__ cost,
+                                                     const float* __restrict__ dcost,
+                                                     float* __restrict__ dOut, int P, int R,
+                                                     int C, int D) {
+  constexpr int TL = 64, PT = TL + 4;
+  __shared__ __align__(16) float ds[TL][PT];
+  __shared__ __align__(16) float opT[16 * NB][PT];
+  const int nown = COLS ? C : R, nstr = COLS ? R : C;
+  const int gx = (nown + TL - 1) / TL;
+  const unsigned total = (unsigned)gx * P, L = blockIdx.x;
+  const unsigned id = (total & 7) ? L : (L & 7) * (total >> 3) + (L >> 3);
+  const int p = id / gx, own0 = (id % gx) * TL;
+  const int tid = threadIdx.x, ln = tid & 63, lr = ln & 15, lg = ln >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const size_t prc = (size_t)p * R * C;
+  const float* other = COLS ? A + (size_t)p * R * D : Bm + (size_t)p * C * D;
+  const float* self = COLS ? Bm + (size_t)p * C * D : A + (size_t)p * R * D;
+
+  // The next tile goes into registers while this one is contracted: dS (DG
+  // by the tile's 127 anti-diagonals, four per pass, one per wavefront, each
+  // a contiguous run; else by rows) and the other operand's 64 x 16NB block.
+  // Lane l first computes the run starts of tile diagonals l and l + 64,
+  // which each pass then takes with v_readlane. Loads are raw buffer loads;
+  // lanes outside the plane pass kOob and read 0.
+  constexpr int NV = DG ? (2 * TL) / 4 : TL * TL / 256, NW = 4 * NB;
+  Buf bd, bo;
+  bd.init(dcost + prc, (long long)R * C);
+  bo.init(other, (long long)nstr * D);
+  float v[NV], w[NW];
+  auto load = [&](int s0) {
+    const int r0 = COLS ? s0 : own0, c0 = COLS ? own0 : s0;
+    int run[2] = {0, 0};
+    if (DG) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int d = r0 + c0 + 64 * h + ln;
+        if (d <= R + C - 2)
+          run[h] = (int)(diag_offset(d, R, C) - (d - C + 1 > 0 ? d - C + 1 : 0));
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < NV; ++it) {
+      int r, c, so = 0;
+      bool ok;
+      if (DG) {
+        const int dd = 4 * it + wv;   // it < 16: dd < 64
+        const int rr = (dd < TL ? 0 : dd - TL + 1) + ln, cc = dd - rr;
+        r = r0 + rr;
+        c = c0 + cc;
+        ok = dd < 2 * TL - 1 && rr < TL && cc >= 0;
+        so = __builtin_amdgcn_readlane(run[it < 16 ? 0 : 1], dd & 63) * 4;
+      } else {
+        const int e = it * 256 + tid;
+        r = r0 + (e >> 6);
+        c = c0 + (e & 63);
+        ok = true;
+      }
+      const int vo = !(ok && r < R && c < C) ? kOob : (DG ? r : r * C + c) * 4;
+      if (MET == MET_RAW) {
+        v[it] = bd.ldf(vo, so);
+      } else {
+        const size_t oo = prc + (size_t)r * C + c;
+        v[it] = vo == kOob ? 0.f : cost_adjoint<float, MET>(dcost[oo], cost[oo]);
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < NW; ++it) {
+      const int e = it * 256 + tid, si = e & 63, dcol = e >> 6;
+      w[it] = bo.ldf(s0 + si < nstr && dcol < D ? ((s0 + si) * D + dcol) * 4 : kOob, 0);
+    }
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int it = 0; it < NV; ++it) {
+      int rr, cc;
+      bool ok;
+      if (DG) {
+        const int dd = 4 * it + wv;
+        rr = (dd < TL ? 0 : dd - TL + 1) + ln;
+        cc = dd - rr;
+        ok = dd < 2 * TL - 1 && rr < TL && cc >= 0;
+      } else {
+        const int e = it * 256 + tid;
+        rr = e >> 6;
+        cc = e & 63;
+        ok = true;
+      }
+      if (ok) {
+        if (COLS)
+          ds[cc][rr] = v[it];
+        else
+          ds[rr][cc] = v[it];
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < NW; ++it) {
+      const int e = it * 256 + tid;
+      opT[e >> 6][e & 63] = w[it];
+    }
+  };
+
+  f32x4 acc[NB];
+#pragma unroll
+  for (int n = 0; n < NB; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float rs = 0.f;
+  load(0);
+  for (int s0 = 0; s0 < nstr; s0 += TL) {
+    __syncthreads();   // the previous tile's LDS reads are done
+    stash();
+    __syncthreads();
+    if (s0 + TL < nstr) load(s0 + TL);
+#pragma unroll
+    for (int kb = 0; kb < TL; kb += 16) {
+      const f32x4 a4 = *reinterpret_cast<const f32x4*>(&ds[16 * wv + lr][kb + 4 * lg]);
+      rs += (a4.x + a4.y) + (a4.z + a4.w);
+#pragma unroll
+      for (int n = 0; n < NB; ++n) {
+        const f32x4 b4 = *reinterpret_cast<const f32x4*>(&opT[16 * n + lr][kb + 4 * lg]);
+        acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.x, b4.x, acc[n], 0, 0, 0);
+        acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.y, b4.y, acc[n], 0, 0, 0);
+        acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.z, b4.z, acc[n], 0, 0, 0);
+        acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.w, b4.w, acc[n], 0, 0, 0);
+      }
+    }
+  }
+  // row sums: the four k groups of row l % 16 sit in lanes l % 16 + 16 g
+  rs += __shfl_xor(rs, 16);
+  rs += __shfl_xor(rs, 32);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int o = own0 + 16 * wv + 4 * lg + i;   // result row of register i
+    const float so = __shfl(rs, 4 * lg + i);
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+      const int d = 16 * n + lr;
+      if (o < nown && d < D)
+        dOut[((size_t)p * nown + o) * D + d] = 2.f * (so * self[(size_t)o * D + d] - acc[n][i]);
+    }
+  }
+}
+
 // ------------------------------------------------ fused per-pair backward
 //
 // One workgroup per pair with dS = adjoint(dcost) [R, C] in LDS together
@@ -488,9 +650,37 @@ static int pair_cost_bwd_impl(const T* A, const T* Bm, const T* cost, const T* d
 #undef TW_PAIR_SMALL
     return check_launch(what);
   }
-  // (a float64 pass with 64 features would need 66 KB of static LDS)
-  if (D <= (sizeof(T) == 4 ? 64 : 32)) {
-    const int dpt = D <= 4 ? 1 : (D <= 8 ? 2 : (D <= 16 ? 4 : (D <= 32 ? 8 : 16)));
+  if constexpr (sizeof(T) == 4) {
+    // (byte offsets within a pair's plane and operands fit 31 bits)
+    const long long big = (long long)(R > C ? R : C) * D;
+    if (D <= 64 && (long long)R * C < (1LL << 29) && big < (1LL << 29)) {
+      const int nb = (D + 15) / 16;
+      const unsigned ga = (unsigned)((R + 63) / 64) * P, gb = (unsigned)((C + 63) / 64) * P;
+#define TW_PAIR_MFMA(MET_, NB_)                                                                \
+  hipLaunchKernelGGL((pair_bwd_mfma<MET_, false, NB_, DG>), dim3(ga), dim3(256), 0, s, A, Bm,  \
+                     cost, dcost, dA, P, R, C, D);                                             \
+  hipLaunchKernelGGL((pair_bwd_mfma<MET_, true, NB_, DG>), dim3(gb), dim3(256), 0, s, A, Bm,   \
+                     cost, dcost, dB, P, R, C, D);
+#define TW_PAIR_MFMA_D(MET_)                 \
+  switch (nb) {                              \
+    case 1: TW_PAIR_MFMA(MET_, 1) break;     \
+    case 2: TW_PAIR_MFMA(MET_, 2) break;     \
+    case 3: TW_PAIR_MFMA(MET_, 3) break;     \
+    default: TW_PAIR_MFMA(MET_, 4) break;    \
+  }
+      if (metric == MET_RAW) { TW_PAIR_MFMA_D(MET_RAW) }
+      else if constexpr (!DG) {
+        if (metric == MET_SQ) { TW_PAIR_MFMA_D(MET_SQ) }
+        else { TW_PAIR_MFMA_D(MET_EUC) }
+      }
+#undef TW_PAIR_MFMA_D
+#undef TW_PAIR_MFMA
+      return check_launch(what);
+    }
+  }
+  // float64 tiles (a pass with 64 features would need 66 KB of static LDS)
+  if (sizeof(T) == 8 && D <= 32) {
+    const int dpt = D <= 4 ? 1 : (D <= 8 ? 2 : (D <= 16 ? 4 : 8));
     const dim3 ga((R + 63) / 64, P), gb((C + 63) / 64, P), block(256);
 #define TW_PAIR_TILED(MET_, DPT_)                                                               \
   hipLaunchKernelGGL((pair_bwd_tiled<T, MET_, false, DPT_, DG>), ga, block, 0, s, A, Bm, cost,  \
@@ -503,17 +693,14 @@ static int pair_cost_bwd_impl(const T* A, const T* Bm, const T* cost, const T* d
     case 1: TW_PAIR_TILED(MET_, 1) break;          \
     case 2: TW_PAIR_TILED(MET_, 2) break;          \
     case 4: TW_PAIR_TILED(MET_, 4) break;          \
-    case 8: TW_PAIR_TILED(MET_, 8) break;          \
-    default:                                       \
-      if constexpr (sizeof(T) == 4) {             \
-        TW_PAIR_TILED(MET_, 16)                    \
-      }                                            \
-      break;                                       \
+    default: TW_PAIR_TILED(MET_, 8) break;         \
   }
-    if (metric == MET_RAW) { TW_PAIR_TILED_D(MET_RAW) }
-    else if constexpr (!DG) {
-      if (metric == MET_SQ) { TW_PAIR_TILED_D(MET_SQ) }
-      else { TW_PAIR_TILED_D(MET_EUC) }
+    if constexpr (sizeof(T) == 8) {
+      if (metric == MET_RAW) { TW_PAIR_TILED_D(MET_RAW) }
+      else if constexpr (!DG) {
+        if (metric == MET_SQ) { TW_PAIR_TILED_D(MET_SQ) }
+        else { TW_PAIR_TILED_D(MET_EUC) }
+      }
     }
 #undef TW_PAIR_TILED_D
 #undef TW_PAIR_TILED
