@@ -167,7 +167,7 @@ def _hip_call_times(name, inputs, iters):
             o1, o2, ws, wsb), io + carried))
         calls.append(("udtw_bwd", lambda: _hip.call(
             "tw_udtw_feat_bwd", f32, X, Y, vx, vy, R, P, g, g if pen else None, B, N, M, D, gamma,
-            beta, 1e-8, 0.0, 1, 1, dX, dY, dvx, dvy, ws, wsb), 2 * io + carried))
+            beta, 1e-8, 0.0, 1, 1, dX, dY, dvx, dvy, None, ws, wsb), 2 * io + carried))
     elif name == "cfg5a":
         (c,) = inputs
         B = c.shape[0]

@@ -81,7 +81,11 @@ int tw_udtw_cost_bwd_f64(const double* cost, const double* pen, const double* R,
  * tw_udtw_feat_workspace_bytes(...) bytes. Backward: grad_dist / grad_pen
  * with element stride grad_stride (1, or 0: one shared value); writes
  * dX [B,N,D], dY [B,M,D] and, unless both are NULL, dvx [B,N], dvy [B,M]
- * (gradients with respect to vx, vy as given: d sigma when sigma != 0). */
+ * (gradients with respect to vx, vy as given: d sigma when sigma != 0).
+ * fwd_workspace: for D > 1, the forward's workspace as that call left it (it
+ * holds the pairwise squared distances), or NULL to recompute them into
+ * workspace. The backward writes their adjoint into workspace; fwd_workspace
+ * is only read, unless it is workspace itself. */
 size_t tw_udtw_feat_workspace_bytes(int B, int N, int M, int D, int elem_size);
 int tw_udtw_feat_fwd_f32(const float* X, const float* Y, const float* vx, const float* vy, int B,
                          int N, int M, int D, float gamma, float beta, float eps,
@@ -97,13 +101,15 @@ int tw_udtw_feat_bwd_f32(const float* X, const float* Y, const float* vx, const 
                          const float* R, const float* P, const float* grad_dist,
                          const float* grad_pen, int B, int N, int M, int D, float gamma,
                          float beta, float eps, float bandwidth, int sigma, int grad_stride,
-                         float* dX, float* dY, float* dvx, float* dvy, float* workspace,
+                         float* dX, float* dY, float* dvx, float* dvy,
+                         const float* fwd_workspace, float* workspace,
                          size_t workspace_bytes, hipStream_t stream);
 int tw_udtw_feat_bwd_f64(const double* X, const double* Y, const double* vx, const double* vy,
                          const double* R, const double* P, const double* grad_dist,
                          const double* grad_pen, int B, int N, int M, int D, double gamma,
                          double beta, double eps, double bandwidth, int sigma, int grad_stride,
-                         double* dX, double* dY, double* dvx, double* dvy, double* workspace,
+                         double* dX, double* dY, double* dvx, double* dvy,
+                         const double* fwd_workspace, double* workspace,
                          size_t workspace_bytes, hipStream_t stream);
 
 /* -------------------------------------------------------------- JEANIE --

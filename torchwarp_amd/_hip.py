@@ -21,7 +21,7 @@ SIGNATURES = {
     "tw_udtw_cost_fwd": "ppiiiffpppps",
     "tw_udtw_cost_bwd": "ppppppiiiffipps",
     "tw_udtw_feat_fwd": "ppppiiiiffffipppppzs",
-    "tw_udtw_feat_bwd": "ppppppppiiiiffffiipppppzs",
+    "tw_udtw_feat_bwd": "ppppppppiiiiffffiippppppzs",
     "tw_jeanie_cost_fwd": "piiiiiiiifpps",
     "tw_jeanie_cost_bwd": "ppppiiiiiiiifps",
     "tw_jeanie_feat_fwd": "ppiiiiiiiifippps",

@@ -199,7 +199,8 @@ template <typename T>
 static int feat_bwd(const T* X, const T* Y, const T* vx, const T* vy, const T* R, const T* P,
                     const T* gr, const T* gp, int B, int N, int M, int D, double gamma,
                     double beta, double eps, double band, int sigma, int gstride, T* dX, T* dY,
-                    T* dvx, T* dvy, T* ws, size_t ws_bytes, hipStream_t s, const char* what) {
+                    T* dvx, T* dvy, const T* ws_fwd, T* ws, size_t ws_bytes, hipStream_t s,
+                    const char* what) {
   if (int e = check_dims(what, B, N, M, gamma)) return e;
   if (D <= 0) return fail(TW_EINVAL, "%s: D must be > 0", what);
   if (!X || !Y || !vx || !vy || !R || !gr || !dX || !dY)
@@ -233,10 +234,13 @@ static int feat_bwd(const T* X, const T* Y, const T* vx, const T* vy, const T* R
   const size_t need = (size_t)B * N * M * sizeof(T);
   if (!ws || ws_bytes < need)
     return fail(TW_ESIZE, "%s: workspace of %zu bytes needed", what, need);
-  // recompute the raw squared distances, then overwrite them in place with
-  // their adjoint (each cell is read and written by the same thread)
-  if (int e = sqdist_raw<T>(X, Y, B, N, M, D, ws, s, what)) return e;
-  a.C = ws;
+  // the raw squared distances: the forward's, or recomputed into the
+  // workspace; the sweep writes their adjoint into the workspace (in place
+  // when they are there: each cell is read and written by the same thread)
+  if (!ws_fwd) {
+    if (int e = sqdist_raw<T>(X, Y, B, N, M, D, ws, s, what)) return e;
+  }
+  a.C = ws_fwd ? ws_fwd : ws;
   a.dC = ws;
   if (int e = launch_pen<T, SRC_SQ>(pen, true, a, B, s, what)) return e;
   return sqdist_raw_bwd<T>(X, Y, ws, B, N, M, D, dX, dY, s, what);
@@ -275,22 +279,24 @@ int tw_udtw_feat_bwd_f32(const float* X, const float* Y, const float* vx, const 
                          const float* R, const float* P, const float* grad_dist,
                          const float* grad_pen, int B, int N, int M, int D, float gamma,
                          float beta, float eps, float bandwidth, int sigma, int grad_stride,
-                         float* dX, float* dY, float* dvx, float* dvy, float* workspace,
+                         float* dX, float* dY, float* dvx, float* dvy,
+                         const float* fwd_workspace, float* workspace,
                          size_t workspace_bytes, hipStream_t stream) {
   return feat_bwd<float>(X, Y, vx, vy, R, P, grad_dist, grad_pen, B, N, M, D, gamma, beta, eps,
-                         bandwidth, sigma, grad_stride, dX, dY, dvx, dvy, workspace,
-                         workspace_bytes, stream, "tw_udtw_feat_bwd_f32");
+                         bandwidth, sigma, grad_stride, dX, dY, dvx, dvy, fwd_workspace,
+                         workspace, workspace_bytes, stream, "tw_udtw_feat_bwd_f32");
 }
 
 int tw_udtw_feat_bwd_f64(const double* X, const double* Y, const double* vx, const double* vy,
                          const double* R, const double* P, const double* grad_dist,
                          const double* grad_pen, int B, int N, int M, int D, double gamma,
                          double beta, double eps, double bandwidth, int sigma, int grad_stride,
-                         double* dX, double* dY, double* dvx, double* dvy, double* workspace,
+                         double* dX, double* dY, double* dvx, double* dvy,
+                         const double* fwd_workspace, double* workspace,
                          size_t workspace_bytes, hipStream_t stream) {
   return feat_bwd<double>(X, Y, vx, vy, R, P, grad_dist, grad_pen, B, N, M, D, gamma, beta, eps,
-                          bandwidth, sigma, grad_stride, dX, dY, dvx, dvy, workspace,
-                          workspace_bytes, stream, "tw_udtw_feat_bwd_f64");
+                          bandwidth, sigma, grad_stride, dX, dY, dvx, dvy, fwd_workspace,
+                          workspace, workspace_bytes, stream, "tw_udtw_feat_bwd_f64");
 }
 
 }  // extern "C"

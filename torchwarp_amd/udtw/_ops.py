@@ -87,15 +87,24 @@ register_autocast(dp_backward)
 
 
 def _feat_ws(X, N, M):
+    """The squared-distance plane [B, N*M] of D > 1 (empty for D == 1)."""
     n = _hip.udtw_workspace_elems(X.shape[0], N, M, X.shape[2])
-    return X.new_empty(n) if n else None
+    return X.new_empty(X.shape[0], N * M) if n else X.new_empty(0)
+
+
+def _ws_args(ws):
+    return (ws, ws.numel() * ws.element_size()) if ws.numel() else (None, 0)
 
 
 @torch.library.custom_op("twamd_udtw::fused", mutates_args=())
 def fused(X: Tensor, Y: Tensor, vx: Tensor, vy: Tensor, gamma: float, beta: float, eps: float,
-          bandwidth: float, backend: str, sigma: bool) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
+          bandwidth: float, backend: str,
+          sigma: bool) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """vx, vy: variances [B,N] / [B,M], or with ``sigma`` the standard deviations
-    (any shape holding B*N / B*M values), squared inside the kernel."""
+    (any shape holding B*N / B*M values), squared inside the kernel. Returns
+    (distance, penalty, R, P, S): S is the squared-distance plane the kernels
+    built for D > 1 (empty for D == 1), which the backward reads instead of
+    recomputing it."""
     _hip.require(X, backend, "uDTW")
     B, N, D = X.shape
     M = Y.shape[1]
@@ -104,23 +113,23 @@ def fused(X: Tensor, Y: Tensor, vx: Tensor, vy: Tensor, gamma: float, beta: floa
     R = X.new_empty(B, N * M)
     P = X.new_empty(B, N * M) if pen else X.new_empty(0)
     out_r, out_p = X.new_empty(B), X.new_empty(B)
-    ws = _feat_ws(X, N, M)
+    S = _feat_ws(X, N, M)
     _hip.call("tw_udtw_feat_fwd", X.dtype, X, Y, vx, vy, B, N, M, D, gamma, beta, eps, bandwidth,
-              int(sigma), R, P, out_r, out_p, ws,
-              0 if ws is None else ws.numel() * ws.element_size())
-    return out_r, out_p, R, P
+              int(sigma), R, P, out_r, out_p, *_ws_args(S))
+    return out_r, out_p, R, P, S
 
 
 @fused.register_fake
 def _(X, Y, vx, vy, gamma, beta, eps, bandwidth, backend, sigma):
     B, N, M = X.shape[0], X.shape[1], Y.shape[1]
     P = X.new_empty(B, N * M) if beta != 0.0 else X.new_empty(0)
-    return X.new_empty(B), X.new_empty(B), X.new_empty(B, N * M), P
+    S = X.new_empty(B, N * M) if X.shape[2] > 1 else X.new_empty(0)
+    return X.new_empty(B), X.new_empty(B), X.new_empty(B, N * M), P, S
 
 
 @torch.library.custom_op("twamd_udtw::fused_backward", mutates_args=())
 def fused_backward(X: Tensor, Y: Tensor, vx: Tensor, vy: Tensor, R: Tensor, P: Tensor,
-                   grad_r: Tensor, grad_p: Tensor, gamma: float, beta: float, eps: float,
+                   S: Tensor, grad_r: Tensor, grad_p: Tensor, gamma: float, beta: float, eps: float,
                    bandwidth: float, backend: str,
                    sigma: bool) -> Tuple[Tensor, Tensor, Tensor, Tensor]:
     _hip.require(X, backend, "uDTW")
@@ -131,21 +140,23 @@ def fused_backward(X: Tensor, Y: Tensor, vx: Tensor, vy: Tensor, R: Tensor, P: T
     dX, dY = torch.empty_like(X), torch.empty_like(Y)
     dvx, dvy = torch.empty_like(vx), torch.empty_like(vy)
     ws = _feat_ws(X, N, M)
+    S = S if (ws.numel() and S.shape == ws.shape and S.dtype == ws.dtype
+              and S.is_contiguous()) else None
     grads, gs = _hip.per_pair(*(_hip.dense(X.dtype, grad_r, grad_p, contiguous=False) if pen
                                 else _hip.dense(X.dtype, grad_r, contiguous=False)))
     _hip.call("tw_udtw_feat_bwd", X.dtype, X, Y, vx, vy, R, P if pen else None, grads[0],
               grads[1] if pen else None, B, N, M, D, gamma, beta, eps, bandwidth, int(sigma), gs,
-              dX, dY, dvx, dvy, ws, 0 if ws is None else ws.numel() * ws.element_size())
+              dX, dY, dvx, dvy, S, *_ws_args(ws))
     return dX, dY, dvx, dvy
 
 
 @fused_backward.register_fake
-def _(X, Y, vx, vy, R, P, grad_r, grad_p, gamma, beta, eps, bandwidth, backend, sigma):
+def _(X, Y, vx, vy, R, P, S, grad_r, grad_p, gamma, beta, eps, bandwidth, backend, sigma):
     return torch.empty_like(X), torch.empty_like(Y), torch.empty_like(vx), torch.empty_like(vy)
 
 
 register_vmap(fused, 4)
-register_vmap(fused_backward, 8)
+register_vmap(fused_backward, 9)
 register_autocast(fused)
 register_autocast(fused_backward)
 _dp_direct = direct(dp)
@@ -257,7 +268,7 @@ def _variance(v, seq, sigma):
 
 
 class Fused(torch.autograd.Function):
-    """(X, Y, vx, vy) -> (distance, penalty_sum, R, P); R, P internal."""
+    """(X, Y, vx, vy) -> (distance, penalty_sum, R, P, S); R, P, S internal."""
 
     generate_vmap_rule = True
 
@@ -268,9 +279,9 @@ class Fused(torch.autograd.Function):
     @staticmethod
     def setup_context(ctx, inputs, output):
         X, Y, vx, vy, gamma, beta, eps, bandwidth, backend, sigma = inputs
-        ctx.mark_non_differentiable(output[2], output[3])
+        ctx.mark_non_differentiable(output[2], output[3], output[4])
         ctx.set_materialize_grads(False)
-        ctx.save_for_backward(X, Y, vx, vy, output[2], output[3])
+        ctx.save_for_backward(X, Y, vx, vy, output[2], output[3], output[4])
         ctx.save_for_forward(X, Y, vx, vy)
         ctx.args = (gamma, beta, eps, bandwidth, backend, sigma)
 
@@ -282,14 +293,14 @@ class Fused(torch.autograd.Function):
                                                           eps, bandwidth)
 
     @staticmethod
-    def backward(ctx, g_r, g_p, _g_R, _g_P):
-        X, Y, vx, vy, R, P = ctx.saved_tensors
+    def backward(ctx, g_r, g_p, _g_R, _g_P, _g_S):
+        X, Y, vx, vy, R, P, S = ctx.saved_tensors
         gamma, beta, eps, bandwidth, backend, sigma = ctx.args
         B = X.shape[0]
         g_r = X.new_zeros(B) if g_r is None else g_r
         g_p = X.new_zeros(B) if g_p is None else g_p
-        grads = fused_backward_apply(X, Y, vx, vy, R, P, g_r, g_p, gamma, beta, eps, bandwidth,
-                                     backend, sigma)
+        grads = fused_backward_apply(X, Y, vx, vy, R, P, S, g_r, g_p, gamma, beta, eps,
+                                     bandwidth, backend, sigma)
         return (*grads, None, None, None, None, None, None)
 
     @staticmethod
@@ -297,7 +308,7 @@ class Fused(torch.autograd.Function):
         primals = ctx.saved_tensors
         tangents = tuple(zeros_if_none(t, p) for t, p in zip((t_X, t_Y, t_vx, t_vy), primals))
         t_r, t_p = jvp_of(Fused._f(ctx), primals, tangents)
-        return t_r, t_p, None, None
+        return t_r, t_p, None, None, None
 
 
 class FusedBackward(torch.autograd.Function):
@@ -306,13 +317,13 @@ class FusedBackward(torch.autograd.Function):
     generate_vmap_rule = True
 
     @staticmethod
-    def forward(X, Y, vx, vy, R, P, g_r, g_p, gamma, beta, eps, bandwidth, backend, sigma):
-        return _fused_backward_direct(X, Y, vx, vy, R, P, g_r, g_p, gamma, beta, eps, bandwidth,
-                                      backend, sigma)
+    def forward(X, Y, vx, vy, R, P, S, g_r, g_p, gamma, beta, eps, bandwidth, backend, sigma):
+        return _fused_backward_direct(X, Y, vx, vy, R, P, S, g_r, g_p, gamma, beta, eps,
+                                      bandwidth, backend, sigma)
 
     @staticmethod
     def setup_context(ctx, inputs, output):
-        X, Y, vx, vy, R, P, g_r, g_p, gamma, beta, eps, bandwidth, backend, sigma = inputs
+        X, Y, vx, vy, R, P, S, g_r, g_p, gamma, beta, eps, bandwidth, backend, sigma = inputs
         ctx.save_for_backward(X, Y, vx, vy, g_r, g_p)
         ctx.save_for_forward(X, Y, vx, vy, g_r, g_p)
         ctx.args = (gamma, beta, eps, bandwidth, sigma)
@@ -330,11 +341,11 @@ class FusedBackward(torch.autograd.Function):
         X, Y, vx, vy, g_r, g_p = ctx.saved_tensors
         cot = tuple(zeros_if_none(g, p) for g, p in zip((gg_X, gg_Y, gg_vx, gg_vy), (X, Y, vx, vy)))
         d = vjp_of(FusedBackward._first(ctx), (X, Y, vx, vy, g_r, g_p), cot)
-        return (d[0], d[1], d[2], d[3], None, None, d[4], d[5],
+        return (d[0], d[1], d[2], d[3], None, None, None, d[4], d[5],
                 None, None, None, None, None, None)
 
     @staticmethod
-    def jvp(ctx, t_X, t_Y, t_vx, t_vy, _t_R, _t_P, t_gr, t_gp, *_):
+    def jvp(ctx, t_X, t_Y, t_vx, t_vy, _t_R, _t_P, _t_S, t_gr, t_gp, *_):
         primals = ctx.saved_tensors
         tangents = tuple(zeros_if_none(t, p) for t, p in
                          zip((t_X, t_Y, t_vx, t_vy, t_gr, t_gp), primals))

@@ -147,7 +147,7 @@ def _udtw_fused(X, Y, sigma_x, sigma_y, beta, gamma, bandwidth, eps, backend):
     if sy is sx:
         sy = sx.view_as(sx)
     band = 0.0 if bandwidth is None else float(bandwidth)
-    distance, pen, _, _ = _ops.fused_apply(X, Y, sx, sy, float(gamma), float(beta), float(eps),
+    distance, pen, _, _, _ = _ops.fused_apply(X, Y, sx, sy, float(gamma), float(beta), float(eps),
                                            band, backend, True)
     _check_band_reached(distance, band)
     return UDTWOutput(distance, pen)
