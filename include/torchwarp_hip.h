@@ -190,6 +190,20 @@ int tw_pair_cost_bwd_f64(const double* A, const double* Bm, const double* cost,
                          const double* d_cost, int P, int R, int C, int D, int metric,
                          double* dA, double* dB, hipStream_t stream);
 
+/* RBF-style cost: A [P, R, D] against Bm [P, C, D] ->
+ * cost[p, r, c] = sum_d 2 - 2 exp(-sigma (A[p,r,d] - Bm[p,c,d])^2), sigma > 0.
+ * Replaces rbf_cost (jeanie/distances.py:41-51) and its autograd backward
+ * without forming the [.., T, U, D] difference tensor. Backward:
+ * d_cost [P, R, C] -> dA [P, R, D], dB [P, C, D]. */
+int tw_rbf_cost_fwd_f32(const float* A, const float* Bm, int P, int R, int C, int D, float sigma,
+                        float* cost, hipStream_t stream);
+int tw_rbf_cost_fwd_f64(const double* A, const double* Bm, int P, int R, int C, int D,
+                        double sigma, double* cost, hipStream_t stream);
+int tw_rbf_cost_bwd_f32(const float* A, const float* Bm, const float* d_cost, int P, int R, int C,
+                        int D, float sigma, float* dA, float* dB, hipStream_t stream);
+int tw_rbf_cost_bwd_f64(const double* A, const double* Bm, const double* d_cost, int P, int R,
+                        int C, int D, double sigma, double* dA, double* dB, hipStream_t stream);
+
 /* --------------------------------------------------------- hard paths --
  * Optimal (gamma = 0) alignment path with bit-exact indices. Replaces the
  * numpy DP + backtrack of paths.py:85-127 (_optimal_3d / optimal_path).

@@ -25,7 +25,7 @@ def _declared():
 def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(_hip.LIB_PATH))
     names = _declared()
-    assert len(names) == 28
+    assert len(names) == 32
     for name in names:
         assert hasattr(lib, name), name
     assert lib.tw_version() == 1

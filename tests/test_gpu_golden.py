@@ -162,7 +162,7 @@ def test_large(name, shape, shift):
     close(g, ref["grad"])
 
 
-@pytest.mark.parametrize("name", ["euclidean_cost", "squared_euclidean_cost"])
+@pytest.mark.parametrize("name", G.DISTANCES)
 def test_distances(name):
     ref = golden("jeanie.distance", name=name)
     q = ref["q"].to(DEV).requires_grad_()

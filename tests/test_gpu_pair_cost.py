@@ -77,3 +77,35 @@ def test_pair_cost_matches_float64(shape, metric, dtype):
     assert _maxnorm(got, want) < tol
     assert _maxnorm(a.grad, da) < tol
     assert _maxnorm(b.grad, db) < tol
+
+
+RBF_SHAPES = [  # (query shape, support shape, sigma)
+    ((3, 5, 8), (3, 6, 8), 0.5),          # two sequences
+    ((2, 4, 7, 16), (2, 9, 16), 0.3),     # JEANIE layout: support broadcast over K
+    ((2, 9, 8, 256), (2, 8, 256), 0.5),   # cfg4-like features
+    ((1, 33, 3), (1, 70, 3), 2.0),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("shapes", RBF_SHAPES, ids=lambda s: "x".join(map(str, s[0])))
+def test_rbf_cost_matches_oracle(shapes, dtype):
+    """HIP RBF cost (jeanie/distances.py:41-51) against the float64 oracle, which
+    forms the reference's difference tensor; values and both gradients."""
+    from oracle import jeanie as OJ
+    qs, ss, sigma = shapes
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn(*qs, generator=g, dtype=torch.float64) * 0.7
+    s = torch.randn(*ss, generator=g, dtype=torch.float64) * 0.7
+    w = torch.rand(*OJ.rbf_cost(q, s, sigma).shape, generator=g, dtype=torch.float64)
+    a, b = q.to("cuda", dtype).requires_grad_(True), s.to("cuda", dtype).requires_grad_(True)
+    out = tw.rbf_cost(a, b, sigma=sigma)
+    (out * w.to("cuda", dtype)).sum().backward()
+    rq, rs = q.clone().requires_grad_(True), s.clone().requires_grad_(True)
+    ref = OJ.rbf_cost(rq, rs, sigma)
+    (ref * w).sum().backward()
+    tol = 1e-10 if dtype == torch.float64 else 1e-5
+    assert out.dtype == dtype and out.shape == ref.shape
+    assert _maxnorm(out, ref) < tol
+    assert _maxnorm(a.grad, rq.grad) < tol
+    assert _maxnorm(b.grad, rs.grad) < tol

@@ -76,3 +76,31 @@ def test_udtw_cost_layouts(NM, dtype):
     else:
         assert max(errs[:2]) < 1e-5, errs
         assert max(errs[2:]) < 2e-3, errs
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_feat_bwd_with_and_without_forward_plane(dtype):
+    """tw_udtw_feat_bwd reads the forward's squared distances when given its
+    workspace and recomputes them when given NULL: both give the same bits."""
+    from torchwarp_amd import _hip
+    B, N, M, D = 3, 70, 90, 5
+    g = torch.Generator().manual_seed(8)
+    X, Y = (torch.randn(B, L, D, generator=g, dtype=dtype).cuda() for L in (N, M))
+    vx, vy = (0.5 + torch.rand(B, L, generator=g, dtype=dtype).cuda() for L in (N, M))
+    R, P = X.new_empty(B, N * M), X.new_empty(B, N * M)
+    o1, o2 = X.new_empty(B), X.new_empty(B)
+    nws = _hip.udtw_workspace_elems(B, N, M, D)
+    wsb = nws * X.element_size()
+    S = X.new_empty(nws)
+    _hip.call("tw_udtw_feat_fwd", dtype, X, Y, vx, vy, B, N, M, D, 0.7, 1.0, 1e-8, 0.0, 1,
+              R, P, o1, o2, S, wsb)
+    gr = torch.rand(B, generator=g, dtype=dtype).cuda()
+    outs = []
+    for fwd_ws in (S, None):
+        grads = [torch.empty_like(t) for t in (X, Y, vx, vy)]
+        _hip.call("tw_udtw_feat_bwd", dtype, X, Y, vx, vy, R, P, gr, gr, B, N, M, D, 0.7, 1.0,
+                  1e-8, 0.0, 1, 1, *grads, fwd_ws, X.new_empty(nws), wsb)
+        outs.append(grads)
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)

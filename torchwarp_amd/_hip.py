@@ -30,6 +30,8 @@ SIGNATURES = {
     "tw_fvm_cost_bwd": "ppppiiiifpps",
     "tw_pair_cost_fwd": "ppiiiiips",
     "tw_pair_cost_bwd": "ppppiiiiipps",
+    "tw_rbf_cost_fwd": "ppiiiifps",
+    "tw_rbf_cost_bwd": "pppiiiifpps",
 }
 
 # entry points that exist in float64 only

@@ -56,6 +56,12 @@ def pair_cost(A, Bm, metric):
     return torch.where(pos, torch.where(pos, sq, 1.0).sqrt(), 0.0)
 
 
+def rbf_cost(A, Bm, sigma):
+    """A [P,R,D], Bm [P,C,D] -> [P,R,C]: sum_d 2 - 2 exp(-sigma (a - b)^2)."""
+    diff = A.unsqueeze(-2) - Bm.unsqueeze(-3)
+    return (2.0 - 2.0 * torch.exp(-sigma * diff.pow(2))).sum(-1)
+
+
 def cost_from_features(query, support, metric):
     B, K1, K2, T, D = query.shape
     cost = pair_cost(query.reshape(B, K1 * K2 * T, D), support, metric)

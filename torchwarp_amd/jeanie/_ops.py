@@ -147,6 +147,113 @@ pair_apply = pick(Pair, without_jvp(Pair), Pair.forward)
 pair_backward_apply = pick(PairBackward, without_jvp(PairBackward), PairBackward.forward)
 
 
+# -------------------------------------------------------------- RBF cost
+
+@torch.library.custom_op("twamd_cost::rbf", mutates_args=())
+def rbf(A: Tensor, Bm: Tensor, sigma: float, backend: str) -> Tensor:
+    _hip.require(A, backend, "rbf cost")
+    P, R, D = A.shape
+    C = Bm.shape[1]
+    A, Bm = A.contiguous(), Bm.to(A.dtype).contiguous()
+    out = A.new_empty(P, R, C)
+    _hip.call("tw_rbf_cost_fwd", A.dtype, A, Bm, P, R, C, D, sigma, out)
+    return out
+
+
+@rbf.register_fake
+def _(A, Bm, sigma, backend):
+    return A.new_empty(A.shape[0], A.shape[1], Bm.shape[1])
+
+
+@torch.library.custom_op("twamd_cost::rbf_backward", mutates_args=())
+def rbf_backward(A: Tensor, Bm: Tensor, d_cost: Tensor, sigma: float,
+                 backend: str) -> Tuple[Tensor, Tensor]:
+    _hip.require(A, backend, "rbf cost")
+    P, R, D = A.shape
+    C = Bm.shape[1]
+    A, Bm = A.contiguous(), Bm.to(A.dtype).contiguous()
+    dA, dB = torch.empty_like(A), torch.empty_like(Bm)
+    _hip.call("tw_rbf_cost_bwd", A.dtype, A, Bm, d_cost.to(A.dtype).contiguous(), P, R, C, D,
+              sigma, dA, dB)
+    return dA, dB
+
+
+@rbf_backward.register_fake
+def _(A, Bm, d_cost, sigma, backend):
+    return torch.empty_like(A), torch.empty_like(Bm)
+
+
+register_vmap(rbf, 2)
+register_vmap(rbf_backward, 3)
+register_autocast(rbf)
+register_autocast(rbf_backward)
+
+
+class Rbf(torch.autograd.Function):
+    generate_vmap_rule = True
+
+    @staticmethod
+    def forward(A, Bm, sigma, backend):
+        return _rbf_direct(A, Bm, sigma, backend)
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        A, Bm, sigma, backend = inputs
+        ctx.save_for_backward(A, Bm)
+        ctx.save_for_forward(A, Bm)
+        ctx.args = (sigma, backend)
+
+    @staticmethod
+    def backward(ctx, g):
+        A, Bm = ctx.saved_tensors
+        sigma, backend = ctx.args
+        dA, dB = rbf_backward_apply(A, Bm, g, sigma, backend)
+        return dA, dB, None, None
+
+    @staticmethod
+    def jvp(ctx, tA, tB, *_):
+        A, Bm = ctx.saved_tensors
+        sigma, _ = ctx.args
+        return jvp_of(lambda a, b: _autograd.rbf_cost(a, b, sigma), (A, Bm),
+                      (zeros_if_none(tA, A), zeros_if_none(tB, Bm)))
+
+
+class RbfBackward(torch.autograd.Function):
+    generate_vmap_rule = True
+
+    @staticmethod
+    def forward(A, Bm, g, sigma, backend):
+        return _rbf_backward_direct(A, Bm, g, sigma, backend)
+
+    @staticmethod
+    def setup_context(ctx, inputs, output):
+        A, Bm, g, sigma, backend = inputs
+        ctx.save_for_backward(A, Bm, g)
+        ctx.save_for_forward(A, Bm, g)
+        ctx.sigma = sigma
+
+    @staticmethod
+    def _first(sigma):
+        return lambda a, b, g: vjp_of(lambda x, y: _autograd.rbf_cost(x, y, sigma), (a, b), (g,))
+
+    @staticmethod
+    def backward(ctx, gg_A, gg_B):
+        A, Bm, g = ctx.saved_tensors
+        d = vjp_of(RbfBackward._first(ctx.sigma), (A, Bm, g),
+                   (zeros_if_none(gg_A, A), zeros_if_none(gg_B, Bm)))
+        return d[0], d[1], d[2], None, None
+
+    @staticmethod
+    def jvp(ctx, tA, tB, tg, *_):
+        A, Bm, g = ctx.saved_tensors
+        tangents = tuple(zeros_if_none(t, p) for t, p in zip((tA, tB, tg), (A, Bm, g)))
+        return tuple(jvp_of(RbfBackward._first(ctx.sigma), (A, Bm, g), tangents))
+
+
+rbf_apply = pick(Rbf, without_jvp(Rbf), Rbf.forward)
+rbf_backward_apply = pick(RbfBackward, without_jvp(RbfBackward), RbfBackward.forward)
+
+
 # ----------------------------------------------------------- JEANIE, cost
 
 @torch.library.custom_op("twamd_jeanie::dp", mutates_args=())
@@ -459,6 +566,8 @@ register_autocast(fvm)
 register_autocast(fvm_backward)
 _pair_direct = direct(pair)
 _pair_backward_direct = direct(pair_backward)
+_rbf_direct = direct(rbf)
+_rbf_backward_direct = direct(rbf_backward)
 _dp_direct = direct(dp)
 _dp_backward_direct = direct(dp_backward)
 _features_direct = direct(features)

@@ -5,9 +5,9 @@ Two layouts, as in the reference:
   two sequences: x [..., N, D], y [..., M, D] (same rank) -> [..., N, M]
 
 The (squared) Euclidean costs run on the HIP pair-cost kernel (matrix cores
-for float32): batch dimensions where the support broadcasts over the query
-are folded into the rows of one pairwise block, so the support is never
-expanded in memory.
+for float32), the RBF cost on its own HIP kernel: batch dimensions where the
+support broadcasts over the query are folded into the rows of one pairwise
+block, so the support is never expanded in memory.
 """
 
 import math
@@ -27,7 +27,7 @@ def _check(query, support):
     return support.unsqueeze(-3) if query.ndim > support.ndim else support
 
 
-def _pair_cost(query, support, metric):
+def _pair_cost(query, support, metric=None, sigma=None):
     s = _check(query, support)
     dtype = torch.promote_types(query.dtype, s.dtype)
     if dtype not in (torch.float32, torch.float64):
@@ -43,7 +43,10 @@ def _pair_cost(query, support, metric):
     P, F = math.prod(lead), math.prod(fold)
     A = q.expand(*batch, T, D).reshape(P, F * T, D)
     Bm = s.expand(*lead, *sb[f:], U, D).reshape(P, U, D)
-    cost = _ops.pair_apply(A, Bm, metric, "auto")
+    if sigma is None:
+        cost = _ops.pair_apply(A, Bm, metric, "auto")
+    else:
+        cost = _ops.rbf_apply(A, Bm, float(sigma), "auto")
     return cost.reshape(*batch, T, U)
 
 
@@ -60,12 +63,10 @@ def euclidean_cost(query: torch.Tensor, support: torch.Tensor) -> torch.Tensor:
 def rbf_cost(query: torch.Tensor, support: torch.Tensor, sigma: float = 0.5) -> torch.Tensor:
     """RBF-style base cost d(x,y) = sum_d [2 - 2 exp(-sigma (x_d - y_d)^2)].
 
-    This per-dimension form is not a matrix product; it materialises the
-    [..., K, T, U, D] difference tensor with elementwise ops on the inputs'
-    device, as the reference does.
+    This per-dimension form is not a matrix product. The HIP kernel sums the
+    terms per output cell; the reference's [..., K, T, U, D] difference
+    tensor is never formed.
     """
     if sigma <= 0:
         raise ValueError("sigma must be > 0")
-    s = _check(query, support)
-    diff = query.unsqueeze(-2) - s.unsqueeze(-3)
-    return (2.0 - 2.0 * torch.exp(-sigma * diff.pow(2))).sum(dim=-1)
+    return _pair_cost(query, support, sigma=sigma)

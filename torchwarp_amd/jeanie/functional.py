@@ -53,7 +53,7 @@ def _jeanie_dp_features(query, support, gamma=0.1, max_shift_1=1, max_shift_2=1,
 
     query [B, K1, K2, T, D], support [B, U, D]; metric "euclidean",
     "sqeuclidean" or "rbf". The Euclidean metrics build the cost on the HIP
-    pair-cost kernel; "rbf" materialises its cost with ``rbf_cost``.
+    pair-cost kernel, "rbf" on the HIP RBF kernel (``rbf_cost``).
     """
     if query.ndim != 5 or support.ndim != 3:
         raise ValueError("query must be [B,K1,K2,T,D] and support [B,U,D]")
