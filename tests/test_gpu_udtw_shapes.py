@@ -104,3 +104,51 @@ def test_feat_bwd_with_and_without_forward_plane(dtype):
     torch.cuda.synchronize()
     for a, b in zip(*outs):
         assert torch.equal(a, b)
+
+
+BANDS = [  # (B, N, M, D, bandwidth): blocks of whole wavefronts outside the band are skipped
+    (2, 300, 310, 1, 25.0),     # rows travel by DPP (N > 256)
+    (1, 600, 640, 8, 40.0),     # D > 1: diagonal-major S / dS
+    (2, 200, 220, 3, 21.5),     # columns in LDS (N <= 256)
+    (1, 1100, 1030, 1, 90.0),   # several rows per thread
+]
+
+
+@pytest.mark.parametrize("shape", BANDS, ids=lambda s: "B{}N{}M{}D{}w{}".format(*s))
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_udtw_band_layouts(shape, dtype):
+    """Sakoe-Chiba band |i - j| <= bandwidth (udtw_cuda.cu:126-130) on long
+    sequences, where most wavefront blocks lie outside the band."""
+    B, N, M, D, band = shape
+    g = torch.Generator().manual_seed(10)
+    X = torch.randn(B, N, D, generator=g, dtype=torch.float64) / D ** 0.5
+    Y = torch.randn(B, M, D, generator=g, dtype=torch.float64) / D ** 0.5
+    sx = 0.5 + torch.rand(B, N, 1, generator=g, dtype=torch.float64)
+    sy = 0.5 + torch.rand(B, M, 1, generator=g, dtype=torch.float64)
+    xs = [t.to("cuda", dtype).requires_grad_(True) for t in (X, Y, sx, sy)]
+    d, p = tw.UDTW(gamma=0.5, beta=1.0, bandwidth=band)(*xs)
+    (d + p).sum().backward()
+    ref = [t.clone().requires_grad_(True) for t in (X, Y, sx, sy)]
+    rd, rp = OU.udtw(*ref, gamma=0.5, beta=1.0, bandwidth=band)
+    (rd + rp).sum().backward()
+    errs = [_maxnorm(a, b) for a, b in zip([d, p] + [t.grad for t in xs],
+                                           [rd, rp] + [t.grad for t in ref])]
+    if dtype == torch.float64:
+        assert max(errs) < 1e-9, errs
+    else:
+        assert max(errs[:2]) < 1e-5, errs
+        assert max(errs[2:]) < 2e-3, errs
+
+
+def test_udtw_cost_band_long():
+    g = torch.Generator().manual_seed(11)
+    C = torch.rand(2, 700, 650, generator=g, dtype=torch.float64)
+    Q = 0.2 * torch.rand(2, 700, 650, generator=g, dtype=torch.float64)
+    c, q = C.cuda().requires_grad_(True), Q.cuda().requires_grad_(True)
+    d, p = TF.udtw_from_cost(c, q, gamma=0.5, bandwidth=60)
+    (d + 3 * p).sum().backward()
+    rc, rq = C.clone().requires_grad_(True), Q.clone().requires_grad_(True)
+    rd, rp = OU.udtw_from_cost(rc, rq, gamma=0.5, bandwidth=60)
+    (rd + 3 * rp).sum().backward()
+    errs = [_maxnorm(a, b) for a, b in zip([d, p, c.grad, q.grad], [rd, rp, rc.grad, rq.grad])]
+    assert max(errs) < 1e-9, errs

@@ -318,6 +318,14 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
       }
       Rec4<T>* const out = my_out + half * kSlots;
       const ColRec<T>* const cblk = crow + (d_first + tw + t0);
+      // band: every row of this wavefront is outside |2i - d| <= band on all
+      // of the block's diagonals, so its cells are INF / 0 without arithmetic
+      bool skip = false;
+      if (BAND) {
+        const int dlo = d_first + tw + t0, wlo = wave * 64 * ROWS;
+        skip = (T)(2 * wlo - (dlo + kSlots - 1)) > a.band ||
+               (T)(dlo - 2 * (wlo + 64 * ROWS - 1)) > a.band;
+      }
 #pragma unroll
       for (int u = 0; u < kSlots; ++u) {
         const int d = d_first + tw + t0 + u;
@@ -365,6 +373,10 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
         for (int k = 0; k < ROWS; ++k) {
           const int j = d + jb[k];
           const bool valid = (unsigned)j < (unsigned)M;
+          if (BAND && skip) {
+            nr[k] = INF;
+            np[k] = (T)0;
+          } else {
           const T up = k ? r1[k - 1] : nr1;
           const T dg = k ? r2[k - 1] : nr2;
           const T lf = r1[k];
@@ -398,6 +410,7 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
             np[k] = ok ? pv : (T)0;
           } else {
             np[k] = (T)0;
+          }
           }
           const int vo = valid ? vst[k] : kOob;
           bR.st(nr[k], vo, so);
@@ -648,6 +661,14 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
       const int dlo = d_first - tw - t0 - kSlots;
       const ColRec<T>* const cblk = crow + dlo;
       ColRec<T>* const ablk = arow + dlo;
+      // band: every row of this wavefront is outside |2i - d| <= band on all
+      // of the block's diagonals (the forward left those cells at INF)
+      bool skip = false;
+      if (BAND) {
+        const int bhi = d_first - tw - t0, blo = bhi - (kSlots - 1);
+        const int wlo = wave * 64 * ROWS - ((int)blockDim.x * ROWS - N);
+        skip = (T)(2 * wlo - bhi) > a.band || (T)(blo - 2 * (wlo + 64 * ROWS - 1)) > a.band;
+      }
 #pragma unroll
       for (int u = 0; u < kSlots; ++u) {
         const int d = d_first - tw - t0 - u;
@@ -714,6 +735,14 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
   #pragma unroll
         for (int k = 0; k < ROWS; ++k) {
           const bool valid = (unsigned)(d + jb[k]) < (unsigned)M;
+          // the cell's adjoints (g, h), dS and the variance / feature terms;
+          // all zero for a skipped (out-of-band) block, as for any cell the
+          // forward left at INF
+          T g = (T)0, h = (T)0, dsq = (T)0, df = (T)0, dvar = (T)0;
+          if (BAND && skip) {
+            xe[k] = -INF;
+            xa[k] = (T)0;
+          } else {
           const T rk = valid ? cr[k] : INF;
           const T pk = cp[k];
           T ch, q = (T)0, c = (T)0, rv = (T)1, sq_raw = (T)0, var_raw = (T)1;
@@ -722,8 +751,8 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
             if (PEN) q = cq[k];
           } else {
             if (SRC == SRC_FEAT1) {
-              const T df = xr[k] - yc[k];
-              sq_raw = df * df;
+              const T df0 = xr[k] - yc[k];
+              sq_raw = df0 * df0;
             } else {
               sq_raw = cc[k];
             }
@@ -741,8 +770,7 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
           const T edg = (k + 1 < ROWS) ? e2[k + 1] : ne2;
           const T gdg = (k + 1 < ROWS) ? g2[k + 1] : ng2;
           const T wdn = ex2(edn - rk), wrt = ex2(e1[k] - rk), wdg = ex2(edg - rk);
-          T g = wdn * gdn + wrt * g1[k] + wdg * gdg;
-          T h = (T)0;
+          g = wdn * gdn + wrt * g1[k] + wdg * gdg;
           if (PEN) {
             const T hdn = (k + 1 < ROWS) ? h1[k + 1] : nh1;
             const T adn = (k + 1 < ROWS) ? a1[k + 1] : na1;
@@ -758,25 +786,25 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
           g = live ? g : (T)0;
           h = live ? h : (T)0;
           xe[k] = live ? rk - ch : -INF;
+          xa[k] = valid ? pk - q : (T)0;
+          if (SRC != SRC_COST) {
+            dsq = sq_raw > (T)0 ? g * rv : (T)0;
+            if (SRC == SRC_FEAT1) df = valid ? (T)2 * dsq * (xr[k] - yc[k]) : (T)0;
+            dvar = var_raw > a.eps ? (T)0.5 * (a.beta * h - g * c) * rv : (T)0;
+            dvar = valid ? dvar : (T)0;
+          }
+          }
           xg[k] = g;
           xh[k] = h;
-          xa[k] = valid ? pk - q : (T)0;
 
           const int vn = valid ? vnat[k] : kOob;
           if (SRC == SRC_COST) {
             bdC.st(g, vn, so_n);
             if (PEN) bdQ.st(h, vn, so_n);
           } else {
-            const T dsq = sq_raw > (T)0 ? g * rv : (T)0;
             if (SRC == SRC_SQ)
               bdC.st(dsq, valid ? vst[k] : kOob, __builtin_amdgcn_readlane(so_sd, t0 + u));
-            T df = (T)0;
-            if (SRC == SRC_FEAT1) {
-              df = valid ? (T)2 * dsq * (xr[k] - yc[k]) : (T)0;
-              dxr[k] += df;
-            }
-            T dvar = var_raw > a.eps ? (T)0.5 * (a.beta * h - g * c) * rv : (T)0;
-            dvar = valid ? dvar : (T)0;
+            if (SRC == SRC_FEAT1) dxr[k] += df;
             dvr[k] += dvar;
             if (LC) {
               // this wavefront's sums of column d - row0 (invalid cells add 0)
