@@ -51,9 +51,14 @@ def jvp_of(f, primals, tangents):
 
 
 def vjp_of(f, primals, cotangents):
-    """J^T v of f at primals, itself differentiable."""
-    _, pullback = torch.func.vjp(f, *primals)
-    return pullback(tuple(cotangents))
+    """J^T v of f at primals, itself differentiable. For an f with one tensor
+    output, the one cotangent is passed as that tensor (torch.func matches
+    the cotangents' structure to the outputs')."""
+    out, pullback = torch.func.vjp(f, *primals)
+    cot = tuple(cotangents)
+    if isinstance(out, Tensor) and len(cot) == 1:
+        return pullback(cot[0])
+    return pullback(cot)
 
 
 def without_jvp(cls):
