@@ -244,3 +244,15 @@ def test_jeanie_gradgradcheck():
             lambda q, s: TF.jeanie(q, s, gamma=0.5, max_shift=1, metric=metric), (q2, s))
         assert torch.autograd.gradgradcheck(
             lambda q, s: TF.fvm(q, s, gamma=0.5, metric=metric), (q2, s))
+
+
+@pytest.mark.parametrize("name", ["udtw.softmin", "jeanie.softmin"])
+def test_softmin_helpers(name):
+    """softmin / softmin_weights (sdtw.py) on device tensors, as the reference's
+    tests/test_udtw.py:95-100 and tests/test_jeanie.py:121-124 check them."""
+    ref = golden(name)
+    v, want = ref["v"].to(DEV), ref["outputs"]
+    _close(TF.softmin(v, 0.3, dim=1), want[0])
+    _close(TF.softmin(v, 0.3), want[1])
+    if len(want) > 2:
+        _close(TF.softmin_weights(v, 0.3, dim=1), want[2])

@@ -61,6 +61,20 @@ def vjp_of(f, primals, cotangents):
     return pullback(cot)
 
 
+def per_pair_dot(grads, tangents):
+    """sum_b-wise <grad, tangent>: for outputs with one scalar per pair b,
+    whose gradient with respect to pair b's inputs is the VJP with a unit
+    cotangent, this is the JVP (forward-mode derivative) of that output.
+    Tangents given as None are skipped; None if every one is."""
+    out = None
+    for g, t in zip(grads, tangents):
+        if g is None or t is None:
+            continue
+        v = (g * t).reshape(g.shape[0], -1).sum(1)
+        out = v if out is None else out + v
+    return out
+
+
 def without_jvp(cls):
     """Twin of an autograd.Function without ``jvp`` (dynamo cannot trace one that has it)."""
     ns = {k: v for k, v in vars(cls).items() if k not in ("jvp", "__dict__", "__weakref__")}

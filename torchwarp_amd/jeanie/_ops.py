@@ -28,8 +28,8 @@ import torch
 from torch import Tensor
 
 from .. import _hip
-from .._opsutil import (direct, jvp_of, pick, register_autocast, register_vmap, vjp_of,
-                        without_jvp, zeros_if_none)
+from .._opsutil import (direct, jvp_of, per_pair_dot, pick, register_autocast, register_vmap,
+                        vjp_of, without_jvp, zeros_if_none)
 from . import _autograd
 
 METRIC_CODES = {"sqeuclidean": _hip.METRIC_SQEUC, "euclidean": _hip.METRIC_EUC}
@@ -317,7 +317,7 @@ class DP(torch.autograd.Function):
             ctx.mark_non_differentiable(output[1])
         ctx.set_materialize_grads(False)
         ctx.save_for_backward(cost, output[1])
-        ctx.save_for_forward(cost)
+        ctx.save_for_forward(cost, output[1])
         ctx.args = (s1, s2, gamma, backend, natural_R)
 
     @staticmethod
@@ -330,11 +330,19 @@ class DP(torch.autograd.Function):
 
     @staticmethod
     def jvp(ctx, t_cost, *_):
-        (cost,) = ctx.saved_tensors
-        s1, s2, gamma, _, natural_R = ctx.args
-        t_out, t_R = jvp_of(lambda c: _autograd.jeanie(c, s1, s2, gamma), (cost,),
-                            (zeros_if_none(t_cost, cost),))
-        return t_out, (t_R if natural_R else None)
+        cost, R = ctx.saved_tensors
+        s1, s2, gamma, backend, natural_R = ctx.args
+        if natural_R:
+            # the accumulator is an output too: forward mode through the
+            # autograd-native recursion
+            return jvp_of(lambda c: _autograd.jeanie(c, s1, s2, gamma), (cost,),
+                          (zeros_if_none(t_cost, cost),))
+        # one scalar per pair: the HIP backward's gradient (unit cotangent)
+        # dotted with the tangent
+        one = cost.new_ones(cost.shape[0])
+        t_out = per_pair_dot((dp_backward_apply(cost, R, one, None, s1, s2, gamma, backend),),
+                             (t_cost,))
+        return (torch.zeros_like(one) if t_out is None else t_out), None
 
 
 def _first_order_dp(s1, s2, gamma, with_R):
@@ -462,7 +470,7 @@ class Features(torch.autograd.Function):
             ctx.mark_non_differentiable(R, cost)
         ctx.set_materialize_grads(False)
         ctx.save_for_backward(query, support, cost, R)
-        ctx.save_for_forward(query, support)
+        ctx.save_for_forward(query, support, cost, R)
         ctx.args = (s1, s2, gamma, metric, backend, natural_R)
 
     @staticmethod
@@ -476,12 +484,18 @@ class Features(torch.autograd.Function):
 
     @staticmethod
     def jvp(ctx, t_q, t_s, *_):
-        query, support = ctx.saved_tensors
-        s1, s2, gamma, metric, _, natural_R = ctx.args
-        t_out, t_R = jvp_of(
-            lambda q, s: _autograd.jeanie_features(q, s, s1, s2, gamma, metric),
-            (query, support), (zeros_if_none(t_q, query), zeros_if_none(t_s, support)))
-        return t_out, (t_R if natural_R else None), None
+        query, support, cost, R = ctx.saved_tensors
+        s1, s2, gamma, metric, backend, natural_R = ctx.args
+        if natural_R:
+            t_out, t_R = jvp_of(
+                lambda q, s: _autograd.jeanie_features(q, s, s1, s2, gamma, metric),
+                (query, support), (zeros_if_none(t_q, query), zeros_if_none(t_s, support)))
+            return t_out, t_R, None
+        one = query.new_ones(query.shape[0])
+        grads = features_backward_apply(query, support, cost, R, one, None, s1, s2, gamma,
+                                        metric, backend)
+        t_out = per_pair_dot(grads, (t_q, t_s))
+        return (torch.zeros_like(one) if t_out is None else t_out), None, None
 
 
 class FeaturesBackward(torch.autograd.Function):
@@ -589,7 +603,7 @@ class FVM(torch.autograd.Function):
         ctx.mark_non_differentiable(output[1], output[2])
         ctx.set_materialize_grads(False)
         ctx.save_for_backward(cost, output[1], output[2])
-        ctx.save_for_forward(cost)
+        ctx.save_for_forward(cost, output[1], output[2])
         ctx.args = (gamma, backend)
 
     @staticmethod
@@ -602,10 +616,13 @@ class FVM(torch.autograd.Function):
 
     @staticmethod
     def jvp(ctx, t_cost, *_):
-        (cost,) = ctx.saved_tensors
-        gamma, _ = ctx.args
-        return (jvp_of(lambda c: _autograd.fvm(c, gamma), (cost,), (zeros_if_none(t_cost, cost),)),
-                None, None)
+        # one scalar per pair: the HIP backward's gradient dotted with the tangent
+        cost, temporal, R = ctx.saved_tensors
+        gamma, backend = ctx.args
+        one = cost.new_ones(cost.shape[0])
+        t_out = per_pair_dot((fvm_backward_apply(cost, temporal, R, one, gamma, backend),),
+                             (t_cost,))
+        return (torch.zeros_like(one) if t_out is None else t_out), None, None
 
 
 class FVMBackward(torch.autograd.Function):

@@ -25,8 +25,8 @@ import torch
 from torch import Tensor
 
 from .. import _hip
-from .._opsutil import (direct, jvp_of, pick, register_autocast, register_vmap, vjp_of,
-                        without_jvp, zeros_if_none)
+from .._opsutil import (direct, jvp_of, per_pair_dot, pick, register_autocast, register_vmap,
+                        vjp_of, without_jvp, zeros_if_none)
 from . import _autograd
 
 # ---------------------------------------------------- DP on given matrices
@@ -194,7 +194,7 @@ class DP(torch.autograd.Function):
         ctx.mark_non_differentiable(output[2], output[3])
         ctx.set_materialize_grads(False)
         ctx.save_for_backward(cost, penalty, output[2], output[3])
-        ctx.save_for_forward(cost, penalty)
+        ctx.save_for_forward(cost, penalty, output[2], output[3])
         ctx.args = (gamma, bandwidth, backend)
 
     @staticmethod
@@ -209,13 +209,20 @@ class DP(torch.autograd.Function):
 
     @staticmethod
     def jvp(ctx, t_cost, t_pen, *_):
-        cost, penalty = ctx.saved_tensors
-        gamma, bandwidth, _ = ctx.args
-        pen = _dense_pen(penalty, cost)
-        t_pen = zeros_if_none(t_pen, pen) if penalty.numel() else torch.zeros_like(cost)
-        t_r, t_p = jvp_of(lambda c, q: _autograd.udtw(c, q, gamma, bandwidth), (cost, pen),
-                          (zeros_if_none(t_cost, cost), t_pen))
-        return t_r, t_p, None, None
+        # distance and penalty are one scalar per pair: their tangents are the
+        # HIP backward's gradients (unit cotangent) dotted with the tangents
+        cost, penalty, R, P = ctx.saved_tensors
+        gamma, bandwidth, backend = ctx.args
+        B = cost.shape[0]
+        one, zero = cost.new_ones(B), cost.new_zeros(B)
+        ts = (t_cost, t_pen if penalty.numel() else None)
+        t_r = per_pair_dot(dp_backward_apply(cost, penalty, R, P, one, zero, gamma, bandwidth,
+                                             backend), ts)
+        t_p = None
+        if penalty.numel():
+            t_p = per_pair_dot(dp_backward_apply(cost, penalty, R, P, zero, one, gamma,
+                                                 bandwidth, backend), ts)
+        return (zero if t_r is None else t_r), (zero if t_p is None else t_p), None, None
 
 
 class DPBackward(torch.autograd.Function):
@@ -282,15 +289,8 @@ class Fused(torch.autograd.Function):
         ctx.mark_non_differentiable(output[2], output[3], output[4])
         ctx.set_materialize_grads(False)
         ctx.save_for_backward(X, Y, vx, vy, output[2], output[3], output[4])
-        ctx.save_for_forward(X, Y, vx, vy)
+        ctx.save_for_forward(X, Y, vx, vy, output[2], output[3], output[4])
         ctx.args = (gamma, beta, eps, bandwidth, backend, sigma)
-
-    @staticmethod
-    def _f(ctx):
-        gamma, beta, eps, bandwidth, _, sigma = ctx.args
-        return lambda x, y, a, b: _autograd.udtw_features(x, y, _variance(a, x, sigma),
-                                                          _variance(b, y, sigma), gamma, beta,
-                                                          eps, bandwidth)
 
     @staticmethod
     def backward(ctx, g_r, g_p, _g_R, _g_P, _g_S):
@@ -305,10 +305,19 @@ class Fused(torch.autograd.Function):
 
     @staticmethod
     def jvp(ctx, t_X, t_Y, t_vx, t_vy, *_):
-        primals = ctx.saved_tensors
-        tangents = tuple(zeros_if_none(t, p) for t, p in zip((t_X, t_Y, t_vx, t_vy), primals))
-        t_r, t_p = jvp_of(Fused._f(ctx), primals, tangents)
-        return t_r, t_p, None, None, None
+        # one scalar per pair: gradients of the HIP backward (unit cotangent)
+        # dotted with the tangents
+        X, Y, vx, vy, R, P, S = ctx.saved_tensors
+        gamma, beta, eps, bandwidth, backend, sigma = ctx.args
+        B = X.shape[0]
+        one, zero = X.new_ones(B), X.new_zeros(B)
+        ts = (t_X, t_Y, t_vx, t_vy)
+        args = (gamma, beta, eps, bandwidth, backend, sigma)
+        t_r = per_pair_dot(fused_backward_apply(X, Y, vx, vy, R, P, S, one, zero, *args), ts)
+        t_p = None
+        if beta != 0.0:
+            t_p = per_pair_dot(fused_backward_apply(X, Y, vx, vy, R, P, S, zero, one, *args), ts)
+        return (zero if t_r is None else t_r), (zero if t_p is None else t_p), None, None, None
 
 
 class FusedBackward(torch.autograd.Function):
