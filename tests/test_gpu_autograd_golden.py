@@ -256,3 +256,73 @@ def test_softmin_helpers(name):
     _close(TF.softmin(v, 0.3), want[1])
     if len(want) > 2:
         _close(TF.softmin_weights(v, 0.3, dim=1), want[2])
+
+
+# ------------------------------------------------- torch.compile and autocast
+# (reference tests/test_udtw_parity.py:142-172, tests/test_jeanie_parity.py:246-284)
+
+def _udtw_inputs(B=3, N=5, M=7, D=4, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.rand(B, N, D, generator=g, dtype=torch.float64),
+            torch.rand(B, M, D, generator=g, dtype=torch.float64),
+            0.5 + torch.rand(B, N, 1, generator=g, dtype=torch.float64),
+            0.5 + torch.rand(B, M, 1, generator=g, dtype=torch.float64))
+
+
+@pytest.mark.parametrize("method", METHODS)
+def test_udtw_torch_compile_fullgraph(method):
+    torch._dynamo.reset()
+    X, Y, SX, SY = (t.to(DEV).requires_grad_() for t in _udtw_inputs())
+    f = _scalar(tw.UDTW(gamma=0.3, beta=0.8, normalize=True, method=method))
+    compiled = torch.compile(f, fullgraph=True)
+    want = f(X, Y, SX, SY)
+    got = compiled(X, Y, SX, SY)
+    _close(got, want.detach().cpu())
+    for a, b in zip(torch.autograd.grad(got, (X, Y, SX, SY)),
+                    torch.autograd.grad(want, (X, Y, SX, SY))):
+        _close(a, b.detach().cpu())
+
+
+@pytest.mark.parametrize("path", ["cost", "euclidean"])
+def test_jeanie_torch_compile_fullgraph(path):
+    torch._dynamo.reset()
+    q = torch.randn(2, 3, 5, 4, device=DEV, dtype=torch.float64).requires_grad_()
+    s = torch.randn(2, 6, 4, device=DEV, dtype=torch.float64).requires_grad_()
+
+    def f(q, s):
+        if path == "cost":
+            d, R = TF.jeanie_from_cost(tw.euclidean_cost(q, s), gamma=0.3, max_shift=1,
+                                       return_accumulator=True)
+        else:
+            d, R = TF.jeanie(q, s, gamma=0.3, max_shift=1, return_accumulator=True)
+        return d.sum() + 0.1 * (R ** 2).mean()
+
+    compiled = torch.compile(f, fullgraph=True)
+    want, got = f(q, s), compiled(q, s)
+    _close(got, want.detach().cpu())
+    for a, b in zip(torch.autograd.grad(got, (q, s)), torch.autograd.grad(want, (q, s))):
+        _close(a, b.detach().cpu())
+
+
+def test_autocast_runs_in_float32():
+    X, Y, SX, SY = (t.float().to(DEV).requires_grad_() for t in _udtw_inputs(B=2, N=5, M=6))
+    lin = torch.nn.Linear(4, 4).to(DEV)
+    for method in METHODS:
+        m = tw.UDTW(gamma=0.3, method=method)
+        with torch.autocast("cuda", dtype=torch.float16):
+            d, p = m(lin(X), lin(Y), SX, SY)
+        assert d.dtype == torch.float32 and p.dtype == torch.float32
+        (d.sum() + p.sum()).backward()
+        assert torch.isfinite(X.grad).all()
+        ref_d, _ = m(lin(X).float(), lin(Y).float(), SX, SY)
+        torch.testing.assert_close(d, ref_d, atol=5e-2, rtol=5e-3)
+        X.grad = None
+    q = torch.randn(2, 3, 5, 8, device=DEV).requires_grad_()
+    s = torch.randn(2, 6, 8, device=DEV)
+    lin8 = torch.nn.Linear(8, 8).to(DEV)
+    with torch.autocast("cuda", dtype=torch.float16):
+        a = TF.jeanie(lin8(q), lin8(s), gamma=0.3, max_shift=1)
+        b = TF.jeanie_from_cost(tw.euclidean_cost(lin8(q), lin8(s)), gamma=0.3, max_shift=1)
+    assert a.dtype == torch.float32 and b.dtype == torch.float32
+    (a.sum() + b.sum()).backward()
+    assert torch.isfinite(q.grad).all()

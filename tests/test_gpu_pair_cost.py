@@ -109,3 +109,20 @@ def test_rbf_cost_matches_oracle(shapes, dtype):
     assert _maxnorm(out, ref) < tol
     assert _maxnorm(a.grad, rq.grad) < tol
     assert _maxnorm(b.grad, rs.grad) < tol
+
+
+def test_rbf_cost_vmap_and_autocast():
+    """The RBF op under vmap (folded into the pair dimension) and autocast
+    (computed in float32, as registered)."""
+    g = torch.Generator().manual_seed(13)
+    q = torch.randn(3, 2, 4, 5, 6, generator=g, dtype=torch.float64).cuda()
+    s = torch.randn(3, 2, 7, 6, generator=g, dtype=torch.float64).cuda()
+    got = torch.func.vmap(lambda a, b: tw.rbf_cost(a, b, sigma=0.4))(q, s)
+    want = torch.stack([tw.rbf_cost(q[i], s[i], sigma=0.4) for i in range(3)])
+    torch.testing.assert_close(got, want, rtol=1e-12, atol=1e-12)
+    with torch.autocast("cuda", dtype=torch.float16):
+        half = tw.rbf_cost(q[0].half(), s[0].half(), sigma=0.4)
+    assert half.dtype == torch.float32
+    torch.testing.assert_close(half.double(), tw.rbf_cost(q[0].half().double(),
+                                                          s[0].half().double(), sigma=0.4),
+                               rtol=1e-5, atol=1e-5)
