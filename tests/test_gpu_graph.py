@@ -41,6 +41,12 @@ CASES = {
                  lambda xs: tw.SoftDTW(gamma=0.5)(*xs).mean()),
     "udtw_from_cost": ([((3, 17, 23), 1), ((3, 17, 23), 1)],
                        lambda xs: sum(TF.udtw_from_cost(xs[0], xs[1], gamma=0.3)).sum()),
+    # N > 256 and a small batch: several workgroups per pair in the forward
+    # (sentinel fill kernel, polled hand-off between workgroups)
+    "udtw_d1_groups": ([((2, 600, 1), 0), ((2, 620, 1), 0), ((2, 600, 1), 1),
+                        ((2, 620, 1), 1)], _udtw),
+    "udtw_from_cost_groups": ([((2, 300, 340), 1), ((2, 300, 340), 1)],
+                              lambda xs: sum(TF.udtw_from_cost(xs[0], xs[1], gamma=0.3)).sum()),
     "jeanie_features": ([((7, 9, 8, 32), 0), ((7, 8, 32), 0)],
                         lambda xs: TF.jeanie(xs[0], xs[1], gamma=0.1, max_shift=1).mean()),
     "jeanie_cost_2axes": ([((6, 5, 5, 9, 7), 1)],

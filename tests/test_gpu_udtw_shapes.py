@@ -152,3 +152,24 @@ def test_udtw_cost_band_long():
     (rd + 3 * rp).sum().backward()
     errs = [_maxnorm(a, b) for a, b in zip([d, p, c.grad, q.grad], [rd, rp, rc.grad, rq.grad])]
     assert max(errs) < 1e-9, errs
+
+
+@pytest.mark.parametrize("B,N,M", [(3, 700, 720), (260, 300, 310)])
+def test_udtw_many_groups_and_large_batch(B, N, M):
+    """D = 1 forward with several workgroups per pair (B = 3: three groups
+    each) and, past the workgroup budget (B = 260: 520 groups), one
+    workgroup per pair; float64 against the oracle."""
+    g = torch.Generator().manual_seed(14)
+    X = torch.randn(B, N, 1, generator=g, dtype=torch.float64)
+    Y = torch.randn(B, M, 1, generator=g, dtype=torch.float64)
+    sx = 0.5 + torch.rand(B, N, 1, generator=g, dtype=torch.float64)
+    sy = 0.5 + torch.rand(B, M, 1, generator=g, dtype=torch.float64)
+    xs = [t.cuda().requires_grad_(True) for t in (X, Y, sx, sy)]
+    d, p = tw.UDTW(gamma=1.0, beta=0.5)(*xs)
+    (d + p).sum().backward()
+    ref = [t.clone().requires_grad_(True) for t in (X, Y, sx, sy)]
+    rd, rp = OU.udtw(*ref, gamma=1.0, beta=0.5)
+    (rd + rp).sum().backward()
+    errs = [_maxnorm(a, b) for a, b in zip([d, p] + [t.grad for t in xs],
+                                           [rd, rp] + [t.grad for t in ref])]
+    assert max(errs) < 1e-9, errs

@@ -79,6 +79,7 @@ struct UdtwArgs {
   int sigma;     // VX / VY hold standard deviations: variances are their squares
   T hv1, hv0;    // half variance of an input v: v (hv1 v + hv0)
   int gstride;   // element stride of gr / gp (0: one value for every pair)
+  int groups;    // forward with MW: row groups (workgroups) per pair
 };
 
 // Half of a variance input: 0.5 v, or 0.5 v^2 when the input is a standard
@@ -128,6 +129,44 @@ constexpr int kSlots = 4;            // steps per block (and per loop trip)
 constexpr int kBox = 2 * kSlots;     // mailbox slots per wavefront boundary
 constexpr int kDump = 64 + kBox;
 constexpr int kWindow = 64;          // steps per soffset window (one per lane)
+
+// Several workgroups per pair (MW, forward only): workgroup g of a pair owns
+// rows [256 g, 256 g + 256), four wavefronts of one row per thread, one
+// wavefront per SIMD where the batch leaves CUs idle. Its first wavefront
+// takes the row above (row 256 g - 1, the previous workgroup's last) from
+// the R / P planes: a fill kernel first writes the sentinel into those rows,
+// the producing lane stores each cell a second time with an agent-scope
+// relaxed atomic store, and at the start of every 64-step window lane l of
+// the consumer polls the cell of step l with agent-scope atomic loads until
+// no valid lane holds the sentinel. Each cell is its own flag, so no fence
+// or cache write-back is needed, on any XCD. Workgroup g runs kGroupLag
+// diagonals behind g - 1's first wavefront: its last wavefront's lag plus a
+// window and the HBM round trip, so the polls rarely wait. The waited-on
+// workgroup always has the lower index, so in-order dispatch guarantees
+// progress, and every poll loop is bounded by kMwSpins.
+constexpr int kMwRows = 256;
+constexpr int kGroupLag = kLag * (kMwRows / 64) + kWindow + 16;
+constexpr int kMwSpins = 1 << 16;
+__host__ __device__ constexpr unsigned long long mw_sentinel_bits(int es) {
+  return es == 4 ? 0x7FC0DEADull : 0x7FF8DEADDEADDEADull;
+}
+// Lane l's value of v, wave-uniform.
+__device__ __forceinline__ float lane_val(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ double lane_val(double v, int l) {
+  const long long x = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane((int)x, l);
+  const int hi = __builtin_amdgcn_readlane((int)(x >> 32), l);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+template <typename T>
+__device__ __forceinline__ bool mw_is_sentinel(T v) {
+  if constexpr (sizeof(T) == 4)
+    return __float_as_uint(v) == (unsigned)mw_sentinel_bits(4);
+  else
+    return (unsigned long long)__double_as_longlong(v) == mw_sentinel_bits(8);
+}
 
 // Barrier at the end of a block: every LDS operation of this wavefront is
 // complete (the block's mailbox stores and the reads of the previous block's
@@ -181,20 +220,27 @@ struct MaxThreads {
 
 // LC (one row per thread): the column operands come from LDS (ColRec);
 // otherwise they travel down the rows with the DPP shifts that move R.
-template <typename T, int ROWS, int SRC, bool PEN, bool BAND, int PF, bool LC>
+template <typename T, int ROWS, int SRC, bool PEN, bool BAND, int PF, bool LC, bool MW = false>
 __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_fwd_kernel(UdtwArgs<T> a) {
   extern __shared__ __align__(16) unsigned char smem_raw[];
   constexpr int ES = sizeof(T);
   constexpr bool COLS = SRC != SRC_COST;
   constexpr bool FLOW = COLS && !LC;
   static_assert(!LC || (COLS && ROWS == 1), "LDS columns need one row per thread");
+  static_assert(!MW || (ROWS == 1 && !LC && !BAND), "MW: one row per thread, no band");
   const int N = a.N, M = a.M;
-  const int b = blockIdx.x;
+  // MW: pair b, row group grp of G, rows from rbase
+  const int G = MW ? a.groups : 1;
+  const int b = MW ? (int)blockIdx.x / G : (int)blockIdx.x;
+  const int grp = MW ? (int)blockIdx.x % G : 0;
+  const int rbase = grp * kMwRows;
   const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const T INF = inf_v<T>();
   const long long NM = (long long)N * M;
   const int Dn = N + M - 1;
+  // MW: this workgroup's last wavefront publishes its last row (not the last group's)
+  const bool publish = MW && grp < G - 1 && wave == nw - 1;
 
   // box[v * kBox + slot]: wavefront v's inbox (the row above its first
   // row; box[nw] is the last wavefront's unread outbox), then the dump area.
@@ -234,7 +280,7 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
   Rec4<T>* const my_out = lane == 63 ? outbox : dump + lane;
   __syncthreads();
 
-  const int row0 = tid * ROWS;
+  const int row0 = rbase + tid * ROWS;
   T xr[ROWS], hxr[ROWS], r1[ROWS], r2[ROWS], p1[ROWS], p2[ROWS], yc[ROWS], hyc[ROWS];
   int vst[ROWS], vnat[ROWS], jb[ROWS];
 #pragma unroll
@@ -250,10 +296,11 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
     vnat[k] = i < N ? i * (M - 1) * ES : 0;   // [N, M] offset of (i, d - i) minus d
     jb[k] = i < N ? -i : INT_MIN / 2;         // column of row i on diagonal d is d + jb
   }
-  T nr1 = (tid == 0) ? (T)0 : INF, nr2 = INF, np1 = (T)0, np2 = (T)0;
+  T nr1 = (row0 == 0) ? (T)0 : INF, nr2 = INF, np1 = (T)0, np2 = (T)0;
 
-  const int d_first = -kLag * wave;
-  const int steps = (Dn + kLag * (nw - 1) + kSlots - 1) / kSlots * kSlots;
+  const int d_first = -kLag * wave - (MW ? kGroupLag * grp : 0);
+  const int steps =
+      (Dn + kLag * (nw - 1) + (MW ? kGroupLag * (G - 1) : 0) + kSlots - 1) / kSlots * kSlots;
 
   T rc[PF][ROWS], rq[PF][ROWS];
   // C (and Q) of diagonal d at byte soffset so: max(d, 0) * ES in the [N, M]
@@ -282,12 +329,14 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
   auto sweep = [&](auto edge_tag) {
     constexpr bool EDGE = decltype(edge_tag)::value;
     T ey_ring[kSlots], evy_ring[kSlots];   // EDGE: column d of ring slot d % kSlots
-    int vcol = 0;                          // EDGE: byte offset of column t0
+    // EDGE: byte offset of the column entering row rbase on the block's first
+    // diagonal (negative before the grid: those loads fail the range check)
+    int vcol = (d_first - rbase) * ES;
     if (EDGE && FLOW) {
 #pragma unroll
       for (int u = 0; u < kSlots; ++u) {
-        ey_ring[u] = col_y(u * ES);
-        evy_ring[u] = col_vy(u * ES);
+        ey_ring[u] = col_y(vcol + u * ES);
+        evy_ring[u] = col_vy(vcol + u * ES);
       }
     }
     // LC: this row's column entry on diagonal d is crow[d]; step u of a block
@@ -306,6 +355,27 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
       const int so_st = diag_soff(dl, N, M) * ES;
       const int so_ld = SRC != SRC_FEAT1 ? fetch_so(dl + PF) : 0;
       const int tn = min(kWindow, steps - tw);
+      // MW, edge wavefront of a later group: lane l holds the row above on
+      // step l of the window, (R, P) of cell (rbase - 1, dl - rbase)
+      T win_r = INF, win_p = (T)0;
+      if (MW && EDGE && grp > 0) {
+        const int j = dl - rbase;
+        const bool v = (unsigned)j < (unsigned)M;
+        T* const pr = a.R + (size_t)b * NM + diag_soff(dl - 1, N, M) + (rbase - 1);
+        T* const pp = PEN ? a.P + (size_t)b * NM + diag_soff(dl - 1, N, M) + (rbase - 1) : pr;
+        T vr = INF, vp = (T)0;
+        for (int spin = 0; spin < kMwSpins; ++spin) {
+          if (v) {
+            vr = __hip_atomic_load(pr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (PEN) vp = __hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          const bool pend = v && (mw_is_sentinel(vr) || (PEN && mw_is_sentinel(vp)));
+          if (__ballot(pend) == 0) break;
+          __builtin_amdgcn_s_sleep(4);
+        }
+        win_r = v ? vr : INF;
+        win_p = v ? vp : (T)0;
+      }
     for (int t0 = 0; t0 < tn; t0 += kSlots) {
       const int half = (t0 / kSlots) & 1;   // mailbox half of this block
       Rec4<T> rec[kSlots];
@@ -339,7 +409,10 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
         // the row above the first row on diagonal d-1, and the column
         // entering the first row on diagonal d
         Rec4<T> e;
-        if (EDGE)
+        if (EDGE && MW)
+          e = {lane_val(win_r, t0 + u), lane_val(win_p, t0 + u), ey_ring[u],
+               COLS ? half_var(a, evy_ring[u]) : (T)0.5};
+        else if (EDGE)
           e = {INF, (T)0, ey_ring[u], COLS ? half_var(a, evy_ring[u]) : (T)0.5};
         else
           e = rec[u];
@@ -347,7 +420,8 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
         nr2 = nr1;
         np2 = np1;
         nr1 = shift_prev(r1[ROWS - 1], e.x);
-        if (PEN) np1 = EDGE ? shift_prev0(p1[ROWS - 1]) : shift_prev(p1[ROWS - 1], e.y);
+        if (PEN)
+          np1 = (EDGE && !MW) ? shift_prev0(p1[ROWS - 1]) : shift_prev(p1[ROWS - 1], e.y);
         if (LC) {
           yc[0] = creg[u & 1].y;
           hyc[0] = creg[u & 1].hy;
@@ -415,6 +489,13 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
           const int vo = valid ? vst[k] : kOob;
           bR.st(nr[k], vo, so);
           if (PEN) bP.st(np[k], vo, so);
+          if (MW && publish && lane == 63 && valid) {
+            // the next group's row above: a second, agent-coherent store
+            const size_t c = (size_t)b * NM + (size_t)((so + vst[k]) / ES);
+            __hip_atomic_store(a.R + c, nr[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (PEN)
+              __hip_atomic_store(a.P + c, np[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
         }
 #pragma unroll
         for (int k = 0; k < ROWS; ++k) {
@@ -952,6 +1033,41 @@ struct PrefetchDepth {
   static constexpr int value = ROWS <= 4 ? 4 : (ROWS == 8 ? 2 : 1);
 };
 
+// MW: the sentinel into the boundary rows (256 g - 1, g >= 1) of R and P.
+template <typename T>
+__global__ void __launch_bounds__(256) mw_fill(T* R, T* P, int B, int N, int M, int G) {
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long per = (long long)(G - 1) * M;
+  if (idx >= (long long)B * per) return;
+  const int b = (int)(idx / per);
+  const long long rem = idx - (long long)b * per;
+  const int g = 1 + (int)(rem / M), j = (int)(rem % M);
+  const int row = g * kMwRows - 1;
+  const size_t c = (size_t)b * N * M + diag_soff(row + j, N, M) + row;
+  T v;
+  if constexpr (sizeof(T) == 4)
+    v = __uint_as_float((unsigned)mw_sentinel_bits(4));
+  else
+    v = __longlong_as_double((long long)mw_sentinel_bits(8));
+  R[c] = v;
+  if (P) P[c] = v;
+}
+
+// Several workgroups per pair for the forward when the batch leaves CUs
+// idle (at most this many workgroups). Measured at B = 64 / 16, N = M =
+// 1024: the D = 1 forward 0.74 -> 0.62 / 0.46 ms, the cost-path forward
+// 3.36 -> 2.15 ms; the diagonal-major S forward (D > 1) 0.93 -> 1.07 ms,
+// so it keeps one workgroup per pair. TORCHWARP_UDTW_MW=0 turns MW off, 1
+// uses it for every source.
+constexpr long long kMwMaxGroups = 512;
+static inline bool mw_enabled(int src) {
+  static const int mode = [] {
+    const char* e = getenv("TORCHWARP_UDTW_MW");
+    return e ? atoi(e) : 2;
+  }();
+  return mode == 1 || (mode == 2 && src != SRC_SQ);
+}
+
 template <typename T, int SRC, bool PEN, bool BAND>
 static int launch_udtw(bool backward, const UdtwArgs<T>& a, int B, hipStream_t stream,
                        const char* what) {
@@ -977,6 +1093,22 @@ static int launch_udtw(bool backward, const UdtwArgs<T>& a, int B, hipStream_t s
       else
         hipLaunchKernelGGL((udtw_fwd_kernel<T, 1, SRC, PEN, BAND, PrefetchDepth<1>::value, true>),
                            grid, block, lc_lds, stream, a);
+      return check_launch(what);
+    }
+  }
+  if constexpr (!BAND) {
+    const int G = (a.N + kMwRows - 1) / kMwRows;
+    if (!backward && sh.rows == 1 && G > 1 && (long long)B * G <= kMwMaxGroups &&
+        mw_enabled(SRC)) {
+      UdtwArgs<T> m = a;
+      m.groups = G;
+      const long long fills = (long long)B * (G - 1) * a.M;
+      hipLaunchKernelGGL((mw_fill<T>), dim3((unsigned)((fills + 255) / 256)), dim3(256), 0,
+                         stream, m.R, PEN ? m.P : (T*)nullptr, B, a.N, a.M, G);
+      const size_t mlds = udtw_lds<T>(false, kMwRows / 64, false, a.N, a.M);
+      hipLaunchKernelGGL(
+          (udtw_fwd_kernel<T, 1, SRC, PEN, false, PrefetchDepth<1>::value, false, true>),
+          dim3((unsigned)(B * G)), dim3(kMwRows), mlds, stream, m);
       return check_launch(what);
     }
   }
