@@ -315,7 +315,42 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
       if (SRC == SRC_COST && PEN) q[k] = bQ.ld<T>(vo, so);
     }
   };
-  if (SRC != SRC_FEAT1) {
+  // VEC (cost in the [N, M] layout): a row's cells on the kSlots diagonals
+  // of a block are consecutive in memory, so each lane loads them with one
+  // 16-byte load per plane, a block ahead (into cn / qn, copied into the
+  // ring at the block's start), instead of one 4-byte load per step: the
+  // lanes' rows are M apart, so every load touches one cache line per lane.
+  // Cells off the row read another row's or no data; the sweep masks them.
+  constexpr bool VEC = SRC == SRC_COST && PF == kSlots;
+  T cn[kSlots][ROWS], qn[kSlots][ROWS];
+  auto fetch4 = [&](int d, T (*c)[ROWS], T (*q)[ROWS]) {
+#pragma unroll
+    for (int k = 0; k < ROWS; ++k) {
+      const int vo = vnat[k] + d * ES;   // cell (i, d - i) and the next three
+#pragma unroll
+      for (int h = 0; h < (int)sizeof(T) / 4; ++h) {
+        const unsigned int __attribute__((ext_vector_type(4))) w =
+            __builtin_amdgcn_raw_buffer_load_b128(bC.r, vo + 16 * h, 0, 0);
+        unsigned int __attribute__((ext_vector_type(4))) z = {0, 0, 0, 0};
+        if (PEN) z = __builtin_amdgcn_raw_buffer_load_b128(bQ.r, vo + 16 * h, 0, 0);
+        if constexpr (sizeof(T) == 4) {
+          c[0][k] = __uint_as_float(w.x); c[1][k] = __uint_as_float(w.y);
+          c[2][k] = __uint_as_float(w.z); c[3][k] = __uint_as_float(w.w);
+          q[0][k] = __uint_as_float(z.x); q[1][k] = __uint_as_float(z.y);
+          q[2][k] = __uint_as_float(z.z); q[3][k] = __uint_as_float(z.w);
+        } else {
+          auto dbl = [](unsigned lo, unsigned hi) {
+            return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+          };
+          c[2 * h][k] = dbl(w.x, w.y); c[2 * h + 1][k] = dbl(w.z, w.w);
+          q[2 * h][k] = dbl(z.x, z.y); q[2 * h + 1][k] = dbl(z.z, z.w);
+        }
+      }
+    }
+  };
+  if (VEC) {
+    fetch4(d_first, cn, qn);
+  } else if (SRC != SRC_FEAT1) {
 #pragma unroll
     for (int u = 0; u < PF; ++u) {
       const int d = d_first + u;
@@ -388,6 +423,16 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
       }
       Rec4<T>* const out = my_out + half * kSlots;
       const ColRec<T>* const cblk = crow + (d_first + tw + t0);
+      if (VEC) {
+#pragma unroll
+        for (int u = 0; u < kSlots; ++u)
+#pragma unroll
+          for (int k = 0; k < ROWS; ++k) {
+            rc[u][k] = cn[u][k];
+            rq[u][k] = qn[u][k];
+          }
+        fetch4(d_first + tw + t0 + kSlots, cn, qn);
+      }
       // band: every row of this wavefront is outside |2i - d| <= band on all
       // of the block's diagonals, so its cells are INF / 0 without arithmetic
       bool skip = false;
@@ -508,7 +553,7 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
         // refill, so the slot's register is reused in place and the loop back
         // edge needs no copies (nor the waits they imply).
         __builtin_amdgcn_sched_barrier(0);
-        if (SRC != SRC_FEAT1)
+        if (SRC != SRC_FEAT1 && !VEC)
           fetch(d + PF, __builtin_amdgcn_readlane(so_ld, t0 + u), rc[u % PF], rq[u % PF]);
         if (EDGE && FLOW) {
           ey_ring[u] = col_y(vcol + (u + kSlots) * ES);
