@@ -709,6 +709,7 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
   const int steps = (Dn + kLag * (nw - 1) + kSlots - 1) / kSlots * kSlots;
 
   T rr[PF][ROWS], rp[PF][ROWS], rc[PF][ROWS], rq[PF][ROWS];
+  constexpr bool VEC = SRC == SRC_COST && PF == kSlots;   // block-wide C / Q loads
   // R, P of diagonal d at byte soffset so_d = soff(d) * ES (diagonal-major),
   // C, Q at so_n = max(d, 0) * ES ([N, M])
   auto fetch = [&](int d, int so_d, int so_n, T* r, T* p, T* c, T* q) {
@@ -720,10 +721,51 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
       if (PEN) p[k] = bP.ld<T>(vd, so_d);
       if (SRC == SRC_SQ) {
         c[k] = bC.ld<T>(vd, so_d);   // diagonal-major, as R
-      } else if (SRC != SRC_FEAT1) {
+      } else if (SRC != SRC_FEAT1 && !VEC) {
         const int vn = v ? vnat[k] : kOob;
         c[k] = bC.ld<T>(vn, so_n);
         if (SRC == SRC_COST && PEN) q[k] = bQ.ld<T>(vn, so_n);
+      }
+    }
+  };
+  // VEC: as in the forward, a row's C / Q cells of a block come from one
+  // 16-byte load per plane, a block ahead. The block's diagonals run down
+  // from dh, so cell (i, dh - u - i) of step u is component 3 - u of the
+  // load at (i, dh - 3 - i).
+  T cn[kSlots][ROWS], qn[kSlots][ROWS];
+  auto fetch4 = [&](int dh, T (*c)[ROWS], T (*q)[ROWS]) {
+#pragma unroll
+    for (int k = 0; k < ROWS; ++k) {
+      const int vo = vnat[k] + (dh - (kSlots - 1)) * ES;
+#pragma unroll
+      for (int h = 0; h < (int)sizeof(T) / 4; ++h) {
+        const unsigned int __attribute__((ext_vector_type(4))) w =
+            __builtin_amdgcn_raw_buffer_load_b128(bC.r, vo + 16 * h, 0, 0);
+        unsigned int __attribute__((ext_vector_type(4))) z = {0, 0, 0, 0};
+        if (PEN) z = __builtin_amdgcn_raw_buffer_load_b128(bQ.r, vo + 16 * h, 0, 0);
+        if constexpr (sizeof(T) == 4) {
+          c[3][k] = __uint_as_float(w.x); c[2][k] = __uint_as_float(w.y);
+          c[1][k] = __uint_as_float(w.z); c[0][k] = __uint_as_float(w.w);
+          q[3][k] = __uint_as_float(z.x); q[2][k] = __uint_as_float(z.y);
+          q[1][k] = __uint_as_float(z.z); q[0][k] = __uint_as_float(z.w);
+        } else {
+          auto dbl = [](unsigned lo, unsigned hi) {
+            return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+          };
+          c[3 - 2 * h][k] = dbl(w.x, w.y); c[2 - 2 * h][k] = dbl(w.z, w.w);
+          q[3 - 2 * h][k] = dbl(z.x, z.y); q[2 - 2 * h][k] = dbl(z.z, z.w);
+        }
+      }
+      // At the plane's start (row 0, the last blocks) the load begins before
+      // the plane: a negative voffset fails the range check as a whole, so
+      // those lanes take the block's cells one by one (negative ones read 0).
+      if (__ballot(vo < 0) != 0 && vo < 0) {
+#pragma unroll
+        for (int u = 0; u < kSlots; ++u) {
+          const int vu = vnat[k] + (dh - u) * ES;
+          c[u][k] = bC.ld<T>(vu, 0);
+          q[u][k] = PEN ? bQ.ld<T>(vu, 0) : (T)0;
+        }
       }
     }
   };
@@ -732,6 +774,7 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
     const int d = d_first - u;
     fetch(d, diag_soff(d, N, M) * ES, (d > 0 ? d : 0) * ES, rr[u], rp[u], rc[u], rq[u]);
   }
+  if (VEC) fetch4(d_first, cn, qn);
 
   // The sweep, instantiated for the edge wavefront (the last: its row below
   // is the virtual row N, its entering column comes from a register ring of
@@ -787,6 +830,16 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
       const int dlo = d_first - tw - t0 - kSlots;
       const ColRec<T>* const cblk = crow + dlo;
       ColRec<T>* const ablk = arow + dlo;
+      if (VEC) {
+#pragma unroll
+        for (int u = 0; u < kSlots; ++u)
+#pragma unroll
+          for (int k = 0; k < ROWS; ++k) {
+            rc[u][k] = cn[u][k];
+            rq[u][k] = qn[u][k];
+          }
+        fetch4(d_first - tw - t0 - kSlots, cn, qn);
+      }
       // band: every row of this wavefront is outside |2i - d| <= band on all
       // of the block's diagonals (the forward left those cells at INF)
       bool skip = false;
