@@ -37,6 +37,9 @@ CASES = {
                 _udtw),
     "udtw_d8_swap": ([((5, 33, 8), 0), ((5, 21, 8), 0), ((5, 33, 1), 1), ((5, 21, 1), 1)],
                      _udtw),
+    # Sakoe-Chiba band: the reachability check is made from the shapes
+    "udtw_band": ([((4, 30, 1), 0), ((4, 33, 1), 0), ((4, 30, 1), 1), ((4, 33, 1), 1)],
+                  lambda xs: sum(tw.UDTW(gamma=0.7, beta=1.0, bandwidth=4)(*xs)).mean()),
     "soft_dtw": ([((4, 30, 3), 0), ((4, 25, 3), 0)],
                  lambda xs: tw.SoftDTW(gamma=0.5)(*xs).mean()),
     "udtw_from_cost": ([((3, 17, 23), 1), ((3, 17, 23), 1)],

@@ -6,7 +6,7 @@ import torch
 import torch.nn as nn
 
 from .udtw import _ops as _udtw_ops
-from .udtw.functional import _BACKENDS, _batchable, _check_band_reached, udtw, udtw_from_cost
+from .udtw.functional import _BACKENDS, _batchable, udtw, udtw_from_cost
 
 
 def softmin(x: torch.Tensor, gamma: float, dim: Optional[int] = None) -> torch.Tensor:

@@ -90,11 +90,15 @@ def _batchable(*tensors):
             and all(t.dtype == X.dtype and t.device == X.device for t in tensors))
 
 
-def _check_band_reached(distance, band):
-    # data-dependent; skipped while torch.compile traces (then +inf shows instead)
-    if band > 0 and not torch.compiler.is_compiling():
-        if not bool(torch.isfinite(distance).all()):
-            raise ValueError("No valid DTW path reaches the final cell under the given bandwidth")
+def _check_band_reached(band, N, M):
+    """The reference raises when the distance is not finite under a band
+    (udtw/functional.py:94-98). With finite costs that happens exactly when
+    no monotone path stays within |i - j| <= band, i.e. |N - M| > band, so
+    the check is made from the shapes: no device-to-host synchronisation,
+    and banded calls capture in HIP graphs. (Non-finite inputs give a
+    non-finite result instead of this error.)"""
+    if band > 0 and abs(N - M) > band:
+        raise ValueError("No valid DTW path reaches the final cell under the given bandwidth")
 
 
 def udtw_from_cost(cost, penalty, *, gamma=1.0, bandwidth=None, backend="auto"):
@@ -129,8 +133,8 @@ def udtw_from_cost(cost, penalty, *, gamma=1.0, bandwidth=None, backend="auto"):
         cost = cost.transpose(1, 2)
         penalty = penalty.transpose(1, 2)
     band = 0.0 if bandwidth is None else float(bandwidth)
+    _check_band_reached(band, cost.shape[1], cost.shape[2])
     distance, pen, _, _ = _ops.dp_apply(cost, penalty, float(gamma), band, backend)
-    _check_band_reached(distance, band)
     return UDTWOutput(distance, pen)
 
 
@@ -147,9 +151,9 @@ def _udtw_fused(X, Y, sigma_x, sigma_y, beta, gamma, bandwidth, eps, backend):
     if sy is sx:
         sy = sx.view_as(sx)
     band = 0.0 if bandwidth is None else float(bandwidth)
+    _check_band_reached(band, X.shape[1], Y.shape[1])
     distance, pen, _, _, _ = _ops.fused_apply(X, Y, sx, sy, float(gamma), float(beta), float(eps),
                                            band, backend, True)
-    _check_band_reached(distance, band)
     return UDTWOutput(distance, pen)
 
 
