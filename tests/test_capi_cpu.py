@@ -112,3 +112,39 @@ def test_exports_match_reference_surface():
                  "rbf_cost"):
         assert hasattr(TF, name), name
     assert repr(tw.JEANIE(gamma=0.1, max_shift=(1, 1))).count("max_shift=(1, 1)") == 1
+
+
+def _declared_arities():
+    """name -> number of parameters, from the header's declarations."""
+    text = (ROOT / "include" / "torchwarp_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(tw_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_binding_signatures_match_the_header():
+    """The ctypes argument codes (torchwarp_amd/_hip.py) have exactly as many
+    entries as each declaration has parameters (the stream included)."""
+    ar = _declared_arities()
+    for base, sig in _hip.SIGNATURES.items():
+        for suffix in ("_f32", "_f64"):
+            assert ar[base + suffix] == len(sig), (base + suffix, ar[base + suffix], sig)
+    for base, sig in _hip.SIGNATURES_F64.items():
+        assert ar[base + "_f64"] == len(sig), base
+
+
+def test_invalid_arguments_are_rejected_before_any_launch():
+    """Argument errors return TW_EINVAL with a message and launch nothing, so
+    they can be checked without a GPU."""
+    lib = _hip.library()
+    f = lib.tw_rbf_cost_fwd_f32
+    assert f(None, None, 1, 2, 3, 4, -1.0, None, None) == 1
+    assert b"sigma" in lib.tw_last_error()
+    g = lib.tw_pair_cost_fwd_f32
+    assert g(None, None, 1, 0, 3, 4, 1, None, None) == 1
+    assert b"bad sizes" in lib.tw_last_error()
+    h = lib.tw_rbf_cost_bwd_f64
+    assert h(None, None, None, 2, -1, 3, 4, 0.5, None, None, None) == 1
