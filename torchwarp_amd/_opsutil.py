@@ -70,7 +70,8 @@ def per_pair_dot(grads, tangents):
     for g, t in zip(grads, tangents):
         if g is None or t is None:
             continue
-        v = (g * t).reshape(g.shape[0], -1).sum(1)
+        v = g * t
+        v = v.reshape(v.shape[0], -1).sum(1) if v.numel() else v.new_zeros(v.shape[0])
         out = v if out is None else out + v
     return out
 

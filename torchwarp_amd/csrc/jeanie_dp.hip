@@ -557,8 +557,8 @@ template <typename T>
 int jeanie_cost_fwd(const T* C, int B, int K1, int K2, int Tn, int Un, int swap, int s1, int s2,
                     double gamma, T* R, T* out, hipStream_t s, const char* what) {
   if (int e = jeanie_check<T>(what, B, K1, K2, Tn, Un, s1, s2, gamma)) return e;
-  if (!C || !R || !out) return fail(TW_EINVAL, "%s: null pointer", what);
   if (B == 0) return TW_OK;
+  if (!C || !R || !out) return fail(TW_EINVAL, "%s: null pointer", what);
   JeanieArgs<T> a = {};
   a.C = C;
   a.Rw = R;
@@ -598,8 +598,8 @@ int jeanie_cost_bwd(const T* C, const T* R, const T* gout, const T* gR, int B, i
                     int Tn, int Un, int swap, int s1, int s2, double gamma, T* dC, hipStream_t s,
                     const char* what) {
   if (int e = jeanie_check<T>(what, B, K1, K2, Tn, Un, s1, s2, gamma)) return e;
-  if (!C || !R || !gout || !dC) return fail(TW_EINVAL, "%s: null pointer", what);
   if (B == 0) return TW_OK;
+  if (!C || !R || !gout || !dC) return fail(TW_EINVAL, "%s: null pointer", what);
   JeanieArgs<T> a = {};
   a.C = C;
   a.R = R;
@@ -712,8 +712,8 @@ int fvm_fwd(const T* C, int B, int K, int Tn, int Un, double gamma, T* tmp, T* R
             T* pen_scratch, hipStream_t s, const char* what) {
   if (B < 0 || K <= 0 || Tn <= 0 || Un <= 0 || !(gamma > 0))
     return fail(TW_EINVAL, "%s: bad arguments", what);
-  if (!C || !tmp || !R || !out || !pen_scratch) return fail(TW_EINVAL, "%s: null pointer", what);
   if (B == 0) return TW_OK;
+  if (!C || !tmp || !R || !out || !pen_scratch) return fail(TW_EINVAL, "%s: null pointer", what);
   const int swap = Tn > Un;
   const T k = (T)(1.4426950408889634 / gamma), inv_k = (T)(gamma * 0.6931471805599453);
   dim3 grid((Tn * Un + 255) / 256, B);
@@ -734,8 +734,8 @@ int fvm_bwd(const T* C, const T* tmp, const T* R, const T* gout, int B, int K, i
             double gamma, T* dC, T* ws, hipStream_t s, const char* what) {
   if (B < 0 || K <= 0 || Tn <= 0 || Un <= 0 || !(gamma > 0))
     return fail(TW_EINVAL, "%s: bad arguments", what);
-  if (!C || !tmp || !R || !gout || !dC || !ws) return fail(TW_EINVAL, "%s: null pointer", what);
   if (B == 0) return TW_OK;
+  if (!C || !tmp || !R || !gout || !dC || !ws) return fail(TW_EINVAL, "%s: null pointer", what);
   const int swap = Tn > Un;
   const int N = swap ? Un : Tn, M = swap ? Tn : Un;
   if (int e = udtw_cost_bwd_any<T>(tmp, nullptr, R, nullptr, gout, nullptr, B, N, M, gamma, ws,
@@ -781,8 +781,8 @@ int jeanie_feat_bwd(const T* q, const T* sup, const T* cost, const T* R, const T
                     const char* what) {
   if (metric != 1 && metric != 2)
     return fail(TW_EINVAL, "%s: metric must be 1 (squared) or 2 (Euclidean)", what);
-  if (!ws) return fail(TW_EINVAL, "%s: workspace needed", what);
   if (B == 0) return TW_OK;
+  if (!ws) return fail(TW_EINVAL, "%s: workspace needed", what);
   const int swap = Tq > Us;
   if (int e = jeanie_cost_bwd<T>(cost, R, gout, gR, B, K1, K2, swap ? Us : Tq, swap ? Tq : Us,
                                  swap, s1, s2, gamma, ws, s, what))

@@ -575,8 +575,8 @@ static int pair_cost_fwd_impl(const T* A, const T* Bm, int P, int R, int C, int 
   if (P < 0 || R <= 0 || C <= 0 || D <= 0) return fail(TW_EINVAL, "%s: bad sizes", what);
   if (DG && (metric != MET_RAW || R > C))
     return fail(TW_EINVAL, "%s: internal: diagonal planes are raw with R <= C", what);
-  if (!A || !Bm || !out) return fail(TW_EINVAL, "%s: null pointer", what);
   if (P == 0) return TW_OK;
+  if (!A || !Bm || !out) return fail(TW_EINVAL, "%s: null pointer", what);
   if (P > 65535) return fail(TW_ESIZE, "%s: at most 65535 pairs per call", what);
   if (metric != MET_RAW && metric != MET_SQ && metric != MET_EUC)
     return fail(TW_EINVAL, "%s: unknown metric %d", what, metric);
@@ -624,9 +624,9 @@ static int pair_cost_bwd_impl(const T* A, const T* Bm, const T* cost, const T* d
   if (P < 0 || R <= 0 || C <= 0 || D <= 0) return fail(TW_EINVAL, "%s: bad sizes", what);
   if (DG && (metric != MET_RAW || R > C))
     return fail(TW_EINVAL, "%s: internal: diagonal planes are raw with R <= C", what);
+  if (P == 0) return TW_OK;
   if (!A || !Bm || !dcost || !dA || !dB) return fail(TW_EINVAL, "%s: null pointer", what);
   if (metric != MET_RAW && !cost) return fail(TW_EINVAL, "%s: metric needs the cost", what);
-  if (P == 0) return TW_OK;
   if (P > 65535) return fail(TW_ESIZE, "%s: at most 65535 pairs per call", what);
   if (metric != MET_RAW && metric != MET_SQ && metric != MET_EUC)
     return fail(TW_EINVAL, "%s: unknown metric %d", what, metric);

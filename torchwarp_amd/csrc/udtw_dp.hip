@@ -45,6 +45,7 @@ template <typename T>
 static int cost_fwd(const T* C, const T* Q, int B, int N, int M, double gamma, double band, T* R,
                     T* P, T* out_r, T* out_p, hipStream_t s, const char* what) {
   if (int e = check_dims(what, B, N, M, gamma)) return e;
+  if (B == 0) return TW_OK;
   if (!C || !R || !out_r || !out_p) return fail(TW_EINVAL, "%s: null pointer", what);
   if (Q && !P) return fail(TW_EINVAL, "%s: a penalty needs the P buffer", what);
   UdtwArgs<T> a = {};
@@ -65,6 +66,7 @@ static int cost_bwd(const T* C, const T* Q, const T* R, const T* P, const T* gr,
                     int B, int N, int M, double gamma, double band, int gstride, T* dC, T* dQ,
                     hipStream_t s, const char* what) {
   if (int e = check_dims(what, B, N, M, gamma)) return e;
+  if (B == 0) return TW_OK;
   if (!C || !R || !gr || !dC) return fail(TW_EINVAL, "%s: null pointer", what);
   const bool pen = Q != nullptr;
   if (pen && (!P || !gp)) return fail(TW_EINVAL, "%s: a penalty needs P and grad_pen", what);
@@ -167,6 +169,7 @@ static int feat_fwd(const T* X, const T* Y, const T* vx, const T* vy, int B, int
                     const char* what) {
   if (int e = check_dims(what, B, N, M, gamma)) return e;
   if (D <= 0) return fail(TW_EINVAL, "%s: D must be > 0", what);
+  if (B == 0) return TW_OK;
   if (!X || !Y || !vx || !vy || !R || !out_r || !out_p)
     return fail(TW_EINVAL, "%s: null pointer", what);
   const bool pen = beta != 0.0;
@@ -203,6 +206,7 @@ static int feat_bwd(const T* X, const T* Y, const T* vx, const T* vy, const T* R
                     const char* what) {
   if (int e = check_dims(what, B, N, M, gamma)) return e;
   if (D <= 0) return fail(TW_EINVAL, "%s: D must be > 0", what);
+  if (B == 0) return TW_OK;
   if (!X || !Y || !vx || !vy || !R || !gr || !dX || !dY)
     return fail(TW_EINVAL, "%s: null pointer", what);
   if ((dvx == nullptr) != (dvy == nullptr))

@@ -3,6 +3,8 @@
 pair, then soft-DTW -- both inside the HIP FVM kernels.
 """
 
+import math
+
 import torch
 
 from . import _ops
@@ -24,7 +26,8 @@ def fvm_from_cost(cost, *, gamma=0.1, backend="auto"):
     if backend not in ("auto", "cuda", "torch"):
         raise ValueError("backend must be one of ('auto', 'cuda', 'torch')")
     B, T, U = cost.shape[0], cost.shape[-2], cost.shape[-1]
-    flat = cost.reshape(B, -1, T, U)
+    K = math.prod(cost.shape[1:-2])   # explicit, so an empty batch reshapes too
+    flat = cost.reshape(B, K, T, U)
     if flat.dtype not in (torch.float32, torch.float64):
         flat = flat.float()
     out, _, _ = _ops.fvm_apply(flat, float(gamma), backend)
@@ -41,10 +44,10 @@ def fvm(query, support, *, gamma=0.1, metric="euclidean", backend="auto"):
                          "[B, K'..., U, D]")
     B, T, D = query.shape[0], query.shape[-2], query.shape[-1]
     U = support.shape[-2]
-    q = query.reshape(B, -1, T, D)
+    q = query.reshape(B, math.prod(query.shape[1:-2]), T, D)
     if support.ndim == 3:
         cost = _METRICS[metric](q, support)
     else:
-        s = support.reshape(B, -1, U, D)
+        s = support.reshape(B, math.prod(support.shape[1:-2]), U, D)
         cost = _METRICS[metric](q.unsqueeze(2), s.unsqueeze(1))
     return fvm_from_cost(cost, gamma=gamma, backend=backend)
