@@ -23,6 +23,8 @@ SHAPES = [  # (B, N, M, D, gamma)
     (2, 300, 310, 1, 1.0),
     (2, 290, 270, 4, 1.0),     # N > M: the API swaps the sequences
     (1, 600, 640, 8, 1.0),     # one row per thread in float32, two in float64
+    (2, 250, 260, 4, 1.0),     # ragged row and column tails of the cost tiles
+    (1, 64, 1000, 4, 1.0),     # few rows against long columns
     (1, 1100, 1030, 1, 1.0),   # beyond 1024 rows: several rows per thread
 ]
 
