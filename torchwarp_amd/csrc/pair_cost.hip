@@ -325,6 +325,31 @@ __global__ void __launch_bounds__(256) pair_fwd_mfma(const float* __restrict__ A
     for (int t = 0; t < TN; ++t)
       tl[4 * g + i][16 * t + li] = finish_cost<float, MET>(nr + nb[t] - 2.f * acc[t][i]);
   }
+  if ((long long)R * C < (1LL << 31)) {
+    // Lane l holds the run starts (plane_index minus the row) of tile
+    // diagonals l and l + 64, below 2^31 by the plane size; each store picks
+    // its group's start from four v_readlane results instead of evaluating
+    // diag_offset per cell.
+    int run0 = 0, run1 = 0;
+    {
+      const int d0 = r0 + c0 + lane, d1 = d0 + 64;
+      if (d0 <= R + C - 2) run0 = (int)(diag_offset(d0, R, C) - (d0 - C + 1 > 0 ? d0 - C + 1 : 0));
+      if (d1 <= R + C - 2) run1 = (int)(diag_offset(d1, R, C) - (d1 - C + 1 > 0 ? d1 - C + 1 : 0));
+    }
+#pragma unroll
+    for (int dd0 = 0; dd0 < 16 + W - 1; dd0 += 4) {
+      const int dd = dd0 + g, rr = li, cc = dd - rr;
+      const int r = r0 + rr, c = c0 + cc;
+      int sk[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        sk[k] = dd0 + k < 64 ? __builtin_amdgcn_readlane(run0, (dd0 + k) & 63)
+                             : __builtin_amdgcn_readlane(run1, (dd0 + k) & 63);
+      const int st = g == 0 ? sk[0] : (g == 1 ? sk[1] : (g == 2 ? sk[2] : sk[3]));
+      if (dd < 16 + W - 1 && cc >= 0 && cc < W && r < R && c < C) o[(size_t)st + r] = tl[rr][cc];
+    }
+    return;
+  }
   for (int dd0 = 0; dd0 < 16 + W - 1; dd0 += 4) {
     const int dd = dd0 + g, rr = li, cc = dd - rr;
     const int r = r0 + rr, c = c0 + cc;
