@@ -5,8 +5,10 @@ Reference formulas (jeanie/distances.py:25-38, udtw/_autograd.py:24-29):
 S = |a|^2 + |b|^2 - 2 a.b, squared-Euclidean max(S, 0), Euclidean
 sqrt(max(S, 0)) with zero gradient at zero distance. The check runs on ragged
 shapes that exercise partial 16-row / 16-column tiles, D that is and is not a
-multiple of 4 and 16 (matrix-core and FMA forward), and C on both sides of the
-fused backward's limit. float64 within 1e-10 and float32 within 1e-5 of the
+multiple of 4 and 16 (the float32 matrix-core forward takes 16-byte chunks or
+single elements; float64 runs the FMA forward), D on both sides of the
+matrix-core backward's limit of 64, and C on both sides of the fused
+backward's limit. float64 within 1e-10 and float32 within 1e-5 of the
 largest entry (values and gradients; random inputs keep every distance clear
 of zero, where the GEMM form cancels).
 """
@@ -31,6 +33,7 @@ SHAPES = [  # (P, R, C, D)
     (1, 65, 129, 33),
     (2, 200, 100, 64),
     (3, 100, 90, 3),
+    (1, 30, 200, 75),   # D > 64 and not a multiple of 4
 ]
 
 

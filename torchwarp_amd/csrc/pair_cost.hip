@@ -244,7 +244,19 @@ __device__ __forceinline__ f32x4 ld4(const Buf& b, int v, int s) {
                __uint_as_float(w.w)};
 }
 
-template <int MET, int TN, bool DG>
+// Elements k..k+3 of the row at byte offset v as four single-dword loads
+// (rows of any D are only 4-byte aligned); elements at or past D, and every
+// element of a row at kOob, read 0.
+__device__ __forceinline__ f32x4 ld4_dwords(const Buf& b, int v, int k, int D) {
+  f32x4 x;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) x[j] = b.ldf(v == kOob || k + j >= D ? kOob : v + (k + j) * 4, 0);
+  return x;
+}
+
+// D4: D % 4 == 0, each row's chunk is one 16-byte load; otherwise four
+// single-dword loads with the tail masked.
+template <int MET, int TN, bool DG, bool D4>
 __global__ void __launch_bounds__(256) pair_fwd_mfma(const float* __restrict__ A,
                                                      const float* __restrict__ Bm,
                                                      float* __restrict__ out, int R, int C,
@@ -261,12 +273,13 @@ __global__ void __launch_bounds__(256) pair_fwd_mfma(const float* __restrict__ A
   ba.init(A + (size_t)p * R * D, (long long)R * D);
   bb.init(Bm + (size_t)p * C * D, (long long)C * D);
   const int ra = r0 + li;
-  const int va = ra < R ? (ra * D + 4 * g) * 4 : kOob;
+  // D4: offset of the lane's chunk; else of its row
+  const int va = ra < R ? (ra * D + (D4 ? 4 * g : 0)) * 4 : kOob;
   int vb[TN];
 #pragma unroll
   for (int t = 0; t < TN; ++t) {
     const int cb = c0 + 16 * t + li;
-    vb[t] = cb < C ? (cb * D + 4 * g) * 4 : kOob;
+    vb[t] = cb < C ? (cb * D + (D4 ? 4 * g : 0)) * 4 : kOob;
   }
   f32x4 acc[TN];
   float na = 0.f, nb[TN];
@@ -277,11 +290,11 @@ __global__ void __launch_bounds__(256) pair_fwd_mfma(const float* __restrict__ A
   }
   for (int k0 = 0; k0 < D; k0 += 16) {
     const bool kin = k0 + 4 * g < D;   // D % 4 == 0: a chunk is all in or all out
-    const f32x4 a4 = ld4(ba, kin ? va : kOob, k0 * 4);
+    const f32x4 a4 = D4 ? ld4(ba, kin ? va : kOob, k0 * 4) : ld4_dwords(ba, va, k0 + 4 * g, D);
     na += a4.x * a4.x + a4.y * a4.y + a4.z * a4.z + a4.w * a4.w;
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
-      const f32x4 b4 = ld4(bb, kin ? vb[t] : kOob, k0 * 4);
+      const f32x4 b4 = D4 ? ld4(bb, kin ? vb[t] : kOob, k0 * 4) : ld4_dwords(bb, vb[t], k0 + 4 * g, D);
       nb[t] += b4.x * b4.x + b4.y * b4.y + b4.z * b4.z + b4.w * b4.w;
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.x, b4.x, acc[t], 0, 0, 0);
       acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.y, b4.y, acc[t], 0, 0, 0);
@@ -607,7 +620,7 @@ static int pair_cost_fwd_impl(const T* A, const T* Bm, int P, int R, int C, int 
     return fail(TW_EINVAL, "%s: unknown metric %d", what, metric);
   if ((long long)R * D >= (1LL << 29) || (long long)C * D >= (1LL << 29))
     return fail(TW_ESIZE, "%s: one pair's block must stay below 2 GiB", what);
-  if (sizeof(T) == 4 && D % 4 == 0) {
+  if (sizeof(T) == 4) {
     // TN column tiles of 16 per wavefront share the A operand
     const int TN = C > 32 ? 4 : (C > 16 ? 2 : 1);
     const long long strips = (long long)((R + 15) / 16) * ((C + 16 * TN - 1) / (16 * TN));
@@ -615,8 +628,15 @@ static int pair_cost_fwd_impl(const T* A, const T* Bm, int P, int R, int C, int 
     const float* Af = reinterpret_cast<const float*>(A);
     const float* Bf = reinterpret_cast<const float*>(Bm);
     float* of = reinterpret_cast<float*>(out);
-#define TW_PAIR_MFMA(MET_, TN_) \
-  hipLaunchKernelGGL((pair_fwd_mfma<MET_, TN_, DG>), grid, block, 0, s, Af, Bf, of, R, C, D)
+#define TW_PAIR_MFMA(MET_, TN_)                                                              \
+  do {                                                                                       \
+    if (D % 4 == 0)                                                                          \
+      hipLaunchKernelGGL((pair_fwd_mfma<MET_, TN_, DG, true>), grid, block, 0, s, Af, Bf, of, \
+                         R, C, D);                                                           \
+    else                                                                                     \
+      hipLaunchKernelGGL((pair_fwd_mfma<MET_, TN_, DG, false>), grid, block, 0, s, Af, Bf,    \
+                         of, R, C, D);                                                       \
+  } while (0)
 #define TW_PAIR_MFMA_TN(MET_)          \
   if (TN == 4) TW_PAIR_MFMA(MET_, 4);  \
   else if (TN == 2) TW_PAIR_MFMA(MET_, 2); \
