@@ -33,7 +33,8 @@ SHAPES = [  # (P, R, C, D)
     (1, 65, 129, 33),
     (2, 200, 100, 64),
     (3, 100, 90, 3),
-    (1, 30, 200, 75),   # D > 64 and not a multiple of 4
+    (1, 30, 200, 75),   # D > 64 and not a multiple of 4: backward by feature slices
+    (2, 80, 90, 128),   # two whole 64-feature slices
 ]
 
 

@@ -373,16 +373,17 @@ __global__ void __launch_bounds__(256) pair_fwd_mfma(const float* __restrict__ A
 
 // ---------------------------------------------------------- MFMA backward
 //
-// fp32, D <= 64: the tiled backward's two passes (dA by 64-row blocks, dB by
+// fp32: the tiled backward's two passes (dA by 64-row blocks, dB by
 // 64-column blocks, each reading dS once) with the contraction on the matrix
-// cores. A workgroup owns 64 indices of one side; per 64-wide tile of the
+// cores. A launch covers the features k0 .. k0 + 16NB - 1 (NB <= 4); larger
+// D takes one launch pair per 64-feature slice. A workgroup owns 64 indices of one side; per 64-wide tile of the
 // streamed side it stages dS as ds[owned][streamed] and the other operand
 // transposed, opT[d][streamed], both with rows of 68 floats (16-byte aligned
 // for the float4 reads; the diagonal stores of the DG loader step 67 banks
 // per lane, so they do not conflict). Wavefront w owns rows 16w..16w+15 and
 // accumulates its 16 x 16NB block of dS . other with v_mfma_f32_16x16x4f32,
-// lane l reading the float4s ds[16w + l % 16][k0 + 4 (l / 16)] and
-// opT[16n + l % 16][k0 + 4 (l / 16)] (the k-permuted operand layout of the
+// lane l reading the float4s ds[16w + l % 16][kb + 4 (l / 16)] and
+// opT[16n + l % 16][kb + 4 (l / 16)] (the k-permuted operand layout of the
 // forward). The row sums of dS come from the same float4s. The next tile's
 // dS is loaded into registers before the MFMAs of this one. Workgroups are
 // numbered so that the tiles of one pair run on one XCD (the hardware
@@ -394,7 +395,7 @@ __global__ void __launch_bounds__(256) pair_bwd_mfma(const float* __restrict__ A
                                                      const float* __restrict__ cost,
                                                      const float* __restrict__ dcost,
                                                      float* __restrict__ dOut, int P, int R,
-                                                     int C, int D) {
+                                                     int C, int D, int k0) {
   constexpr int TL = 64, PT = TL + 4;
   __shared__ __align__(16) float ds[TL][PT];
   __shared__ __align__(16) float opT[16 * NB][PT];
@@ -459,7 +460,7 @@ __global__ void __launch_bounds__(256) pair_bwd_mfma(const float* __restrict__ A
 #pragma unroll
     for (int it = 0; it < NW; ++it) {
       const int e = it * 256 + tid, si = e & 63, dcol = e >> 6;
-      w[it] = bo.ldf(s0 + si < nstr && dcol < D ? ((s0 + si) * D + dcol) * 4 : kOob, 0);
+      w[it] = bo.ldf(s0 + si < nstr && k0 + dcol < D ? ((s0 + si) * D + k0 + dcol) * 4 : kOob, 0);
     }
   };
   auto stash = [&]() {
@@ -525,7 +526,7 @@ __global__ void __launch_bounds__(256) pair_bwd_mfma(const float* __restrict__ A
     const float so = __shfl(rs, 4 * lg + i);
 #pragma unroll
     for (int n = 0; n < NB; ++n) {
-      const int d = 16 * n + lr;
+      const int d = k0 + 16 * n + lr;
       if (o < nown && d < D)
         dOut[((size_t)p * nown + o) * D + d] = 2.f * (so * self[(size_t)o * D + d] - acc[n][i]);
     }
@@ -698,14 +699,13 @@ static int pair_cost_bwd_impl(const T* A, const T* Bm, const T* cost, const T* d
   if constexpr (sizeof(T) == 4) {
     // (byte offsets within a pair's plane and operands fit 31 bits)
     const long long big = (long long)(R > C ? R : C) * D;
-    if (D <= 64 && (long long)R * C < (1LL << 29) && big < (1LL << 29)) {
-      const int nb = (D + 15) / 16;
+    if ((long long)R * C < (1LL << 29) && big < (1LL << 29)) {
       const unsigned ga = (unsigned)((R + 63) / 64) * P, gb = (unsigned)((C + 63) / 64) * P;
 #define TW_PAIR_MFMA(MET_, NB_)                                                                \
   hipLaunchKernelGGL((pair_bwd_mfma<MET_, false, NB_, DG>), dim3(ga), dim3(256), 0, s, A, Bm,  \
-                     cost, dcost, dA, P, R, C, D);                                             \
+                     cost, dcost, dA, P, R, C, D, k0);                                         \
   hipLaunchKernelGGL((pair_bwd_mfma<MET_, true, NB_, DG>), dim3(gb), dim3(256), 0, s, A, Bm,   \
-                     cost, dcost, dB, P, R, C, D);
+                     cost, dcost, dB, P, R, C, D, k0);
 #define TW_PAIR_MFMA_D(MET_)                 \
   switch (nb) {                              \
     case 1: TW_PAIR_MFMA(MET_, 1) break;     \
@@ -713,10 +713,15 @@ static int pair_cost_bwd_impl(const T* A, const T* Bm, const T* cost, const T* d
     case 3: TW_PAIR_MFMA(MET_, 3) break;     \
     default: TW_PAIR_MFMA(MET_, 4) break;    \
   }
-      if (metric == MET_RAW) { TW_PAIR_MFMA_D(MET_RAW) }
-      else if constexpr (!DG) {
-        if (metric == MET_SQ) { TW_PAIR_MFMA_D(MET_SQ) }
-        else { TW_PAIR_MFMA_D(MET_EUC) }
+      // the passes are separable over features: D > 64 runs as 64-feature
+      // slices, each reading dS again
+      for (int k0 = 0; k0 < D; k0 += 64) {
+        const int nb = ((D - k0 < 64 ? D - k0 : 64) + 15) / 16;
+        if (metric == MET_RAW) { TW_PAIR_MFMA_D(MET_RAW) }
+        else if constexpr (!DG) {
+          if (metric == MET_SQ) { TW_PAIR_MFMA_D(MET_SQ) }
+          else { TW_PAIR_MFMA_D(MET_EUC) }
+        }
       }
 #undef TW_PAIR_MFMA_D
 #undef TW_PAIR_MFMA
