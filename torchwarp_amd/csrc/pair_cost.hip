@@ -123,18 +123,21 @@ __global__ void __launch_bounds__(256) pair_bwd_b_fma(const T* __restrict__ A,
 }
 
 
-// Tiled fp64 backward for D <= 32, one pass over dS per output: a workgroup owns
+// Tiled fp64 backward, one pass over dS per output: a workgroup owns
 // 64 rows (dA, COLS false) or 64 columns (dB, COLS true) of a pair and
 // streams the other axis in 64-wide tiles. Each dS tile is read with
 // coalesced 256-byte rows and staged in LDS as [owned][streamed] next to the
 // matching 64 x D block of the other operand; four threads share an owned
-// index and each accumulates DPT of its D outputs, summing in a fixed order.
+// index and each accumulates DPT of its outputs, summing in a fixed order. A
+// launch covers the features k0 .. k0 + 4 DPT - 1 (DPT <= 8); larger D takes
+// one launch pair per 32-feature slice.
 template <typename T, int MET, bool COLS, int DPT, bool DG>
 __global__ void __launch_bounds__(256) pair_bwd_tiled(const T* __restrict__ A,
                                                       const T* __restrict__ Bm,
                                                       const T* __restrict__ cost,
                                                       const T* __restrict__ dcost,
-                                                      T* __restrict__ dOut, int R, int C, int D) {
+                                                      T* __restrict__ dOut, int R, int C, int D,
+                                                      int k0) {
   constexpr int TL = 64;
   // row pitch: TL + 1 keeps row-wise and column-wise accesses conflict-free;
   // the diagonal loads (DG) need TL + 2 (a diagonal's cells then fall in
@@ -203,7 +206,7 @@ __global__ void __launch_bounds__(256) pair_bwd_tiled(const T* __restrict__ A,
     }
     for (int e = tid; e < TL * 4 * DPT; e += 256) {
       const int si = e / (4 * DPT), d = e - si * (4 * DPT);
-      op[si][d] = (s0 + si < nstr && d < D) ? other[(size_t)(s0 + si) * D + d] : (T)0;
+      op[si][d] = (s0 + si < nstr && k0 + d < D) ? other[(size_t)(s0 + si) * D + k0 + d] : (T)0;
     }
     __syncthreads();
 #pragma unroll 8
@@ -218,7 +221,7 @@ __global__ void __launch_bounds__(256) pair_bwd_tiled(const T* __restrict__ A,
   if (o < nown) {
 #pragma unroll
     for (int k = 0; k < DPT; ++k) {
-      const int d = dg * DPT + k;
+      const int d = k0 + dg * DPT + k;
       if (d < D) dOut[((size_t)p * nown + o) * D + d] = (T)2 * (sum * self[(size_t)o * D + d] - acc[k]);
     }
   }
@@ -728,16 +731,15 @@ static int pair_cost_bwd_impl(const T* A, const T* Bm, const T* cost, const T* d
       return check_launch(what);
     }
   }
-  // float64 tiles (a pass with 64 features would need 66 KB of static LDS)
-  if (sizeof(T) == 8 && D <= 32) {
-    const int dpt = D <= 4 ? 1 : (D <= 8 ? 2 : (D <= 16 ? 4 : 8));
+  // float64 tiles (a pass with 64 features would need 66 KB of static LDS):
+  // the passes are separable over features, D > 32 runs as 32-feature slices
+  if (sizeof(T) == 8) {
     const dim3 ga((R + 63) / 64, P), gb((C + 63) / 64, P), block(256);
 #define TW_PAIR_TILED(MET_, DPT_)                                                               \
   hipLaunchKernelGGL((pair_bwd_tiled<T, MET_, false, DPT_, DG>), ga, block, 0, s, A, Bm, cost,  \
-                     dcost, dA, R, C, D);                                                       \
+                     dcost, dA, R, C, D, k0);                                                   \
   hipLaunchKernelGGL((pair_bwd_tiled<T, MET_, true, DPT_, DG>), gb, block, 0, s, A, Bm, cost,   \
-                     dcost, \
-                     dB, R, C, D);
+                     dcost, dB, R, C, D, k0);
 #define TW_PAIR_TILED_D(MET_)                      \
   switch (dpt) {                                   \
     case 1: TW_PAIR_TILED(MET_, 1) break;          \
@@ -746,10 +748,14 @@ static int pair_cost_bwd_impl(const T* A, const T* Bm, const T* cost, const T* d
     default: TW_PAIR_TILED(MET_, 8) break;         \
   }
     if constexpr (sizeof(T) == 8) {
-      if (metric == MET_RAW) { TW_PAIR_TILED_D(MET_RAW) }
-      else if constexpr (!DG) {
-        if (metric == MET_SQ) { TW_PAIR_TILED_D(MET_SQ) }
-        else { TW_PAIR_TILED_D(MET_EUC) }
+      for (int k0 = 0; k0 < D; k0 += 32) {
+        const int w = D - k0 < 32 ? D - k0 : 32;
+        const int dpt = w <= 4 ? 1 : (w <= 8 ? 2 : (w <= 16 ? 4 : 8));
+        if (metric == MET_RAW) { TW_PAIR_TILED_D(MET_RAW) }
+        else if constexpr (!DG) {
+          if (metric == MET_SQ) { TW_PAIR_TILED_D(MET_SQ) }
+          else { TW_PAIR_TILED_D(MET_EUC) }
+        }
       }
     }
 #undef TW_PAIR_TILED_D
