@@ -19,7 +19,10 @@ One JSON line is printed with ``roofline`` for the dominant kernel (algorithmic
 bytes per launch / its mean duration, timed with HIP events on the stream the
 kernel runs on) and ``cpu_baseline`` (the CPU oracle, the clean-room
 restatement of the reference's vectorised PyTorch backend, timed on this
-host on a bounded sample). ``--all`` adds one line per config to stderr.
+host on a bounded sample). The metric has two halves; the second, JEANIE
+with two viewpoint axes (K = 25, configs[4]), is measured in the same run and
+reported in the same line as ``config.jeanie_k25`` with its own roofline and
+CPU baseline. ``--all`` adds one line per config to stderr.
 """
 
 import argparse
@@ -199,6 +202,18 @@ def _hip_call_times(name, inputs, iters):
     return best
 
 
+def _roofline(name, inputs, iters):
+    """Roofline record of a config's dominant DP kernel, or None."""
+    kt = _hip_call_times(name, inputs, iters)
+    if kt is None:
+        return None
+    label, kms, nbytes = kt
+    gbs = nbytes / (kms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 5), "traffic": _traffic(label, name),
+            "kernel": label, "kernel_ms": round(kms, 5), "algorithmic_bytes": nbytes}
+
+
 def _traffic(label, name):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
@@ -257,9 +272,21 @@ def cpu_baseline(name, budget_s=10.0):
         if el >= budget_s or n >= 50:
             break
     return {"value": w["cells"] * n / el, "unit": "cells/s", "cores": cores,
-            "kind": "port",
+            "kind": "port", "cpu_model": _cpu_model(),
+            "pairs_per_s": w["pairs"] * n / el,
             "sample": "{}: full batch fwd+bwd x{} in {:.1f} s, fp32, oracle/ on {} threads"
                       .format(name, n, el, cores)}
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 # -------------------------------------------------------------------- main
@@ -350,14 +377,19 @@ def main():
     name = args.config
     mode = "eager" if args.eager else "both"
     inputs, ms, cells_s, pairs_s = run_config(name, args.steps, args.warmup, mode)
-    kt = _hip_call_times(name, inputs, max(args.steps, 10))
-    roof = None
-    if kt is not None:
-        label, kms, nbytes = kt
-        gbs = nbytes / (kms * 1e-3) / 1e9
-        roof = {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gbs / HBM_PEAK_GBS, 5), "traffic": _traffic(label, name),
-                "kernel": label, "kernel_ms": round(kms, 5), "algorithmic_bytes": nbytes}
+    roof = _roofline(name, inputs, max(args.steps, 10))
+    # The metric's second half: JEANIE with two viewpoint axes, K = 25
+    # (configs[4], the 5 x 5 cost fwd+bwd), measured the same way.
+    second = None
+    if name != "cfg5a":
+        j_in, j_ms, j_cells, j_pairs = run_config("cfg5a", args.steps, args.warmup, mode)
+        second = {"workload": "cfg5a", "metric": "JEANIE K=25 fwd+bwd, cells/s",
+                  "value": round(j_cells, 1), "unit": "cells/s", "ms_per_step": round(j_ms, 5),
+                  "pairs_per_s": round(j_pairs, 1), "cells": work("cfg5a")["cells"],
+                  "pairs": work("cfg5a")["pairs"],
+                  "eager_ms_per_step": round(EAGER_MS["cfg5a"], 5),
+                  "roofline": _roofline("cfg5a", j_in, max(args.steps, 10)),
+                  "cpu_baseline": None if args.no_cpu else cpu_baseline("cfg5a", 8.0)}
     line = {
         "metric": METRIC,
         "value": round(cells_s, 1),
@@ -375,7 +407,8 @@ def main():
                    "pairs": work(name)["pairs"],
                    "timing": ("eager steps" if args.eager else
                               "HIP-graph replays of the public-API step (forward, loss, backward)"),
-                   "eager_ms_per_step": round(EAGER_MS[name], 5)},
+                   "eager_ms_per_step": round(EAGER_MS[name], 5),
+                   "jeanie_k25": second},
         "roofline": roof,
         "cpu_baseline": None if args.no_cpu else cpu_baseline(name),
     }

@@ -35,6 +35,10 @@ extern "C" {
 #define TW_EINVAL 1  /* bad argument */
 #define TW_ELAUNCH 2 /* kernel launch failed */
 #define TW_ESIZE 3   /* problem larger than this build handles / workspace too small */
+#define TW_EWAIT 4   /* an earlier launch's bounded cross-workgroup wait gave up */
+
+/* Bits of the per-device asynchronous status word (tw_async_status). */
+#define TW_STATUS_WAIT_GAVE_UP 1u
 
 /* Pairwise metrics (tw_pair_cost_*, tw_jeanie_feat_*). */
 #define TW_METRIC_RAW 0   /* |a|^2 + |b|^2 - 2 a.b, unclamped */
@@ -43,6 +47,22 @@ extern "C" {
 
 int tw_version(void);
 const char* tw_last_error(void);
+
+/* Asynchronous status of the current device. A uDTW sweep split over several
+ * workgroups per pair hands boundary rows between them and waits for each
+ * with a bounded poll; if a wait runs out (the producing workgroup was held
+ * off the GPU for that long) the kernel sets TW_STATUS_WAIT_GAVE_UP in a
+ * per-device word, its outputs become NaN, and it exits normally. This call
+ * synchronises the device, then returns TW_EWAIT if the bit is set (clearing
+ * it when `clear` is non-zero) or TW_OK. It is sticky across calls, like an
+ * asynchronous launch error, and must not be called during stream capture.
+ * No counterpart in the reference: its kernels never wait on each other. */
+int tw_async_status(int clear);
+/* Test hook (no counterpart in the reference): poll limit of those waits
+ * (spins > 0; 0 restores the default) and, with drop_handoff != 0, boundary
+ * rows that are never handed over, so that a test can make a wait give up
+ * while every kernel still exits normally. Process-wide; not for production. */
+void tw_test_set_wait(int spins, int drop_handoff);
 
 /* ---------------------------------------------------------------- uDTW --
  * DP on precomputed matrices, N <= M (callers transpose).

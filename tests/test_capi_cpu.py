@@ -25,14 +25,15 @@ def _declared():
 def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(_hip.LIB_PATH))
     names = _declared()
-    assert len(names) == 32
+    assert len(names) == 34
     for name in names:
         assert hasattr(lib, name), name
     assert lib.tw_version() == 1
 
 
 def test_binding_covers_every_entry_point():
-    bound = {"tw_version", "tw_last_error", "tw_udtw_feat_workspace_bytes"}
+    bound = {"tw_version", "tw_last_error", "tw_udtw_feat_workspace_bytes", "tw_async_status",
+             "tw_test_set_wait"}
     for base in _hip.SIGNATURES:
         bound |= {base + "_f32", base + "_f64"}
     bound |= {base + "_f64" for base in _hip.SIGNATURES_F64}

@@ -81,35 +81,100 @@ def test_cfg1_soft_dtw(dtype):
     _check([d, x.grad], [want[0], want[2]], dtype, "cfg1")
 
 
+# cfg3: the launch is the full batch (64 pairs); the float64 oracle checks
+# the first CFG3_CHECKED of them (each takes ~1.5 s on one CPU thread), with
+# the gradient of the full batch's mean (1/64 per pair).
+CFG3_CHECKED = 8
+
+
+def _cfg3(beta):
+    X, Y, sx, sy = make_inputs("cfg3", dtype=torch.float64)
+    if beta == 0.0:   # soft-DTW: sigma = 1
+        sx, sy = torch.ones_like(sx), torch.ones_like(sy)
+    return X, Y, sx, sy
+
+
+def _cfg3_gpu(X, Y, sx, sy, beta, dtype):
+    if beta == 0.0:
+        x, y = (t.to(DEV, dtype).requires_grad_(True) for t in (X, Y))
+        d = tw.SoftDTW(gamma=0.1)(x, y)
+        d.mean().backward()
+        return [d, torch.zeros_like(d), x.grad, y.grad]
+    got = _udtw_gpu(X, Y, sx, sy, 0.1, beta, dtype)
+    return got[:4]
+
+
+def _cfg3_oracle(X, Y, sx, sy, beta, k):
+    X, Y, sx, sy = (t[:k] for t in (X, Y, sx, sy))
+    vx, vy = sx.squeeze(-1) ** 2, sy.squeeze(-1) ** 2
+    r, p, R, P = OU.features_forward(X, Y, vx, vy, 0.1, beta, 1e-8)
+    g = torch.full((k,), 1.0 / 64, dtype=torch.float64)
+    dX, dY, _, _ = OU.features_backward(X, Y, vx, vy, R, P, g, g if beta else 0 * g, 0.1, beta,
+                                        1e-8)
+    return [r, p if beta else 0 * r, dX, dY]
+
+
+@pytest.mark.parametrize("beta", [1.0, 0.0], ids=["udtw", "soft_dtw"])
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
-def test_cfg3_udtw_long(dtype):
-    """Full N = M = 1024, D = 16, gamma = 0.1 on 4 of the 64 pairs (pairs are
-    independent; the per-pair code path is that of the full batch)."""
-    X, Y, sx, sy = (t[:4] for t in make_inputs("cfg3", dtype=torch.float64))
-    got = _udtw_gpu(X, Y, sx, sy, 0.1, 1.0, dtype)
-    want = _udtw_oracle(X, Y, sx, sy, 0.1, 1.0)
+def test_cfg3_full_batch(dtype, beta):
+    """B = 64, N = M = 1024, D = 16, gamma = 0.1: uDTW (beta = 1, loss
+    mean(d + omega)) and soft-DTW (beta = 0, sigma = 1, loss mean(d)), the
+    forward and backward launched on the whole batch."""
+    torch.set_num_threads(min(16, torch.get_num_threads()))
+    X, Y, sx, sy = _cfg3(beta)
+    got = [t.detach()[:CFG3_CHECKED] for t in _cfg3_gpu(X, Y, sx, sy, beta, dtype)]
+    want = _cfg3_oracle(X, Y, sx, sy, beta, CFG3_CHECKED)
+    errs = [maxnorm_err(a, b) if b.abs().max() > 0 else a.abs().max().item()
+            for a, b in zip(got, want)]
+    print("\ncfg3 {} {}: max-normalised errors (d, omega, dX, dY) {}".format(
+        "uDTW" if beta else "soft-DTW", dtype, ["%.2e" % e for e in errs]))
     if dtype == torch.float64:
-        errs = [maxnorm_err(a, b) for a, b in zip(got, want)]
-        print("\ncfg3 float64: max-normalised errors", ["%.2e" % e for e in errs])
         assert max(errs[:2]) < F64_TOL
-        # Gradients: R reaches ~1.4e5 in units of gamma/log2(e) here, so every
-        # backward weight carries ~3e-11 relative rounding in ANY float64
-        # implementation (the oracle included) and ~2000 chained steps give
-        # ~1e-9; the two independent float64 results agree to that floor.
+        # The two float64 computations each carry their own rounding of the
+        # DP at this scale (R reaches ~2.7e4 with gamma = 0.1): the float64
+        # oracle is ~5e-10 from the extended-precision value
+        # (tests/test_oracle_longdouble.py), and test_cfg3_float64_against_
+        # extended_precision below bounds this kernel's own distance to it.
         assert max(errs[2:]) < 2e-9
     else:
-        errs = [maxnorm_err(a, b) for a, b in zip(got, want)]
-        print("\ncfg3 float32: max-normalised errors", ["%.2e" % e for e in errs])
         assert errs[0] < F32_VALUE_TOL
-        # gamma = 0.1 at N = 1024: R reaches ~1.4e5 (scaled), so float32 holds
-        # it to ~1e-2 absolute; the penalty (a softmax expectation) keeps
-        # ~4e-5 and the gradients a few 1e-2 in any float32 implementation,
-        # and they move with the rounding of the cost itself (summation
-        # order of |x|^2 + |y|^2 - 2 x.y). The reference documents, at
-        # N = 1000 and gamma = 0.1, 1e-2 for its float32 kernel and 0.6 for
-        # its float32 PyTorch backend (docs/limitations.md:31-42).
         assert errs[1] < 1e-4
-        assert max(errs[2:]) < 1e-1
+        # The reference documents 1e-2 for its float32 kernel at N = 1000,
+        # gamma = 0.1 (docs/limitations.md:31-36).
+        assert max(errs[2:]) < CFG3_F32_GRAD_TOL
+
+
+# float32 gradients at cfg3, relative to the largest entry; the measured
+# errors are recorded in the design notes.
+CFG3_F32_GRAD_TOL = 1e-2
+
+
+@pytest.mark.parametrize("beta", [1.0, 0.0], ids=["udtw", "soft_dtw"])
+def test_cfg3_float64_against_extended_precision(beta):
+    """Pair 0 of cfg3 in float64 on the GPU (launched with the full batch)
+    against the same pair in 80-bit extended precision (oracle/udtw_ld.py):
+    the kernel's gradients must be at least as close to the extended-precision
+    value as the float64 oracle's (which follows the reference's algorithm)."""
+    import numpy as np
+    from oracle import udtw_ld
+    X, Y, sx, sy = _cfg3(beta)
+    got = [t.detach()[:1].double().cpu().numpy() for t in
+           _cfg3_gpu(X, Y, sx, sy, beta, torch.float64)]
+    vx, vy = (sx[0, :, 0] ** 2).numpy(), (sy[0, :, 0] ** 2).numpy()
+    r, p, dX, dY, _, _ = udtw_ld.features_value_and_grads(
+        X[0].numpy(), Y[0].numpy(), vx, vy, 0.1, beta, 1e-8, 1.0 / 64, (1.0 / 64) if beta else 0.0)
+    ref = _cfg3_oracle(X, Y, sx, sy, beta, 1)
+
+    def err(a, b):
+        a, b = np.asarray(a, np.longdouble).ravel(), np.asarray(b, np.longdouble).ravel()
+        return float(np.abs(a - b).max() / np.abs(b).max())
+    hip = [err(got[2][0], dX), err(got[3][0], dY)]
+    orc = [err(ref[2][0].numpy(), dX), err(ref[3][0].numpy(), dY)]
+    print("\ncfg3 pair 0 {} float64 vs extended precision: HIP dX, dY {}, float64 oracle {}"
+          .format("uDTW" if beta else "soft-DTW", ["%.2e" % e for e in hip],
+                  ["%.2e" % e for e in orc]))
+    assert err(got[0][0], r) < 1e-13
+    assert max(hip) < max(2 * max(orc), 1e-10)
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])

@@ -61,3 +61,84 @@ def test_one_past_the_longest_raises():
     s1, s2 = torch.ones(1, 16385, 1, device="cuda"), torch.ones(1, 16390, 1, device="cuda")
     with pytest.raises((RuntimeError, ValueError), match="16384"):
         tw.UDTW()(x, y, s1, s2)
+
+
+# ---- batches past 65535 pairs (the cost kernels index pairs in grid.y and
+# launch in chunks; FVM folds the pair into grid.x). Pairs are independent, so
+# the full batch must equal a float64 evaluation, and a slice of it must equal
+# the same pairs computed alone, bit for bit.
+
+BIG = 70000
+
+
+def _maxnorm(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return ((a - b).abs().max() / b.abs().max().clamp_min(1e-300)).item()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_pair_and_rbf_costs_past_65535_pairs(dtype):
+    g = torch.Generator().manual_seed(21)
+    A = torch.randn(BIG, 3, 5, generator=g, dtype=torch.float64)
+    Bm = torch.randn(BIG, 4, 5, generator=g, dtype=torch.float64)
+    tol = 1e-10 if dtype == torch.float64 else 1e-5
+    for fn in (tw.squared_euclidean_cost, tw.rbf_cost):
+        a = A.to("cuda", dtype).requires_grad_(True)
+        b = Bm.to("cuda", dtype).requires_grad_(True)
+        c = fn(a, b)
+        w = torch.linspace(0.5, 1.5, c.numel(), device="cuda", dtype=dtype).view_as(c)
+        (c * w).sum().backward()
+        ar, br = A.clone().requires_grad_(True), Bm.clone().requires_grad_(True)
+        if fn is tw.squared_euclidean_cost:
+            cr = ((ar[:, :, None, :] - br[:, None, :, :]) ** 2).sum(-1)
+        else:
+            cr = (2 - 2 * torch.exp(-0.5 * (ar[:, :, None, :] - br[:, None, :, :]) ** 2)).sum(-1)
+        (cr * w.double().cpu()).sum().backward()
+        for got, want in ((c, cr), (a.grad, ar.grad), (b.grad, br.grad)):
+            assert _maxnorm(got, want) < tol, fn.__name__
+        # the last pairs alone: bitwise the batch's
+        tail = fn(A[-7:].to("cuda", dtype), Bm[-7:].to("cuda", dtype))
+        assert torch.equal(tail, c[-7:].detach())
+
+
+def test_udtw_features_past_65535_pairs_and_normalize_past_21845():
+    g = torch.Generator().manual_seed(22)
+    for B, norm in ((BIG, False), (22000, True)):
+        X = torch.randn(B, 3, 2, generator=g, dtype=torch.float64).cuda()
+        Y = torch.randn(B, 3, 2, generator=g, dtype=torch.float64).cuda()
+        sx = (0.5 + torch.rand(B, 3, 1, generator=g, dtype=torch.float64)).cuda()
+        sy = (0.5 + torch.rand(B, 3, 1, generator=g, dtype=torch.float64)).cuda()
+        m = tw.UDTW(gamma=0.5, beta=1.0, normalize=norm)
+        d, p = m(X, Y, sx, sy)
+        # the same pairs through the materialised-matrix path
+        cost, pen, _ = TF.pairwise_matrices(X, Y, sx, sy, beta=1.0)
+        dc, pc = TF.udtw_from_cost(cost, pen, gamma=0.5)
+        if norm:
+            for A_, S_ in ((X, sx), (Y, sy)):
+                c2, p2, _ = TF.pairwise_matrices(A_, A_, S_, S_, beta=1.0)
+                d2, q2 = TF.udtw_from_cost(c2, p2, gamma=0.5)
+                dc, pc = dc - 0.5 * d2, pc - 0.5 * q2
+        torch.testing.assert_close(d, dc, rtol=1e-10, atol=1e-10)
+        torch.testing.assert_close(p, pc, rtol=1e-10, atol=1e-10)
+        head = m(X[:5], Y[:5], sx[:5], sy[:5])
+        assert torch.equal(head[0], d[:5]) and torch.equal(head[1], p[:5])
+
+
+def test_jeanie_features_and_fvm_past_65535_pairs():
+    g = torch.Generator().manual_seed(23)
+    q = torch.randn(BIG, 2, 3, 4, generator=g, dtype=torch.float64).cuda()
+    s = torch.randn(BIG, 3, 4, generator=g, dtype=torch.float64).cuda()
+    d = TF.jeanie(q, s, gamma=0.3, max_shift=1)
+    dc = TF.jeanie_from_cost(tw.euclidean_cost(q, s), gamma=0.3, max_shift=1)
+    torch.testing.assert_close(d, dc, rtol=1e-10, atol=1e-10)
+    c = torch.rand(BIG, 3, 4, 5, generator=g, dtype=torch.float64).cuda().requires_grad_(True)
+    f = TF.fvm_from_cost(c, gamma=0.2)
+    f.sum().backward()
+    c5 = c[-5:].detach().clone().requires_grad_(True)
+    f5 = TF.fvm_from_cost(c5, gamma=0.2)
+    f5.sum().backward()
+    assert torch.equal(f5, f[-5:].detach()) and torch.equal(c5.grad, c.grad[-5:])
+    from oracle import jeanie as OJ
+    cc = c[-3:].detach().cpu()
+    torch.testing.assert_close(f[-3:].detach().cpu(), OJ.fvm_from_cost(cc, gamma=0.2),
+                               rtol=1e-10, atol=1e-10)

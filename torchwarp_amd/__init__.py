@@ -7,6 +7,7 @@ A drop-in for torchwarp's public API (``src/torchwarp/__init__.py:1-21``):
 """
 
 from . import functional, paths
+from ._hip import check_async_status
 from .jeanie import FVM, JEANIE, euclidean_cost, rbf_cost, squared_euclidean_cost
 from .sdtw import SoftDTW
 from .udtw import UDTW
@@ -15,5 +16,5 @@ __version__ = "0.1.0"
 
 __all__ = [
     "UDTW", "SoftDTW", "JEANIE", "FVM", "euclidean_cost", "squared_euclidean_cost",
-    "rbf_cost", "functional", "paths",
+    "rbf_cost", "functional", "paths", "check_async_status",
 ]

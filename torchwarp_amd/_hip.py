@@ -67,6 +67,10 @@ def _load():
     lib.tw_version.restype = ctypes.c_int
     lib.tw_udtw_feat_workspace_bytes.restype = ctypes.c_size_t
     lib.tw_udtw_feat_workspace_bytes.argtypes = [ctypes.c_int] * 5
+    lib.tw_async_status.restype = ctypes.c_int
+    lib.tw_async_status.argtypes = [ctypes.c_int]
+    lib.tw_test_set_wait.restype = None
+    lib.tw_test_set_wait.argtypes = [ctypes.c_int, ctypes.c_int]
     for base, sig in SIGNATURES.items():
         for suffix, real in (("_f32", ctypes.c_float), ("_f64", ctypes.c_double)):
             fn = getattr(lib, base + suffix)
@@ -134,6 +138,33 @@ def call(base, dtype, *args):
             rc = fn(*cargs, torch._C._cuda_getCurrentRawStream(dev))
     if rc != 0:
         raise RuntimeError("torchwarp_amd: " + _lib.tw_last_error().decode())
+    if _CHECK_ASYNC:
+        check_async_status(dev)
+
+
+# TORCHWARP_CHECK_ASYNC=1: synchronise after every launch and raise at once if
+# a bounded cross-workgroup wait gave up (a debugging mode, like a blocking
+# launch mode; it cannot be used under stream capture).
+_CHECK_ASYNC = os.environ.get("TORCHWARP_CHECK_ASYNC") == "1"
+
+
+def check_async_status(device=None, clear=True):
+    """Synchronise ``device`` (default: the current one) and raise RuntimeError
+    if a uDTW sweep split over several workgroups per pair gave up waiting for
+    a neighbouring workgroup's boundary row since the last check (that call's
+    outputs are NaN). The status is sticky until checked; ``clear`` resets it."""
+    lib = library()
+    if device is None:
+        dev = torch.cuda.current_device()
+    elif isinstance(device, int):
+        dev = device
+    else:
+        dev = torch.device(device).index
+        dev = torch.cuda.current_device() if dev is None else dev
+    with torch.cuda.device(dev):
+        rc = lib.tw_async_status(1 if clear else 0)
+    if rc != 0:
+        raise RuntimeError("torchwarp_amd: " + lib.tw_last_error().decode())
 
 
 def udtw_workspace_elems(B, N, M, D):

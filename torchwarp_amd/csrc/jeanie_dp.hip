@@ -648,9 +648,10 @@ template <typename T, int KU>
 __global__ void __launch_bounds__(256) fvm_softmin_fwd(const T* __restrict__ C, T* __restrict__ tmp,
                                                        int K, int Tn, int Un, int swap, T k,
                                                        T inv_k) {
-  const int b = blockIdx.y;
-  const int cell = blockIdx.x * blockDim.x + threadIdx.x;
-  const int plane = Tn * Un;
+  // workgroup w covers cells (w % bpp) * 256 .. of pair w / bpp
+  const int plane = Tn * Un, bpp = (plane + 255) / 256;
+  const int b = (int)blockIdx.x / bpp;
+  const int cell = ((int)blockIdx.x - b * bpp) * 256 + (int)threadIdx.x;
   if (cell >= plane) return;
   const T* c = C + (size_t)b * K * plane + cell;
   const T INF = inf_v<T>();
@@ -678,9 +679,9 @@ __global__ void __launch_bounds__(256) fvm_softmin_bwd(const T* __restrict__ C,
                                                        const T* __restrict__ dtmp,
                                                        T* __restrict__ dC, int K, int Tn, int Un,
                                                        int swap, T k) {
-  const int b = blockIdx.y;
-  const int cell = blockIdx.x * blockDim.x + threadIdx.x;
-  const int plane = Tn * Un;
+  const int plane = Tn * Un, bpp = (plane + 255) / 256;
+  const int b = (int)blockIdx.x / bpp;
+  const int cell = ((int)blockIdx.x - b * bpp) * 256 + (int)threadIdx.x;
   if (cell >= plane) return;
   const int t = cell / Un, u = cell - t * Un;
   const int o = swap ? u * Tn + t : cell;
@@ -716,7 +717,8 @@ int fvm_fwd(const T* C, int B, int K, int Tn, int Un, double gamma, T* tmp, T* R
   if (!C || !tmp || !R || !out || !pen_scratch) return fail(TW_EINVAL, "%s: null pointer", what);
   const int swap = Tn > Un;
   const T k = (T)(1.4426950408889634 / gamma), inv_k = (T)(gamma * 0.6931471805599453);
-  dim3 grid((Tn * Un + 255) / 256, B);
+  // pair and cell block in grid.x (any batch size)
+  dim3 grid((unsigned)((long long)B * ((Tn * Un + 255) / 256)));
   if (K <= 32)
     hipLaunchKernelGGL((fvm_softmin_fwd<T, 32>), grid, dim3(256), 0, s, C, tmp, K, Tn, Un, swap,
                        k, inv_k);
@@ -742,7 +744,8 @@ int fvm_bwd(const T* C, const T* tmp, const T* R, const T* gout, int B, int K, i
                                    nullptr, s, what))
     return e;
   const T k = (T)(1.4426950408889634 / gamma);
-  dim3 grid((Tn * Un + 255) / 256, B);
+  // pair and cell block in grid.x (any batch size)
+  dim3 grid((unsigned)((long long)B * ((Tn * Un + 255) / 256)));
   if (K <= 32)
     hipLaunchKernelGGL((fvm_softmin_bwd<T, 32>), grid, dim3(256), 0, s, C, tmp, ws, dC, K, Tn, Un,
                        swap, k);

@@ -608,6 +608,8 @@ __global__ void __launch_bounds__(256) pair_bwd_small(const T* __restrict__ A,
 // ------------------------------------------------------------- launchers
 
 static inline unsigned blocks_for(long long n) { return (unsigned)((n + 255) / 256); }
+// Pairs per launch: the launches below put the pair index in grid.y.
+constexpr int kMaxPairsPerLaunch = 65535;
 
 // DG: the cost plane is stored by anti-diagonals (plane_index; raw metric,
 // R <= C), as the uDTW sweeps read it.
@@ -619,11 +621,20 @@ static int pair_cost_fwd_impl(const T* A, const T* Bm, int P, int R, int C, int 
     return fail(TW_EINVAL, "%s: internal: diagonal planes are raw with R <= C", what);
   if (P == 0) return TW_OK;
   if (!A || !Bm || !out) return fail(TW_EINVAL, "%s: null pointer", what);
-  if (P > 65535) return fail(TW_ESIZE, "%s: at most 65535 pairs per call", what);
   if (metric != MET_RAW && metric != MET_SQ && metric != MET_EUC)
     return fail(TW_EINVAL, "%s: unknown metric %d", what, metric);
   if ((long long)R * D >= (1LL << 29) || (long long)C * D >= (1LL << 29))
     return fail(TW_ESIZE, "%s: one pair's block must stay below 2 GiB", what);
+  if (P > kMaxPairsPerLaunch) {
+    // the pair index is grid.y (at most 65535): launch in chunks of pairs
+    for (int p0 = 0; p0 < P; p0 += kMaxPairsPerLaunch) {
+      const int np = P - p0 < kMaxPairsPerLaunch ? P - p0 : kMaxPairsPerLaunch;
+      if (int e = pair_cost_fwd_impl<T, DG>(A + (size_t)p0 * R * D, Bm + (size_t)p0 * C * D, np,
+                                            R, C, D, metric, out + (size_t)p0 * R * C, s, what))
+        return e;
+    }
+    return TW_OK;
+  }
   if (sizeof(T) == 4) {
     // TN column tiles of 16 per wavefront share the A operand
     const int TN = C > 32 ? 4 : (C > 16 ? 2 : 1);
@@ -676,9 +687,20 @@ static int pair_cost_bwd_impl(const T* A, const T* Bm, const T* cost, const T* d
   if (P == 0) return TW_OK;
   if (!A || !Bm || !dcost || !dA || !dB) return fail(TW_EINVAL, "%s: null pointer", what);
   if (metric != MET_RAW && !cost) return fail(TW_EINVAL, "%s: metric needs the cost", what);
-  if (P > 65535) return fail(TW_ESIZE, "%s: at most 65535 pairs per call", what);
   if (metric != MET_RAW && metric != MET_SQ && metric != MET_EUC)
     return fail(TW_EINVAL, "%s: unknown metric %d", what, metric);
+  if (P > kMaxPairsPerLaunch) {
+    // the pair index is grid.y (at most 65535): launch in chunks of pairs
+    for (int p0 = 0; p0 < P; p0 += kMaxPairsPerLaunch) {
+      const int np = P - p0 < kMaxPairsPerLaunch ? P - p0 : kMaxPairsPerLaunch;
+      const size_t oa = (size_t)p0 * R * D, ob = (size_t)p0 * C * D, oc = (size_t)p0 * R * C;
+      if (int e = pair_cost_bwd_impl<T, DG>(A + oa, Bm + ob, cost ? cost + oc : nullptr,
+                                            dcost + oc, np, R, C, D, metric, dA + oa, dB + ob, s,
+                                            what))
+        return e;
+    }
+    return TW_OK;
+  }
   const int cmax = C <= 8 ? 8 : (C <= 16 ? 16 : (C <= 32 ? 32 : (C <= 64 ? 64 : 0)));
   const size_t lds = ((size_t)R * cmax + R + cmax) * sizeof(T);
   if (cmax && lds <= 48 * 1024) {

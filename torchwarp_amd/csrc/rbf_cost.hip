@@ -67,13 +67,14 @@ __global__ void __launch_bounds__(256) rbf_bwd_kernel(const T* __restrict__ A,
 }
 
 static inline unsigned rbf_blocks(long long n) { return (unsigned)((n + 255) / 256); }
+// Pairs per launch: the pair index is grid.y (at most 65535).
+constexpr int kRbfMaxPairs = 65535;
 
 template <typename T>
 static int rbf_check(const T* A, const T* Bm, int P, int R, int C, int D, double sigma,
                      const char* what) {
   if (P < 0 || R < 0 || C < 0 || D < 0) return fail(TW_EINVAL, "%s: bad sizes", what);
   if (!(sigma > 0.0)) return fail(TW_EINVAL, "%s: sigma must be > 0", what);
-  if (P > 65535) return fail(TW_ESIZE, "%s: at most 65535 pairs per call", what);
   if ((long long)R * C > (1LL << 40) || (long long)(R > C ? R : C) * D > (1LL << 40))
     return fail(TW_ESIZE, "%s: plane too large", what);
   if (P > 0 && D > 0 && ((R > 0 && !A) || (C > 0 && !Bm)))
@@ -87,9 +88,14 @@ static int rbf_fwd(const T* A, const T* Bm, int P, int R, int C, int D, T sigma,
   if (int e = rbf_check(A, Bm, P, R, C, D, (double)sigma, what)) return e;
   if (P == 0 || R == 0 || C == 0) return TW_OK;
   if (!out) return fail(TW_EINVAL, "%s: null pointer", what);
-  hipLaunchKernelGGL(rbf_fwd_kernel<T>, dim3(rbf_blocks((long long)R * C), P), dim3(256), 0, s,
-                     A, Bm, out, R, C, D, sigma);
-  return check_launch(what);
+  for (int p0 = 0; p0 < P; p0 += kRbfMaxPairs) {
+    const int np = P - p0 < kRbfMaxPairs ? P - p0 : kRbfMaxPairs;
+    hipLaunchKernelGGL(rbf_fwd_kernel<T>, dim3(rbf_blocks((long long)R * C), np), dim3(256), 0, s,
+                       A + (size_t)p0 * R * D, Bm + (size_t)p0 * C * D, out + (size_t)p0 * R * C,
+                       R, C, D, sigma);
+    if (int e = check_launch(what)) return e;
+  }
+  return TW_OK;
 }
 
 template <typename T>
@@ -100,13 +106,19 @@ static int rbf_bwd(const T* A, const T* Bm, const T* dcost, int P, int R, int C,
   if ((R > 0 && !dA) || (C > 0 && !dB) || ((long long)R * C > 0 && !dcost))
     return fail(TW_EINVAL, "%s: null pointer", what);
   // with no terms to sum (R or C zero) the kernels write zero gradients
-  if (R > 0)
-    hipLaunchKernelGGL((rbf_bwd_kernel<T, false>), dim3(rbf_blocks((long long)R * D), P),
-                       dim3(256), 0, s, A, Bm, dcost, dA, R, C, D, sigma);
-  if (C > 0)
-    hipLaunchKernelGGL((rbf_bwd_kernel<T, true>), dim3(rbf_blocks((long long)C * D), P),
-                       dim3(256), 0, s, A, Bm, dcost, dB, R, C, D, sigma);
-  return check_launch(what);
+  for (int p0 = 0; p0 < P; p0 += kRbfMaxPairs) {
+    const int np = P - p0 < kRbfMaxPairs ? P - p0 : kRbfMaxPairs;
+    const size_t oa = (size_t)p0 * R * D, ob = (size_t)p0 * C * D, oc = (size_t)p0 * R * C;
+    const T* dc = dcost ? dcost + oc : dcost;
+    if (R > 0)
+      hipLaunchKernelGGL((rbf_bwd_kernel<T, false>), dim3(rbf_blocks((long long)R * D), np),
+                         dim3(256), 0, s, A + oa, Bm + ob, dc, dA + oa, R, C, D, sigma);
+    if (C > 0)
+      hipLaunchKernelGGL((rbf_bwd_kernel<T, true>), dim3(rbf_blocks((long long)C * D), np),
+                         dim3(256), 0, s, A + oa, Bm + ob, dc, dB + ob, R, C, D, sigma);
+    if (int e = check_launch(what)) return e;
+  }
+  return TW_OK;
 }
 
 }  // namespace tw

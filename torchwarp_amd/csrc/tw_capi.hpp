@@ -10,6 +10,8 @@
 #define TW_EINVAL 1
 #define TW_ELAUNCH 2
 #define TW_ESIZE 3
+#define TW_EWAIT 4
+#define TW_STATUS_WAIT_GAVE_UP 1u
 
 namespace tw {
 
@@ -19,5 +21,12 @@ int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);
 // Device limits of the current device, queried once per device.
 int max_lds_bytes();
+// Device address of the current device's asynchronous status word (bit
+// TW_STATUS_WAIT_GAVE_UP: a bounded cross-workgroup wait ran out), or null.
+unsigned int* status_word();
+// Poll limit of a cross-workgroup wait (dflt unless a test set one) and the
+// test hook that keeps boundary rows from being handed over.
+int wait_spins(int dflt);
+int wait_drop_handoff();
 
 }  // namespace tw

@@ -80,6 +80,9 @@ struct UdtwArgs {
   T hv1, hv0;    // half variance of an input v: v (hv1 v + hv0)
   int gstride;   // element stride of gr / gp (0: one value for every pair)
   int groups;    // forward with MW: row groups (workgroups) per pair
+  unsigned int* status;   // MW: per-device status word (TW_STATUS_WAIT_GAVE_UP)
+  int spins;              // MW: poll limit of a boundary-row wait
+  int drop_handoff;       // MW test hook: boundary rows are never handed over
 };
 
 // Half of a variance input: 0.5 v, or 0.5 v^2 when the input is a standard
@@ -143,7 +146,10 @@ constexpr int kWindow = 64;          // steps per soffset window (one per lane)
 // diagonals behind g - 1's first wavefront: its last wavefront's lag plus a
 // window and the HBM round trip, so the polls rarely wait. The waited-on
 // workgroup always has the lower index, so in-order dispatch guarantees
-// progress, and every poll loop is bounded by kMwSpins.
+// progress, and every poll loop is bounded by kMwSpins rounds (a test can set
+// fewer). A wait that runs out sets TW_STATUS_WAIT_GAVE_UP in the device's
+// status word and lets the sentinel (a NaN) flow on into the pair's outputs,
+// so the kernel still exits and tw_async_status reports the failure.
 constexpr int kMwRows = 256;
 constexpr int kGroupLag = kLag * (kMwRows / 64) + kWindow + 16;
 constexpr int kMwSpins = 1 << 16;
@@ -241,6 +247,8 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
   const int Dn = N + M - 1;
   // MW: this workgroup's last wavefront publishes its last row (not the last group's)
   const bool publish = MW && grp < G - 1 && wave == nw - 1;
+  // MW test hook: the published row is not stored at all (its wait gives up)
+  const bool drop_row = publish && lane == 63 && a.drop_handoff;
 
   // box[v * kBox + slot]: wavefront v's inbox (the row above its first
   // row; box[nw] is the last wavefront's unread outbox), then the dump area.
@@ -399,7 +407,8 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
         T* const pr = a.R + (size_t)b * NM + diag_soff(dl - 1, N, M) + (rbase - 1);
         T* const pp = PEN ? a.P + (size_t)b * NM + diag_soff(dl - 1, N, M) + (rbase - 1) : pr;
         T vr = INF, vp = (T)0;
-        for (int spin = 0; spin < kMwSpins; ++spin) {
+        int spin = 0;
+        for (; spin < a.spins; ++spin) {
           if (v) {
             vr = __hip_atomic_load(pr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (PEN) vp = __hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -408,6 +417,11 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
           if (__ballot(pend) == 0) break;
           __builtin_amdgcn_s_sleep(4);
         }
+        // The wait ran out: report it (the sentinel, a NaN, then flows into
+        // this pair's outputs) and go on, so the kernel still exits.
+        if (spin == a.spins && lane == 0)
+          __hip_atomic_fetch_or(a.status, TW_STATUS_WAIT_GAVE_UP, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
         win_r = v ? vr : INF;
         win_p = v ? vp : (T)0;
       }
@@ -531,10 +545,10 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
             np[k] = (T)0;
           }
           }
-          const int vo = valid ? vst[k] : kOob;
+          const int vo = (valid && !(MW && drop_row)) ? vst[k] : kOob;
           bR.st(nr[k], vo, so);
           if (PEN) bP.st(np[k], vo, so);
-          if (MW && publish && lane == 63 && valid) {
+          if (MW && publish && lane == 63 && valid && !drop_row) {
             // the next group's row above: a second, agent-coherent store
             const size_t c = (size_t)b * NM + (size_t)((so + vst[k]) / ES);
             __hip_atomic_store(a.R + c, nr[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -580,7 +594,7 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
   if (row0 <= N - 1 && N - 1 < row0 + ROWS) {
     const int so = (int)(NM - 1) * ES;
     const T rl = bR.ld<T>(0, so);
-    a.out_r[b] = rl < INF ? rl * a.inv_k : INF;
+    a.out_r[b] = rl * a.inv_k;   // INF (unreachable) and NaN pass through
     a.out_p[b] = PEN ? bP.ld<T>(0, so) : (T)0;
   }
 }
@@ -1200,6 +1214,10 @@ static int launch_udtw(bool backward, const UdtwArgs<T>& a, int B, hipStream_t s
         mw_enabled(SRC)) {
       UdtwArgs<T> m = a;
       m.groups = G;
+      m.status = status_word();
+      if (!m.status) return fail(TW_ELAUNCH, "%s: no device status word", what);
+      m.spins = wait_spins(kMwSpins);
+      m.drop_handoff = wait_drop_handoff();
       const long long fills = (long long)B * (G - 1) * a.M;
       hipLaunchKernelGGL((mw_fill<T>), dim3((unsigned)((fills + 255) / 256)), dim3(256), 0,
                          stream, m.R, PEN ? m.P : (T*)nullptr, B, a.N, a.M, G);

@@ -6,24 +6,20 @@ from .functional import _BACKENDS, _check_hyperparameters, udtw
 
 
 class UDTW(nn.Module):
-    """Uncertainty-DTW module; see ``torchwarp_amd.functional.udtw``.
+    """Module form of ``torchwarp_amd.functional.udtw`` with its settings fixed.
 
-    Args:
-        gamma: SoftMin temperature (> 0).
-        beta: Penalty weight (>= 0).
-        normalize: If True, return d(X,Y) - 0.5 [d(X,X) + d(Y,Y)] for both the
-            distance and the penalty.
-        bandwidth: Sakoe-Chiba band; None or 0 disables pruning.
-        method: "gemm" (default: cost built inside the fused kernel) or
-            "diff" (materialised [B,N,M] matrices).
-        backend: "auto" or "cuda".
+    Constructor settings: ``gamma`` is the soft-minimum temperature (positive);
+    ``beta`` weighs the uncertainty penalty (non-negative); ``normalize``
+    subtracts half of the two self-alignments, d(X,Y) - [d(X,X) + d(Y,Y)] / 2,
+    from both outputs; ``bandwidth`` restricts paths to |i - j| <= bandwidth
+    (None or 0: no restriction); ``method`` chooses between building the
+    cost inside the HIP kernels ("gemm") and materialising the [B, N, M]
+    cost and penalty first ("diff"); ``backend`` is "auto" or "cuda".
 
-    Forward:
-        X, Y: [B,N,D], [B,M,D]
-        sigma_x, sigma_y: [B,N,1], [B,M,1] positive standard deviations.
-
-    Returns:
-        UDTWOutput(distance [B], penalty [B]); the penalty is beta-weighted.
+    Calling the module on sequences X [B, N, D], Y [B, M, D] and their
+    per-step standard deviations sigma_x [B, N, 1], sigma_y [B, M, 1]
+    returns ``UDTWOutput(distance, penalty)``, two [B] tensors, the penalty
+    already multiplied by beta.
     """
 
     def __init__(self, gamma=1.0, beta=1.0, normalize=False, bandwidth=None, *,
