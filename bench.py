@@ -155,15 +155,18 @@ def _hip_call_times(name, inputs, iters):
         B, N, D = X.shape
         M = Y.shape[1]
         pen = beta != 0
-        R = X.new_empty(B, N * M)
+        R = X.new_empty(B, _hip.carry_cols(N, M, gamma, X.dtype))
         P = X.new_empty(B, N * M) if pen else None
         o1, o2 = X.new_empty(B), X.new_empty(B)
-        nws = _hip.udtw_workspace_elems(B, N, M, D)
+        nws = _hip.udtw_workspace_elems(B, N, M, D, X.dtype)
         ws = X.new_empty(nws) if nws else None
         wsb = 0 if ws is None else nws * 4
         g = torch.full((B,), 1.0 / B, device=dev)
         dX, dY, dvx, dvy = [torch.empty_like(t) for t in (X, Y, vx, vy)]
         io = 4 * (X.numel() + Y.numel() + vx.numel() + vy.numel())
+        # R and P at 4 B/cell each (fp32); where the kernels keep R in double
+        # precision (long sequences, small gamma) its extra 4 B/cell count as
+        # overhead, not as algorithmic bytes
         carried = 4 * B * N * M * (2 if pen else 1)
         calls.append(("udtw_fwd", lambda: _hip.call(
             "tw_udtw_feat_fwd", f32, X, Y, vx, vy, B, N, M, D, gamma, beta, 1e-8, 0.0, 1, R, P,

@@ -12,8 +12,9 @@
  *    (thread-local). B = 0 is a no-op returning TW_OK.
  *  - _f32 and _f64 variants compute in float / double.
  *  - "R" and "P" buffers of the uDTW functions are internal tensors carried
- *    from a forward call to the matching backward call ([B, N*M], opaque
- *    layout). The JEANIE "R" is the accumulator in the cost's own layout.
+ *    from a forward call to the matching backward call (opaque layout; P is
+ *    [B, N*M] elements, R takes tw_udtw_carry_bytes bytes). The JEANIE "R"
+ *    is the accumulator in the cost's own layout.
  *
  * Citations (file:line) are into the reference torchwarp sources
  * (src/torchwarp/...): each entry point replaces the named pybind function
@@ -50,30 +51,55 @@ const char* tw_last_error(void);
 
 /* Asynchronous status of the current device. A uDTW sweep split over several
  * workgroups per pair hands boundary rows between them and waits for each
- * with a bounded poll; if a wait runs out (the producing workgroup was held
- * off the GPU for that long) the kernel sets TW_STATUS_WAIT_GAVE_UP in a
- * per-device word, its outputs become NaN, and it exits normally. This call
+ * with a poll bounded in time (2 s on the device's real-time counter); if a
+ * wait runs out (the producing workgroup was held off the GPU for that long)
+ * the kernel sets TW_STATUS_WAIT_GAVE_UP in a per-device word, its outputs
+ * become NaN, and it exits normally. This call
  * synchronises the device, then returns TW_EWAIT if the bit is set (clearing
  * it when `clear` is non-zero) or TW_OK. It is sticky across calls, like an
  * asynchronous launch error, and must not be called during stream capture.
  * No counterpart in the reference: its kernels never wait on each other. */
 int tw_async_status(int clear);
-/* Test hook (no counterpart in the reference): poll limit of those waits
- * (spins > 0; 0 restores the default) and, with drop_handoff != 0, boundary
+/* Test hook (no counterpart in the reference): a limit of `spins` poll rounds
+ * for those waits (spins > 0; 0 restores the time bound alone) and, with
+ * drop_handoff != 0, boundary
  * rows that are never handed over, so that a test can make a wait give up
  * while every kernel still exits normally. Process-wide; not for production. */
 void tw_test_set_wait(int spins, int drop_handoff);
+/* Test hook (no counterpart in the reference): how uDTW splits a pair over
+ * workgroups, overriding TORCHWARP_UDTW_MW: 0 one workgroup per pair (then
+ * at most 1024 rows in float, 512 in double), 1 several workgroups whenever a
+ * pair has more than 256 rows, 2 the default (several workgroups for
+ * sequences longer than one workgroup holds, and for small batches in the
+ * forward), -1 back to the environment's choice. Process-wide; sizes queried
+ * before a change do not apply after it. Not for production. */
+void tw_test_set_mw(int mode);
 
 /* ---------------------------------------------------------------- uDTW --
- * DP on precomputed matrices, N <= M (callers transpose).
+ * Bytes of the R buffer a uDTW forward fills and the matching backward reads,
+ * for B pairs of N x M (N <= M) at this gamma: B*N*M*elem_size, except that
+ * _f32 calls keep R in double precision (B*N*M*8 bytes) when the accumulated
+ * cost can grow large against float32's spacing ((N + M - 1) log2(e) / gamma
+ * above 2048, one row per thread serving N, the double plane below 2 GiB). No counterpart in the reference,
+ * whose float32 kernels keep R in float32. Host only. */
+size_t tw_udtw_carry_bytes(int B, int N, int M, double gamma, int elem_size);
+
+/* DP on precomputed matrices, N <= M (callers transpose).
  * Replaces udtw_cuda.cu:624-657 (forward) / :659-690 (backward) and the ops
  * torchwarp_udtw::dp / dp_backward (udtw/_ops.py:100-138).
  * cost, pen: [B,N,M]; pen may be NULL (zero penalty, P unused).
- * R, P: [B, N*M] internal; out_dist, out_pen: [B].
+ * R: tw_udtw_carry_bytes(B, N, M, gamma, elem) bytes, P: [B, N*M], internal;
+ * out_dist, out_pen: [B].
  * Backward: the forward's bandwidth; grad_dist, grad_pen [B] (grad_pen may be
  * NULL iff pen is NULL), read with element stride grad_stride (1, or 0 for one
  * value shared by every pair, e.g. the expanded gradient of a mean);
- * d_cost, d_pen [B,N,M] (d_pen may be NULL). */
+ * d_cost, d_pen [B,N,M] (d_pen may be NULL); workspace of
+ * tw_udtw_cost_workspace_bytes(...) bytes (NULL when that is 0): sequences
+ * longer than one workgroup holds (N > 1024 in float, 512 in double) run with
+ * several workgroups per pair, which hand boundary records to each other
+ * through it. There is no length limit beyond the 2 GiB of one pair's N*M
+ * planes (32-bit offsets within a pair). */
+size_t tw_udtw_cost_workspace_bytes(int B, int N, int M, int elem_size);
 int tw_udtw_cost_fwd_f32(const float* cost, const float* pen, int B, int N, int M, float gamma,
                          float bandwidth, float* R, float* P, float* out_dist, float* out_pen,
                          hipStream_t stream);
@@ -83,11 +109,13 @@ int tw_udtw_cost_fwd_f64(const double* cost, const double* pen, int B, int N, in
 int tw_udtw_cost_bwd_f32(const float* cost, const float* pen, const float* R, const float* P,
                          const float* grad_dist, const float* grad_pen, int B, int N, int M,
                          float gamma, float bandwidth, int grad_stride, float* d_cost,
-                         float* d_pen, hipStream_t stream);
+                         float* d_pen, float* workspace, size_t workspace_bytes,
+                         hipStream_t stream);
 int tw_udtw_cost_bwd_f64(const double* cost, const double* pen, const double* R,
                          const double* P, const double* grad_dist, const double* grad_pen, int B,
                          int N, int M, double gamma, double bandwidth, int grad_stride,
-                         double* d_cost, double* d_pen, hipStream_t stream);
+                         double* d_cost, double* d_pen, double* workspace,
+                         size_t workspace_bytes, hipStream_t stream);
 
 /* uDTW straight from the features, N <= M. Replaces udtw_cuda.cu:738-775
  * (fused_forward) / :777-814 (fused_backward) together with the bmm / vecdot /
@@ -97,8 +125,14 @@ int tw_udtw_cost_bwd_f64(const double* cost, const double* pen, const double* R,
  * kernels square them; this folds the reference's sigma.pow(2) of
  * udtw/functional.py:157-158 and its backward into the call).
  * beta == 0 (soft-DTW) skips the penalty: P may be NULL, out_pen gets 0.
- * D == 1 runs fully fused; D > 1 needs workspace of
- * tw_udtw_feat_workspace_bytes(...) bytes. Backward: grad_dist / grad_pen
+ * R: tw_udtw_carry_bytes(B, N, M, gamma, elem) bytes, P: [B, N*M], internal.
+ * D == 1 runs fully fused; the forward with D > 1 needs workspace of
+ * B*N*M elements (the squared distances), the backward
+ * tw_udtw_feat_workspace_bytes(...) bytes: those squared distances (D > 1),
+ * then, for sequences longer than one workgroup holds (N > 1024 in float, 512
+ * in double; several workgroups per pair), their boundary hand-off records.
+ * There is no length limit beyond the 2 GiB of one pair's N*M planes.
+ * Backward: grad_dist / grad_pen
  * with element stride grad_stride (1, or 0: one shared value); writes
  * dX [B,N,D], dY [B,M,D] and, unless both are NULL, dvx [B,N], dvy [B,M]
  * (gradients with respect to vx, vy as given: d sigma when sigma != 0).
@@ -179,7 +213,10 @@ int tw_jeanie_feat_bwd_f64(const double* query, const double* support, const dou
  * fvm_from_cost (jeanie/fvm.py:15-38: logsumexp over the viewpoints, then
  * soft_dtw_from_cost, sdtw.py:29-47) on cost [B, K, T, U], K = product of
  * the viewpoint dims. temporal: [B, T*U] (saved), R: [B, T*U] internal,
- * out [B], scratch [B]. Backward workspace: B*T*U elements. */
+ * out [B], scratch [B]. Backward workspace: tw_fvm_workspace_bytes(...)
+ * bytes (B*T*U elements, plus the hand-off records of the soft-DTW backward
+ * when min(T, U) is longer than one workgroup holds). */
+size_t tw_fvm_workspace_bytes(int B, int K, int T, int U, int elem_size);
 int tw_fvm_cost_fwd_f32(const float* cost, int B, int K, int T, int U, float gamma,
                         float* temporal, float* R, float* out, float* scratch,
                         hipStream_t stream);
@@ -188,10 +225,12 @@ int tw_fvm_cost_fwd_f64(const double* cost, int B, int K, int T, int U, double g
                         hipStream_t stream);
 int tw_fvm_cost_bwd_f32(const float* cost, const float* temporal, const float* R,
                         const float* grad_out, int B, int K, int T, int U, float gamma,
-                        float* d_cost, float* workspace, hipStream_t stream);
+                        float* d_cost, float* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
 int tw_fvm_cost_bwd_f64(const double* cost, const double* temporal, const double* R,
                         const double* grad_out, int B, int K, int T, int U, double gamma,
-                        double* d_cost, double* workspace, hipStream_t stream);
+                        double* d_cost, double* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
 
 /* ------------------------------------------------------- pairwise cost --
  * A [P, R, D] against Bm [P, C, D] -> cost [P, R, C] with a TW_METRIC_*.

@@ -25,7 +25,7 @@ def _declared():
 def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(_hip.LIB_PATH))
     names = _declared()
-    assert len(names) == 34
+    assert len(names) == 38
     for name in names:
         assert hasattr(lib, name), name
     assert lib.tw_version() == 1
@@ -33,7 +33,8 @@ def test_library_exports_every_declared_symbol():
 
 def test_binding_covers_every_entry_point():
     bound = {"tw_version", "tw_last_error", "tw_udtw_feat_workspace_bytes", "tw_async_status",
-             "tw_test_set_wait"}
+             "tw_test_set_wait", "tw_udtw_carry_bytes",
+             "tw_udtw_cost_workspace_bytes", "tw_test_set_mw", "tw_fvm_workspace_bytes"}
     for base in _hip.SIGNATURES:
         bound |= {base + "_f32", base + "_f64"}
     bound |= {base + "_f64" for base in _hip.SIGNATURES_F64}
@@ -44,6 +45,20 @@ def test_workspace_query_is_host_only():
     lib = _hip.library()
     assert lib.tw_udtw_feat_workspace_bytes(2, 3, 4, 1, 4) == 0
     assert lib.tw_udtw_feat_workspace_bytes(2, 3, 4, 5, 4) == 2 * 3 * 4 * 4
+    # past 1024 rows (float; 512 in double) the backward runs ceil(N / 256)
+    # workgroups per pair and hands boundary records (4 float / 6 double words
+    # of 8 bytes per column) across the G - 1 group boundaries
+    assert lib.tw_udtw_feat_workspace_bytes(1, 2000, 2100, 1, 4) == 7 * 2100 * 4 * 8
+    assert lib.tw_udtw_feat_workspace_bytes(2, 2000, 2100, 5, 4) == \
+        2 * 2000 * 2100 * 4 + 2 * 7 * 2100 * 4 * 8
+    assert lib.tw_udtw_feat_workspace_bytes(1, 600, 700, 1, 8) == 2 * 700 * 6 * 8
+    assert lib.tw_udtw_cost_workspace_bytes(3, 1025, 1100, 4) == 3 * 4 * 1100 * 4 * 8
+    assert lib.tw_udtw_cost_workspace_bytes(3, 1100, 1025, 4) == 3 * 4 * 1100 * 4 * 8
+    # up to 1024 rows, pairs split over workgroups only when the batch has
+    # fewer pairs than the device has CUs (256 assumed without a device)
+    assert lib.tw_udtw_cost_workspace_bytes(3, 1024, 1100, 4) == 3 * 3 * 1100 * 4 * 8
+    assert lib.tw_udtw_cost_workspace_bytes(300, 1024, 1100, 4) == 0
+    assert lib.tw_udtw_cost_workspace_bytes(3, 256, 1100, 4) == 0
 
 
 def test_cpu_tensors_fail_loudly():
@@ -149,3 +164,20 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert b"bad sizes" in lib.tw_last_error()
     h = lib.tw_rbf_cost_bwd_f64
     assert h(None, None, None, 2, -1, 3, 4, 0.5, None, None, None) == 1
+
+
+def test_carry_bytes_query():
+    """R is carried in the compute type, except float32 calls on long
+    sequences at a small gamma, which keep R in double precision."""
+    lib = _hip.library()
+    q = lib.tw_udtw_carry_bytes
+    assert q(256, 140, 140, 1.0, 4) == 256 * 140 * 140 * 4        # cfg2: float32 R
+    assert q(64, 1024, 1024, 0.1, 4) == 64 * 1024 * 1024 * 8      # cfg3: double R
+    assert q(64, 1024, 1024, 0.1, 8) == 64 * 1024 * 1024 * 8      # float64 anyway
+    assert q(1, 2000, 2000, 0.1, 4) == 2000 * 2000 * 8            # several workgroups per pair
+    assert q(1, 2000, 2000, 1.0, 4) == 2000 * 2000 * 8
+    assert q(1, 700, 700, 1.0, 4) == 700 * 700 * 4               # scale 2016: float32 R
+    assert q(1, 720, 720, 1.0, 4) == 720 * 720 * 8               # scale 2076: double R
+    assert q(0, 5, 5, 1.0, 4) == 0
+    assert _hip.carry_cols(1024, 1024, 0.1, torch.float32) == 2 * 1024 * 1024
+    assert _hip.carry_cols(140, 140, 1.0, torch.float32) == 140 * 140

@@ -144,9 +144,10 @@ def test_cfg3_full_batch(dtype, beta):
         assert max(errs[2:]) < CFG3_F32_GRAD_TOL
 
 
-# float32 gradients at cfg3, relative to the largest entry; the measured
-# errors are recorded in the design notes.
-CFG3_F32_GRAD_TOL = 1e-2
+# float32 gradients at cfg3, relative to the largest entry: measured 1.1e-3
+# (uDTW) and 1.3e-5 (soft-DTW) with R carried in double precision (5e-2 and
+# 2.8e-2 with float32 R); the gate is about 3x the measured uDTW error.
+CFG3_F32_GRAD_TOL = 3e-3
 
 
 @pytest.mark.parametrize("beta", [1.0, 0.0], ids=["udtw", "soft_dtw"])

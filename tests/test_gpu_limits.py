@@ -1,8 +1,8 @@
-"""Edge sizes: an empty batch, the longest sequences this build takes, one past.
+"""Edge sizes: an empty batch, long sequences, planes past 2 GiB, large batches.
 
 The longest case is beyond what the float64 oracle finishes in seconds, so it
 is checked by a size-independent property: the fused feature path (one
-kernel family, 16 rows per thread) and the cost path on the materialised
+kernel family, 64 workgroups per pair) and the cost path on the materialised
 matrices (another kernel family) must agree, and swapping the sequences
 must not change the result.
 """
@@ -56,11 +56,13 @@ def test_longest_sequences_agree_across_kernel_families():
     torch.testing.assert_close(p1, p3, rtol=1e-4, atol=1e-3)
 
 
-def test_one_past_the_longest_raises():
-    x, y = torch.rand(1, 16385, 1, device="cuda"), torch.rand(1, 16390, 1, device="cuda")
-    s1, s2 = torch.ones(1, 16385, 1, device="cuda"), torch.ones(1, 16390, 1, device="cuda")
-    with pytest.raises((RuntimeError, ValueError), match="16384"):
-        tw.UDTW()(x, y, s1, s2)
+def test_planes_past_2_gib_raise_value_error():
+    """No length limit, but one pair's N x M planes are addressed with 32-bit
+    byte offsets: 23200 x 23200 in float32 (2.15e9 bytes) is one past."""
+    x, y = torch.rand(1, 23200, 1, device="cuda"), torch.rand(1, 23200, 1, device="cuda")
+    s1 = torch.ones(1, 23200, 1, device="cuda")
+    with pytest.raises(ValueError, match="below 2 GiB"):
+        tw.UDTW()(x, y, s1, s1)
 
 
 # ---- batches past 65535 pairs (the cost kernels index pairs in grid.y and

@@ -79,7 +79,12 @@ def test_udtw_cost_layouts(NM, dtype):
         assert max(errs) < 1e-9, errs
     else:
         assert max(errs[:2]) < 1e-5, errs
-        assert max(errs[2:]) < 2e-3, errs
+        # d cost carries the penalty coupling -Pbar (P_k - A_s) / gamma: P
+        # accumulates ~N + M penalties with float32 softmax weights, so each P
+        # is off by ~1e-7 |P|, and differences of P divided by gamma reach the
+        # cost gradient (measured 2.1e-3 at 700 x 650, gamma 0.5, penalty
+        # weight 3; 2.3e-5 without the penalty). R is kept in double here.
+        assert max(errs[2:]) < 3e-3, errs
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
@@ -91,9 +96,10 @@ def test_feat_bwd_with_and_without_forward_plane(dtype):
     g = torch.Generator().manual_seed(8)
     X, Y = (torch.randn(B, L, D, generator=g, dtype=dtype).cuda() for L in (N, M))
     vx, vy = (0.5 + torch.rand(B, L, generator=g, dtype=dtype).cuda() for L in (N, M))
-    R, P = X.new_empty(B, N * M), X.new_empty(B, N * M)
+    R = X.new_empty(B, _hip.carry_cols(N, M, 0.7, dtype))
+    P = X.new_empty(B, N * M)
     o1, o2 = X.new_empty(B), X.new_empty(B)
-    nws = _hip.udtw_workspace_elems(B, N, M, D)
+    nws = _hip.udtw_workspace_elems(B, N, M, D, dtype)
     wsb = nws * X.element_size()
     S = X.new_empty(nws)
     _hip.call("tw_udtw_feat_fwd", dtype, X, Y, vx, vy, B, N, M, D, 0.7, 1.0, 1e-8, 0.0, 1,
@@ -177,3 +183,60 @@ def test_udtw_many_groups_and_large_batch(B, N, M):
     errs = [_maxnorm(a, b) for a, b in zip([d, p] + [t.grad for t in xs],
                                            [rd, rp] + [t.grad for t in ref])]
     assert max(errs) < 1e-9, errs
+
+
+# float32 with R carried in double precision: long sequences at a small gamma
+# ((N + M - 1) log2(e) / gamma > 2048). Every one-row layout: LDS columns
+# (N <= 256), columns by DPP with several workgroups per pair in the forward,
+# the squared-distance plane (D > 1) and the precomputed-cost path. Without
+# double R these shapes carry 1e-2 .. 5e-2 relative gradient error.
+RD_SHAPES = [  # (B, N, M, D, gamma)
+    (2, 200, 230, 1, 0.05),
+    (1, 700, 720, 1, 0.05),
+    (2, 300, 320, 4, 0.05),
+]
+
+
+@pytest.mark.parametrize("shape", RD_SHAPES, ids=lambda s: "B{}N{}M{}D{}".format(*s[:4]))
+def test_float32_with_double_r_matches_float64(shape):
+    from torchwarp_amd import _hip
+    B, N, M, D, gamma = shape
+    assert _hip.carry_cols(N, M, gamma, torch.float32) == 2 * N * M
+    g = torch.Generator().manual_seed(9)
+    X = torch.randn(B, N, D, generator=g, dtype=torch.float64)
+    Y = torch.randn(B, M, D, generator=g, dtype=torch.float64)
+    sx = 0.5 + torch.rand(B, N, 1, generator=g, dtype=torch.float64)
+    sy = 0.5 + torch.rand(B, M, 1, generator=g, dtype=torch.float64)
+    xs = [t.to("cuda", torch.float32).requires_grad_(True) for t in (X, Y, sx, sy)]
+    d, p = tw.UDTW(gamma=gamma, beta=1.0)(*xs)
+    (d + p).sum().backward()
+    ref = [t.clone().requires_grad_(True) for t in (X, Y, sx, sy)]
+    rd, rp = OU.udtw(*ref, gamma=gamma, beta=1.0)
+    (rd + rp).sum().backward()
+    errs = [_maxnorm(a, b) for a, b in zip([d, p] + [t.grad for t in xs],
+                                            [rd, rp] + [t.grad for t in ref])]
+    print("\nfloat32, double R, {}: errors {}".format(shape, ["%.2e" % e for e in errs]))
+    assert max(errs[:2]) < 1e-5, errs
+    # feature gradients measured 3e-5 .. 5e-4; the sigma gradients carry the
+    # penalty coupling through float32 P (measured up to 1.1e-3)
+    assert max(errs[2:4]) < 1e-3, errs
+    assert max(errs[4:]) < 2e-3, errs
+
+
+def test_float32_cost_path_with_double_r_matches_float64():
+    g = torch.Generator().manual_seed(10)
+    C = 3.0 * torch.rand(2, 500, 520, generator=g, dtype=torch.float64)
+    Q = 0.5 * torch.rand(2, 500, 520, generator=g, dtype=torch.float64)
+    c, q = (t.to("cuda", torch.float32).requires_grad_(True) for t in (C, Q))
+    d, p = TF.udtw_from_cost(c, q, gamma=0.05)
+    (d + p).sum().backward()
+    cr, qr = C.clone().requires_grad_(True), Q.clone().requires_grad_(True)
+    rd, rp = OU.udtw_from_cost(cr, qr, gamma=0.05)
+    (rd + rp).sum().backward()
+    errs = [_maxnorm(a, b) for a, b in zip([d, p, c.grad, q.grad], [rd, rp, cr.grad, qr.grad])]
+    print("\nfloat32 cost path, double R: errors", ["%.2e" % e for e in errs])
+    assert max(errs[:2]) < 1e-5, errs
+    # d penalty measured 2e-6; d cost carries the penalty coupling through
+    # float32 P (measured 1.1e-3)
+    assert errs[3] < 1e-4, errs
+    assert errs[2] < 2e-3, errs

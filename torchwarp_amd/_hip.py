@@ -19,7 +19,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libtorchwarp_hip.so"
 # z size_t, s stream
 SIGNATURES = {
     "tw_udtw_cost_fwd": "ppiiiffpppps",
-    "tw_udtw_cost_bwd": "ppppppiiiffipps",
+    "tw_udtw_cost_bwd": "ppppppiiiffipppzs",
     "tw_udtw_feat_fwd": "ppppiiiiffffipppppzs",
     "tw_udtw_feat_bwd": "ppppppppiiiiffffiippppppzs",
     "tw_jeanie_cost_fwd": "piiiiiiiifpps",
@@ -27,7 +27,7 @@ SIGNATURES = {
     "tw_jeanie_feat_fwd": "ppiiiiiiiifippps",
     "tw_jeanie_feat_bwd": "ppppppiiiiiiiifippps",
     "tw_fvm_cost_fwd": "piiiifpppps",
-    "tw_fvm_cost_bwd": "ppppiiiifpps",
+    "tw_fvm_cost_bwd": "ppppiiiifppzs",
     "tw_pair_cost_fwd": "ppiiiiips",
     "tw_pair_cost_bwd": "ppppiiiiipps",
     "tw_rbf_cost_fwd": "ppiiiifps",
@@ -67,10 +67,19 @@ def _load():
     lib.tw_version.restype = ctypes.c_int
     lib.tw_udtw_feat_workspace_bytes.restype = ctypes.c_size_t
     lib.tw_udtw_feat_workspace_bytes.argtypes = [ctypes.c_int] * 5
+    lib.tw_fvm_workspace_bytes.restype = ctypes.c_size_t
+    lib.tw_fvm_workspace_bytes.argtypes = [ctypes.c_int] * 5
+    lib.tw_udtw_cost_workspace_bytes.restype = ctypes.c_size_t
+    lib.tw_udtw_cost_workspace_bytes.argtypes = [ctypes.c_int] * 4
+    lib.tw_udtw_carry_bytes.restype = ctypes.c_size_t
+    lib.tw_udtw_carry_bytes.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_double, ctypes.c_int]
     lib.tw_async_status.restype = ctypes.c_int
     lib.tw_async_status.argtypes = [ctypes.c_int]
     lib.tw_test_set_wait.restype = None
     lib.tw_test_set_wait.argtypes = [ctypes.c_int, ctypes.c_int]
+    lib.tw_test_set_mw.restype = None
+    lib.tw_test_set_mw.argtypes = [ctypes.c_int]
     for base, sig in SIGNATURES.items():
         for suffix, real in (("_f32", ctypes.c_float), ("_f64", ctypes.c_double)):
             fn = getattr(lib, base + suffix)
@@ -167,10 +176,41 @@ def check_async_status(device=None, clear=True):
         raise RuntimeError("torchwarp_amd: " + lib.tw_last_error().decode())
 
 
-def udtw_workspace_elems(B, N, M, D):
-    if D <= 1:
-        return 0
-    return library().tw_udtw_feat_workspace_bytes(B, N, M, D, 1)
+def carry_cols(N, M, gamma, dtype):
+    """Columns of the [B, cols] tensor (of ``dtype``) that holds the uDTW
+    forward's R for the backward: N * M, or 2 * N * M for float32 when the
+    kernels keep R in double precision (long sequences at a small gamma)."""
+    es = 4 if dtype == torch.float32 else 8
+    nbytes = library().tw_udtw_carry_bytes(1, N, M, float(gamma), es)
+    return nbytes // es
+
+
+def check_udtw_plane(N, M, gamma, dtype):
+    """The kernels address one pair's N x M planes with 32-bit byte offsets;
+    past that size raise ValueError, as the reference does for its kernels'
+    size limit (udtw/_ops.py:45-50). There is no limit on the length itself."""
+    es = 4 if dtype == torch.float32 else 8
+    nbytes = max(carry_cols(N, M, gamma, dtype), N * M) * es
+    if nbytes >= 1 << 31:
+        raise ValueError(
+            "uDTW: one pair's {} x {} dynamic-programming plane takes {} bytes; the HIP kernels "
+            "handle planes below 2 GiB (2^29 cells in float32, 2^28 in float64). Shorten or "
+            "downsample the sequences.".format(N, M, nbytes))
+
+
+def udtw_workspace_elems(B, N, M, D, dtype=torch.float32):
+    """Elements (of ``dtype``) of the workspace a feature-path uDTW backward
+    needs: the squared-distance plane for D > 1 and, for sequences longer
+    than one workgroup holds, the hand-off records between workgroups."""
+    es = 4 if dtype == torch.float32 else 8
+    return -(-library().tw_udtw_feat_workspace_bytes(B, N, M, D, es) // es)
+
+
+def udtw_cost_workspace_elems(B, N, M, dtype=torch.float32):
+    """Elements (of ``dtype``) of the workspace a cost-path uDTW backward needs
+    (the hand-off records between workgroups of long sequences; 0 otherwise)."""
+    es = 4 if dtype == torch.float32 else 8
+    return -(-library().tw_udtw_cost_workspace_bytes(B, N, M, es) // es)
 
 
 def dense(dtype, *tensors, contiguous=True):

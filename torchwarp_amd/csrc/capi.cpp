@@ -12,6 +12,10 @@ namespace {
 thread_local std::string g_last_error;
 std::once_flag g_lds_once[64];
 int g_lds_bytes[64];
+std::once_flag g_clk_once[64];
+int g_clk_khz[64];
+std::once_flag g_cu_once[64];
+int g_cus[64];
 }  // namespace
 
 namespace tw {
@@ -46,6 +50,31 @@ int max_lds_bytes() {
     g_lds_bytes[dev] = v;
   });
   return g_lds_bytes[dev];
+}
+
+int num_cus() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::call_once(g_cu_once[dev], [dev] {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        v <= 0)
+      v = 256;
+    g_cus[dev] = v;
+  });
+  return g_cus[dev];
+}
+
+double realtime_khz() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 100000.0;
+  std::call_once(g_clk_once[dev], [dev] {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeWallClockRate, dev) != hipSuccess || v <= 0)
+      v = 100000;   // 100 MHz
+    g_clk_khz[dev] = v;
+  });
+  return (double)g_clk_khz[dev];
 }
 
 }  // namespace tw

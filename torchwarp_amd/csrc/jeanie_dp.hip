@@ -705,8 +705,21 @@ int udtw_cost_fwd_any(const T* C, const T* Q, int B, int N, int M, double gamma,
                       T* R, T* P, T* out_r, T* out_p, hipStream_t s, const char* what);
 template <typename T>
 int udtw_cost_bwd_any(const T* C, const T* Q, const T* R, const T* P, const T* gr, const T* gp,
-                      int B, int N, int M, double gamma, T* dC, T* dQ, hipStream_t s,
-                      const char* what);
+                      int B, int N, int M, double gamma, T* dC, T* dQ, T* ws, size_t ws_bytes,
+                      hipStream_t s, const char* what);
+template <typename T>
+size_t udtw_cost_hand_bytes(int B, int N, int M);
+
+// FVM backward workspace: dtemporal [B, T*U], then (8-byte aligned) the
+// hand-off records of the soft-DTW backward over several workgroups per
+// pair (sequences longer than one workgroup holds).
+template <typename T>
+static size_t fvm_ws_bytes(int B, int Tn, int Un, size_t* hand_at) {
+  const size_t dt = (size_t)B * Tn * Un * sizeof(T), at = (dt + 7) & ~(size_t)7;
+  const size_t hb = udtw_cost_hand_bytes<T>(B, Tn, Un);
+  if (hand_at) *hand_at = at;
+  return hb ? at + hb : dt;
+}
 
 template <typename T>
 int fvm_fwd(const T* C, int B, int K, int Tn, int Un, double gamma, T* tmp, T* R, T* out,
@@ -733,15 +746,19 @@ int fvm_fwd(const T* C, int B, int K, int Tn, int Un, double gamma, T* tmp, T* R
 
 template <typename T>
 int fvm_bwd(const T* C, const T* tmp, const T* R, const T* gout, int B, int K, int Tn, int Un,
-            double gamma, T* dC, T* ws, hipStream_t s, const char* what) {
+            double gamma, T* dC, T* ws, size_t ws_bytes, hipStream_t s, const char* what) {
   if (B < 0 || K <= 0 || Tn <= 0 || Un <= 0 || !(gamma > 0))
     return fail(TW_EINVAL, "%s: bad arguments", what);
   if (B == 0) return TW_OK;
   if (!C || !tmp || !R || !gout || !dC || !ws) return fail(TW_EINVAL, "%s: null pointer", what);
   const int swap = Tn > Un;
   const int N = swap ? Un : Tn, M = swap ? Tn : Un;
+  size_t hand_at = 0;
+  const size_t need = fvm_ws_bytes<T>(B, Tn, Un, &hand_at);
+  if (ws_bytes < need) return fail(TW_ESIZE, "%s: workspace of %zu bytes needed", what, need);
+  T* hand = need > hand_at ? reinterpret_cast<T*>(reinterpret_cast<char*>(ws) + hand_at) : nullptr;
   if (int e = udtw_cost_bwd_any<T>(tmp, nullptr, R, nullptr, gout, nullptr, B, N, M, gamma, ws,
-                                   nullptr, s, what))
+                                   nullptr, hand, hand ? need - hand_at : 0, s, what))
     return e;
   const T k = (T)(1.4426950408889634 / gamma);
   // pair and cell block in grid.x (any batch size)
@@ -867,17 +884,25 @@ int tw_fvm_cost_fwd_f64(const double* cost, int B, int K, int T, int U, double g
   return fvm_fwd<double>(cost, B, K, T, U, gamma, temporal, R, out, scratch, stream,
                          "tw_fvm_cost_fwd_f64");
 }
+size_t tw_fvm_workspace_bytes(int B, int K, int T, int U, int elem_size) {
+  if (B <= 0 || K <= 0 || T <= 0 || U <= 0) return 0;
+  return elem_size == 4 ? fvm_ws_bytes<float>(B, T, U, nullptr)
+                        : fvm_ws_bytes<double>(B, T, U, nullptr);
+}
+
 int tw_fvm_cost_bwd_f32(const float* cost, const float* temporal, const float* R,
                         const float* grad_out, int B, int K, int T, int U, float gamma,
-                        float* d_cost, float* workspace, hipStream_t stream) {
+                        float* d_cost, float* workspace, size_t workspace_bytes,
+                        hipStream_t stream) {
   return fvm_bwd<float>(cost, temporal, R, grad_out, B, K, T, U, gamma, d_cost, workspace,
-                        stream, "tw_fvm_cost_bwd_f32");
+                        workspace_bytes, stream, "tw_fvm_cost_bwd_f32");
 }
 int tw_fvm_cost_bwd_f64(const double* cost, const double* temporal, const double* R,
                         const double* grad_out, int B, int K, int T, int U, double gamma,
-                        double* d_cost, double* workspace, hipStream_t stream) {
+                        double* d_cost, double* workspace, size_t workspace_bytes,
+                        hipStream_t stream) {
   return fvm_bwd<double>(cost, temporal, R, grad_out, B, K, T, U, gamma, d_cost, workspace,
-                         stream, "tw_fvm_cost_bwd_f64");
+                         workspace_bytes, stream, "tw_fvm_cost_bwd_f64");
 }
 
 }  // extern "C"

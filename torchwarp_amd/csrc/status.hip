@@ -28,6 +28,7 @@ unsigned int* g_status_ptr[kMaxDevices];
 
 std::atomic<int> g_test_spins{0};
 std::atomic<int> g_test_drop{0};
+std::atomic<int> g_test_mw{-1};
 }  // namespace
 
 namespace tw {
@@ -49,6 +50,8 @@ int wait_spins(int dflt) {
 }
 
 int wait_drop_handoff() { return g_test_drop.load(std::memory_order_relaxed); }
+
+int test_mw_mode() { return g_test_mw.load(std::memory_order_relaxed); }
 
 }  // namespace tw
 
@@ -73,6 +76,8 @@ int tw_async_status(int clear) {
                     "neighbouring workgroup's boundary row; the outputs of that call are NaN");
   return TW_OK;
 }
+
+void tw_test_set_mw(int mode) { g_test_mw.store(mode >= 0 && mode <= 2 ? mode : -1); }
 
 void tw_test_set_wait(int spins, int drop_handoff) {
   g_test_spins.store(spins > 0 ? spins : 0, std::memory_order_relaxed);

@@ -21,6 +21,10 @@ int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);
 // Device limits of the current device, queried once per device.
 int max_lds_bytes();
+// Frequency of the device's real-time counter (s_memrealtime), kHz.
+double realtime_khz();
+// Compute units of the current device.
+int num_cus();
 // Device address of the current device's asynchronous status word (bit
 // TW_STATUS_WAIT_GAVE_UP: a bounded cross-workgroup wait ran out), or null.
 unsigned int* status_word();
@@ -28,5 +32,7 @@ unsigned int* status_word();
 // test hook that keeps boundary rows from being handed over.
 int wait_spins(int dflt);
 int wait_drop_handoff();
+// Several-workgroups-per-pair mode a test set (tw_test_set_mw), or -1.
+int test_mw_mode();
 
 }  // namespace tw

@@ -34,6 +34,41 @@ static void set_sigma(UdtwArgs<T>& a, int sigma) {
   a.hv0 = (T)(a.sigma ? 0.0 : 0.5);
 }
 
+// float calls carry R in double precision (the RD kernels) when the
+// accumulated cost can grow large against float32's spacing. R sums up to
+// N + M - 1 costs and the backward's weights are exponentials of differences
+// of neighbouring R values in units of gamma / log2(e): once
+// (N + M - 1) log2(e) / gamma passes kRdScale, float32 R loses the low bits
+// those differences need (at N = M = 1024, gamma = 0.1 the gradients would
+// carry ~5e-2 relative error; 1e-3 with R in double). One row per thread
+// must serve N (the RD kernels' layout), and a pair's R plane in double must
+// stay below 2 GiB. TORCHWARP_UDTW_RD = 0 / 1 forces it off / on (where those
+// hold).
+constexpr double kRdScale = 2048.0;
+
+template <typename T>
+static bool carry_double(int N, int M, double gamma) {
+  if (sizeof(T) != 4 || N <= 0 || M <= 0 || !(gamma > 0)) return false;
+  static const int mode = [] {
+    const char* e = getenv("TORCHWARP_UDTW_RD");
+    return e ? atoi(e) : -1;
+  }();
+  if (mode == 0) return false;
+  const int n = N < M ? N : M, m = N < M ? M : N;
+  if (!mw_long<T>(n) && pick_shape<T>(n, false).rows != 1) return false;
+  if ((long long)n * m * 8 >= (1LL << 31)) return false;   // a pair's R plane stays below 2 GiB
+  if (mode == 1) return true;
+  return (double)(n + m - 1) * 1.4426950408889634 / gamma > kRdScale;
+}
+
+// Bytes of the S / dS plane (D > 1) and where the MW hand-off records start
+// in a feature-path backward workspace (8-byte aligned).
+template <typename T>
+static size_t splane_bytes(int B, int N, int M, int D) {
+  return D > 1 ? (size_t)B * N * M * sizeof(T) : 0;
+}
+static size_t align8(size_t n) { return (n + 7) & ~(size_t)7; }
+
 static int check_dims(const char* what, int B, int N, int M, double gamma) {
   if (B < 0 || N <= 0 || M <= 0) return fail(TW_EINVAL, "%s: bad sizes B=%d N=%d M=%d", what, B, N, M);
   if (N > M) return fail(TW_EINVAL, "%s: expected N <= M (got %d > %d)", what, N, M);
@@ -43,7 +78,8 @@ static int check_dims(const char* what, int B, int N, int M, double gamma) {
 
 template <typename T>
 static int cost_fwd(const T* C, const T* Q, int B, int N, int M, double gamma, double band, T* R,
-                    T* P, T* out_r, T* out_p, hipStream_t s, const char* what) {
+                    T* P, T* out_r, T* out_p, hipStream_t s, const char* what,
+                    bool allow_rd = true) {
   if (int e = check_dims(what, B, N, M, gamma)) return e;
   if (B == 0) return TW_OK;
   if (!C || !R || !out_r || !out_p) return fail(TW_EINVAL, "%s: null pointer", what);
@@ -57,6 +93,7 @@ static int cost_fwd(const T* C, const T* Q, int B, int N, int M, double gamma, d
   a.out_p = out_p;
   a.N = N;
   a.M = M;
+  a.rd = allow_rd && carry_double<T>(N, M, gamma);
   set_hyper(a, gamma, 0.0, 1.0, band);
   return launch_pen<T, SRC_COST>(Q != nullptr, false, a, B, s, what);
 }
@@ -64,7 +101,8 @@ static int cost_fwd(const T* C, const T* Q, int B, int N, int M, double gamma, d
 template <typename T>
 static int cost_bwd(const T* C, const T* Q, const T* R, const T* P, const T* gr, const T* gp,
                     int B, int N, int M, double gamma, double band, int gstride, T* dC, T* dQ,
-                    hipStream_t s, const char* what) {
+                    T* ws, size_t ws_bytes, hipStream_t s, const char* what,
+                    bool allow_rd = true) {
   if (int e = check_dims(what, B, N, M, gamma)) return e;
   if (B == 0) return TW_OK;
   if (!C || !R || !gr || !dC) return fail(TW_EINVAL, "%s: null pointer", what);
@@ -83,6 +121,11 @@ static int cost_bwd(const T* C, const T* Q, const T* R, const T* P, const T* gr,
   a.M = M;
   if (gstride != 0 && gstride != 1) return fail(TW_EINVAL, "%s: grad_stride must be 0 or 1", what);
   a.gstride = gstride;
+  a.rd = allow_rd && carry_double<T>(N, M, gamma);
+  const size_t need = mw_hand_bytes<T>(B, N, M);
+  if (need && (!ws || ws_bytes < need))
+    return fail(TW_ESIZE, "%s: workspace of %zu bytes needed", what, need);
+  a.hand = need ? reinterpret_cast<unsigned long long*>(ws) : nullptr;
   set_hyper(a, gamma, 0.0, 1.0, band);
   return launch_pen<T, SRC_COST>(pen, true, a, B, s, what);
 }
@@ -90,14 +133,21 @@ static int cost_bwd(const T* C, const T* Q, const T* R, const T* P, const T* gr,
 template <typename T>
 int udtw_cost_fwd_any(const T* C, const T* Q, int B, int N, int M, double gamma, double band,
                       T* R, T* P, T* out_r, T* out_p, hipStream_t s, const char* what) {
-  return cost_fwd<T>(C, Q, B, N, M, gamma, band, R, P, out_r, out_p, s, what);
+  return cost_fwd<T>(C, Q, B, N, M, gamma, band, R, P, out_r, out_p, s, what, false);
 }
 template <typename T>
 int udtw_cost_bwd_any(const T* C, const T* Q, const T* R, const T* P, const T* gr, const T* gp,
-                      int B, int N, int M, double gamma, T* dC, T* dQ, hipStream_t s,
-                      const char* what) {
-  return cost_bwd<T>(C, Q, R, P, gr, gp, B, N, M, gamma, 0.0, 1, dC, dQ, s, what);
+                      int B, int N, int M, double gamma, T* dC, T* dQ, T* ws, size_t ws_bytes,
+                      hipStream_t s, const char* what) {
+  return cost_bwd<T>(C, Q, R, P, gr, gp, B, N, M, gamma, 0.0, 1, dC, dQ, ws, ws_bytes, s, what,
+                     false);
 }
+template <typename T>
+size_t udtw_cost_hand_bytes(int B, int N, int M) {
+  return mw_hand_bytes<T>(B, N < M ? N : M, N < M ? M : N);
+}
+template size_t udtw_cost_hand_bytes<float>(int, int, int);
+template size_t udtw_cost_hand_bytes<double>(int, int, int);
 template int udtw_cost_fwd_any<float>(const float*, const float*, int, int, int, double, double,
                                       float*, float*, float*, float*, hipStream_t, const char*);
 template int udtw_cost_fwd_any<double>(const double*, const double*, int, int, int, double,
@@ -105,10 +155,11 @@ template int udtw_cost_fwd_any<double>(const double*, const double*, int, int, i
                                        const char*);
 template int udtw_cost_bwd_any<float>(const float*, const float*, const float*, const float*,
                                       const float*, const float*, int, int, int, double, float*,
-                                      float*, hipStream_t, const char*);
+                                      float*, float*, size_t, hipStream_t, const char*);
 template int udtw_cost_bwd_any<double>(const double*, const double*, const double*,
                                        const double*, const double*, const double*, int, int,
-                                       int, double, double*, double*, hipStream_t, const char*);
+                                       int, double, double*, double*, double*, size_t,
+                                       hipStream_t, const char*);
 
 }  // namespace tw
 
@@ -135,17 +186,21 @@ int tw_udtw_cost_fwd_f64(const double* cost, const double* pen, int B, int N, in
 int tw_udtw_cost_bwd_f32(const float* cost, const float* pen, const float* R, const float* P,
                          const float* grad_dist, const float* grad_pen, int B, int N, int M,
                          float gamma, float bandwidth, int grad_stride, float* d_cost,
-                         float* d_pen, hipStream_t stream) {
+                         float* d_pen, float* workspace, size_t workspace_bytes,
+                         hipStream_t stream) {
   return cost_bwd<float>(cost, pen, R, P, grad_dist, grad_pen, B, N, M, gamma, bandwidth,
-                         grad_stride, d_cost, d_pen, stream, "tw_udtw_cost_bwd_f32");
+                         grad_stride, d_cost, d_pen, workspace, workspace_bytes, stream,
+                         "tw_udtw_cost_bwd_f32");
 }
 
 int tw_udtw_cost_bwd_f64(const double* cost, const double* pen, const double* R,
                          const double* P, const double* grad_dist, const double* grad_pen, int B,
                          int N, int M, double gamma, double bandwidth, int grad_stride,
-                         double* d_cost, double* d_pen, hipStream_t stream) {
+                         double* d_cost, double* d_pen, double* workspace,
+                         size_t workspace_bytes, hipStream_t stream) {
   return cost_bwd<double>(cost, pen, R, P, grad_dist, grad_pen, B, N, M, gamma, bandwidth,
-                          grad_stride, d_cost, d_pen, stream, "tw_udtw_cost_bwd_f64");
+                          grad_stride, d_cost, d_pen, workspace, workspace_bytes, stream,
+                          "tw_udtw_cost_bwd_f64");
 }
 
 }  // extern "C"
@@ -183,6 +238,7 @@ static int feat_fwd(const T* X, const T* Y, const T* vx, const T* vy, int B, int
   a.out_p = out_p;
   a.N = N;
   a.M = M;
+  a.rd = carry_double<T>(N, M, gamma);
   set_hyper(a, gamma, beta, eps, band);
   set_sigma(a, sigma);
   if (D == 1) {
@@ -226,8 +282,16 @@ static int feat_bwd(const T* X, const T* Y, const T* vx, const T* vy, const T* R
   a.M = M;
   if (gstride != 0 && gstride != 1) return fail(TW_EINVAL, "%s: grad_stride must be 0 or 1", what);
   a.gstride = gstride;
+  a.rd = carry_double<T>(N, M, gamma);
   set_hyper(a, gamma, beta, eps, band);
   set_sigma(a, sigma);
+  // workspace: the S / dS plane (D > 1), then the MW hand-off records
+  const size_t sp = splane_bytes<T>(B, N, M, D), hb = mw_hand_bytes<T>(B, N, M);
+  const size_t need = hb ? align8(sp) + hb : sp;
+  if (need && (!ws || ws_bytes < need))
+    return fail(TW_ESIZE, "%s: workspace of %zu bytes needed", what, need);
+  a.hand = hb ? reinterpret_cast<unsigned long long*>(reinterpret_cast<char*>(ws) + align8(sp))
+              : nullptr;
   if (D == 1) {
     a.X = X;
     a.Y = Y;
@@ -235,9 +299,6 @@ static int feat_bwd(const T* X, const T* Y, const T* vx, const T* vy, const T* R
     a.dY = dY;
     return launch_pen<T, SRC_FEAT1>(pen, true, a, B, s, what);
   }
-  const size_t need = (size_t)B * N * M * sizeof(T);
-  if (!ws || ws_bytes < need)
-    return fail(TW_ESIZE, "%s: workspace of %zu bytes needed", what, need);
   // the raw squared distances: the forward's, or recomputed into the
   // workspace; the sweep writes their adjoint into the workspace (in place
   // when they are there: each cell is read and written by the same thread)
@@ -254,9 +315,24 @@ static int feat_bwd(const T* X, const T* Y, const T* vx, const T* vy, const T* R
 
 extern "C" {
 
+size_t tw_udtw_carry_bytes(int B, int N, int M, double gamma, int elem_size) {
+  if (B <= 0 || N <= 0 || M <= 0 || (elem_size != 4 && elem_size != 8)) return 0;
+  const bool rd = elem_size == 4 && carry_double<float>(N, M, gamma);
+  return (size_t)B * N * M * (rd ? 8 : (size_t)elem_size);
+}
+
 size_t tw_udtw_feat_workspace_bytes(int B, int N, int M, int D, int elem_size) {
-  if (D <= 1 || B <= 0 || N <= 0 || M <= 0) return 0;
-  return (size_t)B * N * M * (size_t)elem_size;
+  if (B <= 0 || N <= 0 || M <= 0 || D <= 0 || (elem_size != 4 && elem_size != 8)) return 0;
+  const int n = N < M ? N : M, m = N < M ? M : N;
+  const size_t sp = D > 1 ? (size_t)B * N * M * (size_t)elem_size : 0;
+  const size_t hb = elem_size == 4 ? mw_hand_bytes<float>(B, n, m) : mw_hand_bytes<double>(B, n, m);
+  return hb ? align8(sp) + hb : sp;
+}
+
+size_t tw_udtw_cost_workspace_bytes(int B, int N, int M, int elem_size) {
+  if (B <= 0 || N <= 0 || M <= 0 || (elem_size != 4 && elem_size != 8)) return 0;
+  const int n = N < M ? N : M, m = N < M ? M : N;
+  return elem_size == 4 ? mw_hand_bytes<float>(B, n, m) : mw_hand_bytes<double>(B, n, m);
 }
 
 int tw_udtw_feat_fwd_f32(const float* X, const float* Y, const float* vx, const float* vy, int B,

@@ -81,15 +81,18 @@ struct UdtwArgs {
   int gstride;   // element stride of gr / gp (0: one value for every pair)
   int groups;    // forward with MW: row groups (workgroups) per pair
   unsigned int* status;   // MW: per-device status word (TW_STATUS_WAIT_GAVE_UP)
-  int spins;              // MW: poll limit of a boundary-row wait
+  int spins;              // MW: poll rounds of a boundary-row wait (a test's limit)
+  unsigned long long wait_ticks;   // MW: time limit of a wait, device real-time ticks
   int drop_handoff;       // MW test hook: boundary rows are never handed over
+  int rd;                 // float: carry R in double precision (the RD kernels)
+  unsigned long long* hand;   // backward with MW: boundary hand-off records
 };
 
 // Half of a variance input: 0.5 v, or 0.5 v^2 when the input is a standard
 // deviation, as v (hv1 v + hv0) with (hv1, hv0) = (0, 0.5) or (0.5, 0).
 template <typename T>
 __device__ __forceinline__ T half_var(const UdtwArgs<T>& a, T v) {
-  return v * (a.hv1 * v + a.hv0);
+  return v * fma(a.hv1, v, a.hv0);
 }
 
 // ------------------------------------------------------------- pipeline
@@ -144,15 +147,27 @@ constexpr int kWindow = 64;          // steps per soffset window (one per lane)
 // no valid lane holds the sentinel. Each cell is its own flag, so no fence
 // or cache write-back is needed, on any XCD. Workgroup g runs kGroupLag
 // diagonals behind g - 1's first wavefront: its last wavefront's lag plus a
-// window and the HBM round trip, so the polls rarely wait. The waited-on
-// workgroup always has the lower index, so in-order dispatch guarantees
-// progress, and every poll loop is bounded by kMwSpins rounds (a test can set
-// fewer). A wait that runs out sets TW_STATUS_WAIT_GAVE_UP in the device's
-// status word and lets the sentinel (a NaN) flow on into the pair's outputs,
-// so the kernel still exits and tw_async_status reports the failure.
+// window and the HBM round trip, so the polls rarely wait once the pipeline
+// of a pair's groups has filled (a group whose rows have no cells yet on a
+// diagonal steps through it quickly and then waits for the groups below it:
+// the first wait of the last of G groups lasts about G times a few hundred
+// steps). The waited-on workgroup always has the lower index, so in-order
+// dispatch guarantees progress, and every wait is bounded in time by the
+// device's real-time counter (kMwWaitSeconds; a test can bound it by a few
+// poll rounds instead). A wait that runs out sets TW_STATUS_WAIT_GAVE_UP in
+// the device's status word and lets the sentinel (a NaN) flow on into the
+// pair's outputs, so the kernel still exits and tw_async_status reports it.
 constexpr int kMwRows = 256;
 constexpr int kGroupLag = kLag * (kMwRows / 64) + kWindow + 16;
-constexpr int kMwSpins = 1 << 16;
+constexpr int kMwSpins = 0x7FFFFFFF;
+constexpr double kMwWaitSeconds = 2.0;
+// True when a wait that began at tick t0 has polled `spin + 1` rounds out of
+// a.spins, or has lasted longer than a.wait_ticks (wave-uniform).
+template <typename T>
+__device__ __forceinline__ bool wait_ran_out(const UdtwArgs<T>& a, int spin,
+                                             unsigned long long t0) {
+  return spin + 1 >= a.spins || __builtin_amdgcn_s_memrealtime() - t0 > a.wait_ticks;
+}
 __host__ __device__ constexpr unsigned long long mw_sentinel_bits(int es) {
   return es == 4 ? 0x7FC0DEADull : 0x7FF8DEADDEADDEADull;
 }
@@ -174,6 +189,34 @@ __device__ __forceinline__ bool mw_is_sentinel(T v) {
     return (unsigned long long)__double_as_longlong(v) == mw_sentinel_bits(8);
 }
 
+// Backward hand-off records (MW): the top row of a row group hands the group
+// above its (E, Rbar, Pbar, A) and the column gradient sums (dy, dvy) of
+// every diagonal, as 64-bit words stored with agent-scope atomics into a
+// caller workspace pre-filled with kHandSentinel (never a value a record
+// holds: two NaNs with a fixed payload). Floats are packed two per word;
+// with R in double (RD) E takes a word of its own. Per cell
+// hand_words(element size) words are reserved (4 for float, 6 for double).
+constexpr unsigned long long kHandSentinel = 0x7FF8DEAD7FC0DEADull;
+__host__ __device__ constexpr int hand_words(int es) { return es == 4 ? 4 : 6; }
+__device__ __forceinline__ unsigned long long pack_ff(float lo, float hi) {
+  return (unsigned long long)__float_as_uint(lo) | ((unsigned long long)__float_as_uint(hi) << 32);
+}
+__device__ __forceinline__ float word_lo(unsigned long long w) { return __uint_as_float((unsigned)w); }
+__device__ __forceinline__ float word_hi(unsigned long long w) {
+  return __uint_as_float((unsigned)(w >> 32));
+}
+__device__ __forceinline__ unsigned long long word_d(double v) {
+  return (unsigned long long)__double_as_longlong(v);
+}
+__device__ __forceinline__ double word_to_d(unsigned long long w) {
+  return __longlong_as_double((long long)w);
+}
+// Words in use per record for T (float / double) and RD.
+template <typename T, bool RD>
+struct HandRec {
+  static constexpr int words = sizeof(T) == 8 ? 6 : (RD ? 4 : 3);
+};
+
 // Barrier at the end of a block: every LDS operation of this wavefront is
 // complete (the block's mailbox stores and the reads of the previous block's
 // records), then the workgroup barrier. Outstanding global stores are not
@@ -190,6 +233,24 @@ template <typename T>
 struct alignas(4 * sizeof(T)) Rec8 {
   Rec4<T> a, b;
 };
+// Records of the RD kernels (float values; R / E and P / A in double).
+struct alignas(8) RecD4 {   // forward: R (double), P, y, hy
+  double x;
+  float y, z, w;
+};
+struct alignas(8) RecDA {   // backward: E (double), Rbar, Pbar, A
+  double x;
+  float y, z, w;
+};
+struct alignas(16) RecD8 {
+  RecDA a;
+  Rec4<float> b;
+};
+// Mailbox record types of a forward / backward sweep.
+template <typename T, bool RD>
+using FwdRec = std::conditional_t<RD, RecD4, Rec4<T>>;
+template <typename T, bool RD>
+using BwdRec = std::conditional_t<RD, RecD8, Rec8<T>>;
 
 // soff(d) = (index of the first cell of diagonal d) - (row of that cell) in
 // the diagonal-major layout of an N x M grid, N <= M: cell (i, d - i) is
@@ -218,22 +279,31 @@ __host__ __device__ __forceinline__ int col_pad(int N, int nw) {
 // SIMD holds several of the pair's wavefronts and hides their waits: at
 // N = M = 1024 the sweeps take 0.93 / 1.76 ms against 1.28 / 2.24 ms with
 // 4 rows per thread and one wavefront per SIMD.
-template <typename T, int ROWS, bool LC, bool BWD>
+template <typename T, int ROWS, bool LC, bool BWD, bool MW = false>
 struct MaxThreads {
   static constexpr int value =
-      ROWS >= 16 ? 1024 : ((ROWS == 1 && !LC) ? (sizeof(T) == 4 ? 1024 : 512) : 256);
+      MW ? 256 : ROWS >= 16 ? 1024 : ((ROWS == 1 && !LC) ? (sizeof(T) == 4 ? 1024 : 512) : 256);
 };
 
 // LC (one row per thread): the column operands come from LDS (ColRec);
 // otherwise they travel down the rows with the DPP shifts that move R.
-template <typename T, int ROWS, int SRC, bool PEN, bool BAND, int PF, bool LC, bool MW = false>
-__global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_fwd_kernel(UdtwArgs<T> a) {
+template <typename T, int ROWS, int SRC, bool PEN, bool BAND, int PF, bool LC, bool MW = false,
+          bool RD = false>
+__global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false, MW>::value)) udtw_fwd_kernel(UdtwArgs<T> a) {
+  // Products and sums are fused only where written as fma: the edge and the
+  // other wavefronts, and every launch layout, then evaluate a cell alike.
+#pragma clang fp contract(off)
   extern __shared__ __align__(16) unsigned char smem_raw[];
   constexpr int ES = sizeof(T);
+  // RT: the type R is carried in (registers, mailboxes, the R plane)
+  using RT = std::conditional_t<RD, double, T>;
+  constexpr int RES = sizeof(RT);
+  static_assert(!RD || (sizeof(T) == 4 && ROWS == 1), "RD: float, one row per thread");
+  const RT RINF = inf_v<RT>();
   constexpr bool COLS = SRC != SRC_COST;
   constexpr bool FLOW = COLS && !LC;
   static_assert(!LC || (COLS && ROWS == 1), "LDS columns need one row per thread");
-  static_assert(!MW || (ROWS == 1 && !LC && !BAND), "MW: one row per thread, no band");
+  static_assert(!MW || (ROWS == 1 && !LC), "MW: one row per thread");
   const int N = a.N, M = a.M;
   // MW: pair b, row group grp of G, rows from rbase
   const int G = MW ? a.groups : 1;
@@ -252,9 +322,10 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
 
   // box[v * kBox + slot]: wavefront v's inbox (the row above its first
   // row; box[nw] is the last wavefront's unread outbox), then the dump area.
-  Rec4<T>* box = reinterpret_cast<Rec4<T>*>(smem_raw);
-  Rec4<T>* dump = box + (nw + 1) * kBox;
-  const Rec4<T> rec0 = {INF, (T)0, (T)0, (T)0.5};   // the record before the sweep
+  using Rec = FwdRec<T, RD>;
+  Rec* box = reinterpret_cast<Rec*>(smem_raw);
+  Rec* dump = box + (nw + 1) * kBox;
+  const Rec rec0 = {RINF, (T)0, (T)0, (T)0.5};   // the record before the sweep
   for (int t = tid; t < (nw + 1) * kBox; t += blockDim.x) box[t] = rec0;
   ColRec<T>* cols = reinterpret_cast<ColRec<T>*>(dump + kDump);
   const int cpad = col_pad(N, nw);
@@ -271,7 +342,8 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
   }
 
   Buf bR, bP, bC, bQ, bY, bVY;
-  bR.init(a.R + b * NM, NM);
+  RT* const Rpl = reinterpret_cast<RT*>(a.R);   // the R planes ([B, N*M] of RT)
+  bR.init(Rpl + b * NM, NM);
   if (PEN) bP.init(a.P + b * NM, NM);
   if (SRC != SRC_FEAT1) bC.init(a.C + b * NM, NM);
   if (SRC == SRC_COST && PEN) bQ.init(a.Q + b * NM, NM);
@@ -282,29 +354,32 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
   auto col_y = [&](int vcol) -> T { return SRC == SRC_FEAT1 ? bY.ld<T>(vcol, 0) : (T)0; };
   auto col_vy = [&](int vcol) -> T { return FLOW ? bVY.ld<T>(vcol, 0) : (T)1; };
 
-  Rec4<T>* const inbox = box + wave * kBox;
-  Rec4<T>* const outbox = box + (wave + 1) * kBox;
+  Rec* const inbox = box + wave * kBox;
+  Rec* const outbox = box + (wave + 1) * kBox;
   // the mailbox store of a step: lane 63 to the slot, the others to the dump
-  Rec4<T>* const my_out = lane == 63 ? outbox : dump + lane;
+  Rec* const my_out = lane == 63 ? outbox : dump + lane;
   __syncthreads();
 
   const int row0 = rbase + tid * ROWS;
-  T xr[ROWS], hxr[ROWS], r1[ROWS], r2[ROWS], p1[ROWS], p2[ROWS], yc[ROWS], hyc[ROWS];
-  int vst[ROWS], vnat[ROWS], jb[ROWS];
+  T xr[ROWS], hxr[ROWS], p1[ROWS], p2[ROWS], yc[ROWS], hyc[ROWS];
+  RT r1[ROWS], r2[ROWS];
+  int vst[ROWS], vsr[ROWS], vnat[ROWS], jb[ROWS];
 #pragma unroll
   for (int k = 0; k < ROWS; ++k) {
     const int i = row0 + k;
     xr[k] = (SRC == SRC_FEAT1 && i < N) ? a.X[(size_t)b * N + i] : (T)0;
     hxr[k] = (COLS && i < N) ? half_var(a, a.VX[(size_t)b * N + i]) : (T)0.5;
-    r1[k] = r2[k] = INF;
+    r1[k] = r2[k] = RINF;
     p1[k] = p2[k] = (T)0;
     yc[k] = (T)0;
     hyc[k] = (T)0.5;
     vst[k] = i * ES;                          // row offset within a diagonal
+    vsr[k] = i * RES;                         // the same in the R plane
     vnat[k] = i < N ? i * (M - 1) * ES : 0;   // [N, M] offset of (i, d - i) minus d
     jb[k] = i < N ? -i : INT_MIN / 2;         // column of row i on diagonal d is d + jb
   }
-  T nr1 = (row0 == 0) ? (T)0 : INF, nr2 = INF, np1 = (T)0, np2 = (T)0;
+  RT nr1 = (row0 == 0) ? (RT)0 : RINF, nr2 = RINF;
+  T np1 = (T)0, np2 = (T)0;
 
   const int d_first = -kLag * wave - (MW ? kGroupLag * grp : 0);
   const int steps =
@@ -387,7 +462,7 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
     const ColRec<T>* const crow = cols + cpad - row0;
     ColRec<T> creg[2];
     if (LC) creg[0] = crow[d_first];
-    Rec4<T> carry = rec0;   // the record used by the first step of the next block
+    Rec carry = rec0;   // the record used by the first step of the next block
     // Drain the set-up loads here: the compiler derives each in-loop wait on
     // a ring register from every path into the loop, and the entry path
     // would otherwise force a near-full vmcnt wait on every trip.
@@ -400,42 +475,50 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
       const int tn = min(kWindow, steps - tw);
       // MW, edge wavefront of a later group: lane l holds the row above on
       // step l of the window, (R, P) of cell (rbase - 1, dl - rbase)
-      T win_r = INF, win_p = (T)0;
+      RT win_r = RINF;
+      T win_p = (T)0;
       if (MW && EDGE && grp > 0) {
         const int j = dl - rbase;
         const bool v = (unsigned)j < (unsigned)M;
-        T* const pr = a.R + (size_t)b * NM + diag_soff(dl - 1, N, M) + (rbase - 1);
-        T* const pp = PEN ? a.P + (size_t)b * NM + diag_soff(dl - 1, N, M) + (rbase - 1) : pr;
-        T vr = INF, vp = (T)0;
-        int spin = 0;
-        for (; spin < a.spins; ++spin) {
+        const size_t cell = (size_t)b * NM + diag_soff(dl - 1, N, M) + (rbase - 1);
+        RT* const pr = Rpl + cell;
+        T* const pp = PEN ? a.P + cell : a.P;
+        RT vr = RINF;
+        T vp = (T)0;
+        bool gave_up = false;
+        const unsigned long long t0w = __builtin_amdgcn_s_memrealtime();
+        for (int spin = 0;; ++spin) {
           if (v) {
             vr = __hip_atomic_load(pr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (PEN) vp = __hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           }
           const bool pend = v && (mw_is_sentinel(vr) || (PEN && mw_is_sentinel(vp)));
           if (__ballot(pend) == 0) break;
+          if (wait_ran_out(a, spin, t0w)) {
+            gave_up = true;
+            break;
+          }
           __builtin_amdgcn_s_sleep(4);
         }
         // The wait ran out: report it (the sentinel, a NaN, then flows into
         // this pair's outputs) and go on, so the kernel still exits.
-        if (spin == a.spins && lane == 0)
+        if (gave_up && lane == 0)
           __hip_atomic_fetch_or(a.status, TW_STATUS_WAIT_GAVE_UP, __ATOMIC_RELAXED,
                                 __HIP_MEMORY_SCOPE_AGENT);
-        win_r = v ? vr : INF;
+        win_r = v ? vr : RINF;
         win_p = v ? vp : (T)0;
       }
     for (int t0 = 0; t0 < tn; t0 += kSlots) {
       const int half = (t0 / kSlots) & 1;   // mailbox half of this block
-      Rec4<T> rec[kSlots];
+      Rec rec[kSlots];
       if (!EDGE) {
-        const Rec4<T>* prev = inbox + (half ^ 1) * kSlots;
+        const Rec* prev = inbox + (half ^ 1) * kSlots;
         rec[0] = carry;
 #pragma unroll
         for (int u = 1; u < kSlots; ++u) rec[u] = prev[u - 1];
         carry = prev[kSlots - 1];
       }
-      Rec4<T>* const out = my_out + half * kSlots;
+      Rec* const out = my_out + half * kSlots;
       const ColRec<T>* const cblk = crow + (d_first + tw + t0);
       if (VEC) {
 #pragma unroll
@@ -451,7 +534,7 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
       // of the block's diagonals, so its cells are INF / 0 without arithmetic
       bool skip = false;
       if (BAND) {
-        const int dlo = d_first + tw + t0, wlo = wave * 64 * ROWS;
+        const int dlo = d_first + tw + t0, wlo = rbase + wave * 64 * ROWS;
         skip = (T)(2 * wlo - (dlo + kSlots - 1)) > a.band ||
                (T)(dlo - 2 * (wlo + 64 * ROWS - 1)) > a.band;
       }
@@ -467,12 +550,12 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
         }
         // the row above the first row on diagonal d-1, and the column
         // entering the first row on diagonal d
-        Rec4<T> e;
+        Rec e;
         if (EDGE && MW)
           e = {lane_val(win_r, t0 + u), lane_val(win_p, t0 + u), ey_ring[u],
                COLS ? half_var(a, evy_ring[u]) : (T)0.5};
         else if (EDGE)
-          e = {INF, (T)0, ey_ring[u], COLS ? half_var(a, evy_ring[u]) : (T)0.5};
+          e = {RINF, (T)0, ey_ring[u], COLS ? half_var(a, evy_ring[u]) : (T)0.5};
         else
           e = rec[u];
 
@@ -480,7 +563,7 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
         np2 = np1;
         nr1 = shift_prev(r1[ROWS - 1], e.x);
         if (PEN)
-          np1 = (EDGE && !MW) ? shift_prev0(p1[ROWS - 1]) : shift_prev(p1[ROWS - 1], e.y);
+          np1 = (EDGE && !MW) ? shift_prev0(p1[ROWS - 1]) : shift_prev(p1[ROWS - 1], (T)e.y);
         if (LC) {
           yc[0] = creg[u & 1].y;
           hyc[0] = creg[u & 1].hy;
@@ -489,8 +572,8 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
           // them through readfirstlane gives each shift a fresh copy, so the
           // ring registers are never tied to (and overwritten by) a shift
           const T ny = SRC != SRC_FEAT1 ? (T)0
-                       : shift_prev(yc[ROWS - 1], EDGE ? uniform(e.z) : e.z);
-          const T nhy = shift_prev(hyc[ROWS - 1], EDGE ? uniform(e.w) : e.w);
+                       : shift_prev(yc[ROWS - 1], EDGE ? uniform((T)e.z) : (T)e.z);
+          const T nhy = shift_prev(hyc[ROWS - 1], EDGE ? uniform((T)e.w) : (T)e.w);
 #pragma unroll
           for (int k = ROWS - 1; k > 0; --k) {
             yc[k] = yc[k - 1];
@@ -501,18 +584,20 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
         }
 
         const int so = __builtin_amdgcn_readlane(so_st, t0 + u);
-        T nr[ROWS], np[ROWS];
+        const int so_r = so * (RES / ES);   // the same diagonal in the R plane
+        RT nr[ROWS];
+        T np[ROWS];
 #pragma unroll
         for (int k = 0; k < ROWS; ++k) {
           const int j = d + jb[k];
           const bool valid = (unsigned)j < (unsigned)M;
           if (BAND && skip) {
-            nr[k] = INF;
+            nr[k] = RINF;
             np[k] = (T)0;
           } else {
-          const T up = k ? r1[k - 1] : nr1;
-          const T dg = k ? r2[k - 1] : nr2;
-          const T lf = r1[k];
+          const RT up = k ? r1[k - 1] : nr1;
+          const RT dg = k ? r2[k - 1] : nr2;
+          const RT lf = r1[k];
           T ch, q = (T)0;
           if (SRC == SRC_COST) {
             ch = cc[k] * a.k;
@@ -529,29 +614,32 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
             ch = sq * (rcp(var) * a.k);
             if (PEN) q = a.beta_ln2 * lg2(var);
           }
-          const T m = min3(dg, up, lf);
-          const T ed = ex2(m - dg), eu = ex2(m - up), el = ex2(m - lf);
+          // the differences of neighbours are taken in RT, the exponentials
+          // in T (with RD: float exp2 / log2 of double-exact differences)
+          const RT m = min3(dg, up, lf);
+          const T ed = ex2((T)(m - dg)), eu = ex2((T)(m - up)), el = ex2((T)(m - lf));
           const T s = ed + eu + el;
-          const T rv = ch + m - lg2(s);
+          const RT rv = (RT)ch + m - (RT)lg2(s);
           bool ok = valid;
-          if (BAND) ok = ok && (m < INF) && (fabs((T)(2 * (row0 + k) - d)) <= a.band);
-          nr[k] = ok ? rv : INF;
+          if (BAND) ok = ok && (m < RINF) && (fabs((T)(2 * (row0 + k) - d)) <= a.band);
+          nr[k] = ok ? rv : RINF;
           if (PEN) {
             const T pup = k ? p1[k - 1] : np1;
             const T pdg = k ? p2[k - 1] : np2;
-            const T pv = q + (ed * pdg + eu * pup + el * p1[k]) * rcp(s);
+            const T ps = fma(el, p1[k], fma(eu, pup, ed * pdg));
+            const T pv = fma(ps, rcp(s), q);
             np[k] = ok ? pv : (T)0;
           } else {
             np[k] = (T)0;
           }
           }
-          const int vo = (valid && !(MW && drop_row)) ? vst[k] : kOob;
-          bR.st(nr[k], vo, so);
-          if (PEN) bP.st(np[k], vo, so);
+          const bool stv = valid && !(MW && drop_row);
+          bR.st(nr[k], stv ? vsr[k] : kOob, so_r);
+          if (PEN) bP.st(np[k], stv ? vst[k] : kOob, so);
           if (MW && publish && lane == 63 && valid && !drop_row) {
             // the next group's row above: a second, agent-coherent store
             const size_t c = (size_t)b * NM + (size_t)((so + vst[k]) / ES);
-            __hip_atomic_store(a.R + c, nr[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(Rpl + c, nr[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (PEN)
               __hip_atomic_store(a.P + c, np[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           }
@@ -593,8 +681,8 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
   // thread that stored it reads it back
   if (row0 <= N - 1 && N - 1 < row0 + ROWS) {
     const int so = (int)(NM - 1) * ES;
-    const T rl = bR.ld<T>(0, so);
-    a.out_r[b] = rl * a.inv_k;   // INF (unreachable) and NaN pass through
+    const RT rl = bR.ld<RT>(0, (int)(NM - 1) * RES);
+    a.out_r[b] = (T)(rl * (RT)a.inv_k);   // INF (unreachable) and NaN pass through
     a.out_p[b] = PEN ? bP.ld<T>(0, so) : (T)0;
   }
 }
@@ -608,15 +696,31 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, false>::value)) udtw_
 // rows add in sweep order, bottom row first. The wavefronts' sums are added
 // in a fixed order at the end. Otherwise both travel along the rows with DPP
 // shifts.
-template <typename T, int ROWS, int SRC, bool PEN, bool BAND, int PF, bool LC>
-__global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_bwd_kernel(UdtwArgs<T> a) {
+template <typename T, int ROWS, int SRC, bool PEN, bool BAND, int PF, bool LC, bool RD = false,
+          bool MW = false>
+__global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true, MW>::value)) udtw_bwd_kernel(UdtwArgs<T> a) {
+  // (fused only where written as fma, as in the forward)
+#pragma clang fp contract(off)
   extern __shared__ __align__(16) unsigned char smem_raw[];
   constexpr int ES = sizeof(T);
+  // RT: the type R and E = R - C are carried in (as the forward's R plane)
+  using RT = std::conditional_t<RD, double, T>;
+  constexpr int RES = sizeof(RT);
+  static_assert(!RD || (sizeof(T) == 4 && ROWS == 1), "RD: float, one row per thread");
+  const RT RINF = inf_v<RT>();
   constexpr bool COLS = SRC != SRC_COST;
   constexpr bool FLOW = COLS && !LC;
   static_assert(!LC || (COLS && ROWS == 1), "LDS columns need one row per thread");
+  static_assert(!MW || (ROWS == 1 && !LC), "MW: one row per thread");
   const int N = a.N, M = a.M;
-  const int b = blockIdx.x;
+  // MW: G groups of kMwRows rows per pair, aligned to the bottom (the last
+  // ends at row N-1, the first may be partial); group grp has gsh groups
+  // below it. The group below runs first, so it has the lower index.
+  const int G = MW ? a.groups : 1;
+  const int b = MW ? (int)blockIdx.x / G : (int)blockIdx.x;
+  const int gsh = MW ? (int)blockIdx.x % G : 0;
+  const int grp = G - 1 - gsh;
+  const int rbot = N - 1 - kMwRows * gsh;   // MW: this group's last row
   const int tid = threadIdx.x, lane = tid & 63, nw = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const T INF = inf_v<T>();
@@ -626,14 +730,15 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
 
   // Rows are bottom-aligned: row N-1 is the last row of the last wavefront,
   // where every column enters the backward sweep.
-  const int row0 = tid * ROWS - ((int)blockDim.x * ROWS - N);
+  const int row0 = tid * ROWS - ((int)blockDim.x * ROWS - N) - (MW ? kMwRows * gsh : 0);
 
   // box[(v + 1) * kBox + slot]: wavefront v's inbox, the row below its last
   // row: (E, G, H, A) and (y, hy, dy sum, dvy sum); box[0..kBox) is
   // wavefront 0's unread outbox. Then the dump area.
-  Rec8<T>* box = reinterpret_cast<Rec8<T>*>(smem_raw);
-  Rec8<T>* dump = box + (nw + 1) * kBox;
-  const Rec8<T> rec0 = {{-INF, (T)0, (T)0, (T)0}, {(T)0, (T)0.5, (T)0, (T)0}};
+  using Rec = BwdRec<T, RD>;
+  Rec* box = reinterpret_cast<Rec*>(smem_raw);
+  Rec* dump = box + (nw + 1) * kBox;
+  const Rec rec0 = {{-RINF, (T)0, (T)0, (T)0}, {(T)0, (T)0.5, (T)0, (T)0}};
   for (int t = tid; t < (nw + 1) * kBox; t += blockDim.x) box[t] = rec0;
   // LC: column operands, then per wavefront the (dy, dvy) sums (same indexing)
   const int cpad = col_pad(N, nw), ncol = M + 2 * cpad;
@@ -653,7 +758,7 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
   }
 
   Buf bR, bP, bC, bQ, bdC, bdQ, bY, bVY, bdY, bdVY;
-  bR.init(a.R + b * NM, NM);
+  bR.init(reinterpret_cast<const RT*>(a.R) + b * NM, NM);
   if (PEN) bP.init(a.P + b * NM, NM);
   if (SRC != SRC_FEAT1) {
     bC.init(a.C + b * NM, NM);
@@ -679,15 +784,16 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
   auto col_vy = [&](int vcol) -> T { return COLS ? bVY.ld<T>(vcol, 0) : (T)1; };
 
   const bool last_wave = wave == nw - 1;
-  Rec8<T>* const inbox = box + (wave + 1) * kBox;
-  Rec8<T>* const outbox = box + wave * kBox;
-  Rec8<T>* const my_out = lane == 0 ? outbox : dump + lane;
+  Rec* const inbox = box + (wave + 1) * kBox;
+  Rec* const outbox = box + wave * kBox;
+  Rec* const my_out = lane == 0 ? outbox : dump + lane;
   __syncthreads();
 
   T xr[ROWS], hxr[ROWS], dxr[ROWS], dvr[ROWS];
-  T e1[ROWS], e2[ROWS], g1[ROWS], g2[ROWS], h1[ROWS], h2[ROWS], a1[ROWS], a2[ROWS];
+  RT e1[ROWS], e2[ROWS];
+  T g1[ROWS], g2[ROWS], h1[ROWS], h2[ROWS], a1[ROWS], a2[ROWS];
   T yc[ROWS], hyc[ROWS], cy[ROWS], cvy[ROWS];
-  int vst[ROWS], vnat[ROWS], jb[ROWS], vrow0[ROWS];
+  int vst[ROWS], vsr[ROWS], vnat[ROWS], jb[ROWS], vrow0[ROWS];
 #pragma unroll
   for (int k = 0; k < ROWS; ++k) {
     const int i = row0 + k;
@@ -695,23 +801,27 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
     xr[k] = (SRC == SRC_FEAT1 && in) ? a.X[(size_t)b * N + i] : (T)0;
     hxr[k] = (COLS && in) ? half_var(a, a.VX[(size_t)b * N + i]) : (T)0.5;
     dxr[k] = dvr[k] = (T)0;
-    e1[k] = e2[k] = -INF;
+    e1[k] = e2[k] = -RINF;
     g1[k] = g2[k] = h1[k] = h2[k] = a1[k] = a2[k] = (T)0;
     yc[k] = cy[k] = cvy[k] = (T)0;
     hyc[k] = (T)0.5;
     vst[k] = in ? i * ES : 0;
+    vsr[k] = in ? i * RES : 0;
     vnat[k] = in ? i * (M - 1) * ES : 0;
     jb[k] = in ? -i : INT_MIN / 2;
-    vrow0[k] = i == 0 ? 0 : kOob;   // the row that stores finished columns
+    // the row that stores finished columns (MW: in the top group only; the
+    // other groups hand their column sums up with the boundary records)
+    vrow0[k] = (i == 0 && (!MW || grp == 0)) ? 0 : kOob;
   }
   // Row below the last row on the two previous diagonals. The virtual cell
   // (N, M) on diagonal Dn+1 is given E = Rh(N-1, M-1), A = P(N-1, M-1) and the
   // incoming gradients, so the recursion yields grad_dist / grad_pen at
   // (N-1, M-1) without a special case.
-  T ne1 = -INF, ne2 = -INF, ng1 = 0, ng2 = 0, nh1 = 0, nh2 = 0, na1 = 0, na2 = 0;
-  if (last_wave && lane == 63) {
+  RT ne1 = -RINF, ne2 = -RINF;
+  T ng1 = 0, ng2 = 0, nh1 = 0, nh2 = 0, na1 = 0, na2 = 0;
+  if (last_wave && lane == 63 && gsh == 0) {
     const int so = (int)(NM - 1) * ES;
-    ne1 = bR.ld<T>(0, so);
+    ne1 = bR.ld<RT>(0, (int)(NM - 1) * RES);
     ng1 = a.gr[(size_t)b * a.gstride];
     if (PEN) {
       nh1 = a.gp[(size_t)b * a.gstride];
@@ -719,19 +829,26 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
     }
   }
 
-  const int d_first = Dn - 1 + kLag * (nw - 1 - wave);
-  const int steps = (Dn + kLag * (nw - 1) + kSlots - 1) / kSlots * kSlots;
+  const int d_first = Dn - 1 + kLag * (nw - 1 - wave) + (MW ? kGroupLag * gsh : 0);
+  const int steps =
+      (Dn + kLag * (nw - 1) + (MW ? kGroupLag * (G - 1) : 0) + kSlots - 1) / kSlots * kSlots;
+  // MW: the top row of a group above the bottom one publishes its records
+  const bool publish = MW && grp > 0 && wave == 0 && !a.drop_handoff;
+  constexpr int HW = HandRec<T, RD>::words;
+  constexpr int HWS = hand_words(ES);
 
-  T rr[PF][ROWS], rp[PF][ROWS], rc[PF][ROWS], rq[PF][ROWS];
+  RT rr[PF][ROWS];
+  T rp[PF][ROWS], rc[PF][ROWS], rq[PF][ROWS];
   constexpr bool VEC = SRC == SRC_COST && PF == kSlots;   // block-wide C / Q loads
-  // R, P of diagonal d at byte soffset so_d = soff(d) * ES (diagonal-major),
-  // C, Q at so_n = max(d, 0) * ES ([N, M])
-  auto fetch = [&](int d, int so_d, int so_n, T* r, T* p, T* c, T* q) {
+  // R, P of diagonal d at byte soffset so_d = soff(d) * ES (diagonal-major;
+  // R at the same cell of its RES-byte plane), C, Q at so_n = max(d, 0) * ES
+  // ([N, M])
+  auto fetch = [&](int d, int so_d, int so_n, RT* r, T* p, T* c, T* q) {
 #pragma unroll
     for (int k = 0; k < ROWS; ++k) {
       const bool v = (unsigned)(d + jb[k]) < (unsigned)M;
       const int vd = v ? vst[k] : kOob;
-      r[k] = bR.ld<T>(vd, so_d);
+      r[k] = bR.ld<RT>(v ? vsr[k] : kOob, so_d * (RES / ES));
       if (PEN) p[k] = bP.ld<T>(vd, so_d);
       if (SRC == SRC_SQ) {
         c[k] = bC.ld<T>(vd, so_d);   // diagonal-major, as R
@@ -798,7 +915,9 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
     // EDGE: ring slot u of a trip holds column M-1-t0-u, the one entering row
     // N-1 on that step's diagonal
     T ey_ring[kSlots], evy_ring[kSlots];
-    int vcol = (M - 1) * ES;   // EDGE: byte offset of column M-1-t0
+    // EDGE: byte offset of column M-1-t0 (MW: the column entering row rbot
+    // on the group's first diagonal)
+    int vcol = (M - 1 + (MW ? (kGroupLag + kMwRows) * gsh : 0)) * ES;
     if (EDGE && FLOW) {
 #pragma unroll
       for (int u = 0; u < kSlots; ++u) {
@@ -812,7 +931,7 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
     ColRec<T>* const arow = acc + wave * ncol + cpad - row0;
     ColRec<T> creg[2];
     if (LC) creg[0] = crow[d_first];
-    Rec8<T> carry = rec0;   // the record used by the first step of the next block
+    Rec carry = rec0;   // the record used by the first step of the next block
     __builtin_amdgcn_s_waitcnt(0);   // drain the set-up loads (as in the forward)
     for (int tw = 0; tw < steps; tw += kWindow) {
       // lane l: byte soffsets of step tw + l (fetch of R / P and C / Q, and
@@ -824,11 +943,72 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
       // SRC_SQ: the diagonal-major soffset of the step's own diagonal (dS store)
       const int so_sd = SRC == SRC_SQ ? diag_soff(dl, N, M) * ES : 0;
       const int tn = min(kWindow, steps - tw);
+      // MW, edge wavefront of a group above the bottom one: lane l holds the
+      // record of the row below (the next group's top row) on diagonal
+      // dl + 1, i.e. of its cell in column dl - rbot
+      RT wn_e = -RINF;
+      T wn_g = (T)0, wn_h = (T)0, wn_a = (T)0, wn_cy = (T)0, wn_cvy = (T)0;
+      if (MW && EDGE && gsh > 0) {
+        const int jc = dl - rbot;
+        const bool v = (unsigned)jc < (unsigned)M;
+        const unsigned long long* w =
+            a.hand + ((size_t)(b * (G - 1) + grp) * M + (v ? jc : 0)) * HWS;
+        unsigned long long x[HW];
+#pragma unroll
+        for (int q = 0; q < HW; ++q) x[q] = kHandSentinel;
+        bool gave_up = false;
+        const unsigned long long t0w = __builtin_amdgcn_s_memrealtime();
+        for (int spin = 0;; ++spin) {
+          bool pend = false;
+          if (v) {
+#pragma unroll
+            for (int q = 0; q < HW; ++q) {
+              x[q] = __hip_atomic_load(w + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              pend = pend || x[q] == kHandSentinel;
+            }
+          }
+          if (__ballot(pend) == 0) break;
+          if (wait_ran_out(a, spin, t0w)) {
+            gave_up = true;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(4);
+        }
+        // as in the forward: report a wait that ran out and go on (the
+        // sentinel words decode to NaNs, which flow into the gradients)
+        if (gave_up && lane == 0)
+          __hip_atomic_fetch_or(a.status, TW_STATUS_WAIT_GAVE_UP, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+        if (v) {
+          if constexpr (sizeof(T) == 8) {
+            wn_e = word_to_d(x[0]);
+            wn_g = word_to_d(x[1]);
+            wn_h = word_to_d(x[2]);
+            wn_a = word_to_d(x[3]);
+            wn_cy = word_to_d(x[4]);
+            wn_cvy = word_to_d(x[5]);
+          } else if constexpr (RD) {
+            wn_e = word_to_d(x[0]);
+            wn_g = word_lo(x[1]);
+            wn_h = word_hi(x[1]);
+            wn_a = word_lo(x[2]);
+            wn_cy = word_hi(x[2]);
+            wn_cvy = word_lo(x[3]);
+          } else {
+            wn_e = word_lo(x[0]);
+            wn_g = word_hi(x[0]);
+            wn_h = word_lo(x[1]);
+            wn_a = word_hi(x[1]);
+            wn_cy = word_lo(x[2]);
+            wn_cvy = word_hi(x[2]);
+          }
+        }
+      }
     for (int t0 = 0; t0 < tn; t0 += kSlots) {
       const int half = (t0 / kSlots) & 1;   // mailbox half of this block
-      Rec8<T> rec[kSlots];
+      Rec rec[kSlots];
       if (!EDGE) {
-        const Rec8<T>* prev = inbox + (half ^ 1) * kSlots;
+        const Rec* prev = inbox + (half ^ 1) * kSlots;
         rec[0] = carry;
 #pragma unroll
         for (int u = 1; u < kSlots; ++u) {
@@ -838,7 +1018,7 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
         carry.a = prev[kSlots - 1].a;
         if (FLOW) carry.b = prev[kSlots - 1].b;
       }
-      Rec8<T>* const out = my_out + half * kSlots;
+      Rec* const out = my_out + half * kSlots;
       // LC: entries of the block's diagonals (and the next one) at
       // non-negative offsets from the diagonal below the block's last
       const int dlo = d_first - tw - t0 - kSlots;
@@ -859,7 +1039,8 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
       bool skip = false;
       if (BAND) {
         const int bhi = d_first - tw - t0, blo = bhi - (kSlots - 1);
-        const int wlo = wave * 64 * ROWS - ((int)blockDim.x * ROWS - N);
+        const int wlo =
+            wave * 64 * ROWS - ((int)blockDim.x * ROWS - N) - (MW ? kMwRows * gsh : 0);
         skip = (T)(2 * wlo - bhi) > a.band || (T)(blo - 2 * (wlo + 64 * ROWS - 1)) > a.band;
       }
 #pragma unroll
@@ -874,7 +1055,8 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
           csum = ablk[kSlots - u];
           __builtin_amdgcn_sched_barrier(0);
         }
-        T cr[ROWS], cp[ROWS], cc[ROWS], cq[ROWS];
+        RT cr[ROWS];
+        T cp[ROWS], cc[ROWS], cq[ROWS];
   #pragma unroll
         for (int k = 0; k < ROWS; ++k) {
           cr[k] = rr[u % PF][k];
@@ -884,9 +1066,14 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
         }
         // the row below the last row on diagonal d+1, and the column entering
         // the last row on diagonal d
-        Rec8<T> ex;
-        if (EDGE)
-          ex = {{-INF, (T)0, (T)0, (T)0},
+        Rec ex;
+        if (EDGE && MW)   // (the bottom group's window values are the virtual row's)
+          ex = {{lane_val(wn_e, t0 + u), lane_val(wn_g, t0 + u), lane_val(wn_h, t0 + u),
+                 lane_val(wn_a, t0 + u)},
+                {ey_ring[u], COLS ? half_var(a, evy_ring[u]) : (T)0.5,
+                 lane_val(wn_cy, t0 + u), lane_val(wn_cvy, t0 + u)}};
+        else if (EDGE)
+          ex = {{-RINF, (T)0, (T)0, (T)0},
                 {ey_ring[u], COLS ? half_var(a, evy_ring[u]) : (T)0.5, (T)0, (T)0}};
         else
           ex = rec[u];
@@ -895,21 +1082,23 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
         ng2 = ng1;
         nh2 = nh1;
         na2 = na1;
+        constexpr bool ZF = EDGE && !MW;   // the edge's row below is zero
         ne1 = shift_next(e1[0], ex.a.x);
-        ng1 = EDGE ? shift_next0(g1[0]) : shift_next(g1[0], ex.a.y);
+        ng1 = ZF ? shift_next0(g1[0]) : shift_next(g1[0], (T)ex.a.y);
         if (PEN) {
-          nh1 = EDGE ? shift_next0(h1[0]) : shift_next(h1[0], ex.a.z);
-          na1 = EDGE ? shift_next0(a1[0]) : shift_next(a1[0], ex.a.w);
+          nh1 = ZF ? shift_next0(h1[0]) : shift_next(h1[0], (T)ex.a.z);
+          na1 = ZF ? shift_next0(a1[0]) : shift_next(a1[0], (T)ex.a.w);
         }
         if (LC) {
           yc[0] = creg[u & 1].y;
           hyc[0] = creg[u & 1].hy;
         } else if (COLS) {
           const T fy = SRC != SRC_FEAT1 ? (T)0
-                       : shift_next(yc[0], EDGE ? uniform(ex.b.x) : ex.b.x);
-          const T fhy = shift_next(hyc[0], EDGE ? uniform(ex.b.y) : ex.b.y);
-          const T fcy = SRC != SRC_FEAT1 ? (T)0 : EDGE ? shift_next0(cy[0]) : shift_next(cy[0], ex.b.z);
-          const T fcvy = EDGE ? shift_next0(cvy[0]) : shift_next(cvy[0], ex.b.w);
+                       : shift_next(yc[0], EDGE ? uniform((T)ex.b.x) : (T)ex.b.x);
+          const T fhy = shift_next(hyc[0], EDGE ? uniform((T)ex.b.y) : (T)ex.b.y);
+          const T fcy = SRC != SRC_FEAT1 ? (T)0
+                        : ZF ? shift_next0(cy[0]) : shift_next(cy[0], (T)ex.b.z);
+          const T fcvy = ZF ? shift_next0(cvy[0]) : shift_next(cvy[0], (T)ex.b.w);
   #pragma unroll
           for (int k = 0; k + 1 < ROWS; ++k) {
             yc[k] = yc[k + 1];
@@ -924,7 +1113,8 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
         }
 
         const int so_n = __builtin_amdgcn_readlane(so_st, t0 + u);
-        T xe[ROWS], xg[ROWS], xh[ROWS], xa[ROWS];
+        RT xe[ROWS];
+        T xg[ROWS], xh[ROWS], xa[ROWS];
   #pragma unroll
         for (int k = 0; k < ROWS; ++k) {
           const bool valid = (unsigned)(d + jb[k]) < (unsigned)M;
@@ -933,10 +1123,10 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
           // forward left at INF
           T g = (T)0, h = (T)0, dsq = (T)0, df = (T)0, dvar = (T)0;
           if (BAND && skip) {
-            xe[k] = -INF;
+            xe[k] = -RINF;
             xa[k] = (T)0;
           } else {
-          const T rk = valid ? cr[k] : INF;
+          const RT rk = valid ? cr[k] : RINF;
           const T pk = cp[k];
           T ch, q = (T)0, c = (T)0, rv = (T)1, sq_raw = (T)0, var_raw = (T)1;
           if (SRC == SRC_COST) {
@@ -958,32 +1148,33 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
             if (PEN) q = a.beta_ln2 * lg2(var);
           }
           // successors: down (i+1, j) and right (i, j+1) on d+1, diagonal (i+1, j+1) on d+2
-          const T edn = (k + 1 < ROWS) ? e1[k + 1] : ne1;
+          const RT edn = (k + 1 < ROWS) ? e1[k + 1] : ne1;
           const T gdn = (k + 1 < ROWS) ? g1[k + 1] : ng1;
-          const T edg = (k + 1 < ROWS) ? e2[k + 1] : ne2;
+          const RT edg = (k + 1 < ROWS) ? e2[k + 1] : ne2;
           const T gdg = (k + 1 < ROWS) ? g2[k + 1] : ng2;
-          const T wdn = ex2(edn - rk), wrt = ex2(e1[k] - rk), wdg = ex2(edg - rk);
-          g = wdn * gdn + wrt * g1[k] + wdg * gdg;
+          const T wdn = ex2((T)(edn - rk)), wrt = ex2((T)(e1[k] - rk)), wdg = ex2((T)(edg - rk));
+          g = fma(wdg, gdg, fma(wrt, g1[k], wdn * gdn));
           if (PEN) {
             const T hdn = (k + 1 < ROWS) ? h1[k + 1] : nh1;
             const T adn = (k + 1 < ROWS) ? a1[k + 1] : na1;
             const T hdg = (k + 1 < ROWS) ? h2[k + 1] : nh2;
             const T adg = (k + 1 < ROWS) ? a2[k + 1] : na2;
             const T wh_dn = wdn * hdn, wh_rt = wrt * h1[k], wh_dg = wdg * hdg;
-            g -= (wh_dn * (pk - adn) + wh_rt * (pk - a1[k]) + wh_dg * (pk - adg)) * a.inv_gamma;
+            const T cpen = fma(wh_dg, pk - adg, fma(wh_rt, pk - a1[k], wh_dn * (pk - adn)));
+            g = fma(-cpen, a.inv_gamma, g);
             h = wh_dn + wh_rt + wh_dg;
           }
           // outside the grid, and (band) at unreachable cells, nothing flows
           bool live = valid;
-          if (BAND) live = live && rk < INF;
+          if (BAND) live = live && rk < RINF;
           g = live ? g : (T)0;
           h = live ? h : (T)0;
-          xe[k] = live ? rk - ch : -INF;
+          xe[k] = live ? rk - (RT)ch : -RINF;
           xa[k] = valid ? pk - q : (T)0;
           if (SRC != SRC_COST) {
             dsq = sq_raw > (T)0 ? g * rv : (T)0;
             if (SRC == SRC_FEAT1) df = valid ? (T)2 * dsq * (xr[k] - yc[k]) : (T)0;
-            dvar = var_raw > a.eps ? (T)0.5 * (a.beta * h - g * c) * rv : (T)0;
+            dvar = var_raw > a.eps ? (T)0.5 * fma(a.beta, h, -(g * c)) * rv : (T)0;
             dvar = valid ? dvar : (T)0;
           }
           }
@@ -1037,6 +1228,34 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
         } else {
           out[u].a = {e1[0], g1[0], h1[0], a1[0]};
         }
+        if (MW && publish) {
+          // the group above's row below: this row's record of diagonal d
+          const int j = d - row0;
+          if (lane == 0 && (unsigned)j < (unsigned)M) {
+            unsigned long long* w = a.hand + ((size_t)(b * (G - 1) + grp - 1) * M + j) * HWS;
+            unsigned long long x[HW];
+            if constexpr (sizeof(T) == 8) {
+              x[0] = word_d(e1[0]);
+              x[1] = word_d(g1[0]);
+              x[2] = word_d(h1[0]);
+              x[3] = word_d(a1[0]);
+              x[4] = word_d(cy[0]);
+              x[5] = word_d(cvy[0]);
+            } else if constexpr (RD) {
+              x[0] = word_d(e1[0]);
+              x[1] = pack_ff(g1[0], h1[0]);
+              x[2] = pack_ff(a1[0], cy[0]);
+              x[3] = pack_ff(cvy[0], 0.0f);
+            } else {
+              x[0] = pack_ff(e1[0], g1[0]);
+              x[1] = pack_ff(h1[0], a1[0]);
+              x[2] = pack_ff(cy[0], cvy[0]);
+            }
+#pragma unroll
+            for (int q = 0; q < HW; ++q)
+              __hip_atomic_store(w + q, x[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
       }
       block_barrier();
       vcol -= kSlots * ES;
@@ -1075,7 +1294,7 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true>::value)) udtw_b
         a.dVY[(size_t)b * M + j] = a.sigma ? (T)2 * sy_in * svy : svy;
       }
     }
-  } else if (FLOW && a.sigma && vgrad) {
+  } else if (FLOW && a.sigma && vgrad && grp == 0) {
     // the sweep stored d/dv of every column; once all of its stores are
     // complete and visible, scale them to d/ds
     __threadfence();
@@ -1094,31 +1313,15 @@ struct Shape {
   int threads;
 };
 
-// Rows per thread and threads per pair for a grid with N rows (N <= M): one
-// row per thread up to the one-row kernels' thread limit (1024, or 512 in
-// float64), more rows per thread beyond (up to 16, 256 threads; 1024
-// threads at 16 rows).
+// Threads of a one-workgroup-per-pair sweep for a grid with N rows (N <= M):
+// one row per thread, up to the kernels' thread limit (1024 in float, 512 in
+// double); rows {0, 0} past it (those pairs run several workgroups).
 template <typename T>
 static Shape pick_shape(int N, bool backward) {
   const int one_row_max =
       backward ? MaxThreads<T, 1, false, true>::value : MaxThreads<T, 1, false, false>::value;
-  int rows = 1;
-  if (N > one_row_max)
-    while (rows < 16 && (N + rows - 1) / rows > 256) rows *= 2;
-  // tuning override: TORCHWARP_UDTW_ROWS = 1, 2, 4, 8 or 16 rows per thread,
-  // taken when the kernel's thread limit for that row count allows it
-  static const int forced = [] {
-    const char* e = getenv("TORCHWARP_UDTW_ROWS");
-    return e ? atoi(e) : 0;
-  }();
-  const int fmax = forced == 1 ? one_row_max : (forced >= 16 ? 1024 : 256);
-  if ((forced == 1 || forced == 2 || forced == 4 || forced == 8 || forced == 16) &&
-      (N + forced - 1) / forced <= fmax)
-    rows = forced;
-  int threads = (N + rows - 1) / rows;
-  if (threads > 1024) return {0, 0};
-  threads = ((threads + 63) / 64) * 64;
-  return {rows, threads};
+  if (N > one_row_max) return {0, 0};
+  return {1, ((N + 63) / 64) * 64};
 }
 
 // LDS of one workgroup: the mailbox rings and the dump area of the
@@ -1126,8 +1329,11 @@ static Shape pick_shape(int N, bool backward) {
 // LDS of a sweep: mailboxes and dump, then with LDS columns (lc) the column
 // entries and, in the backward, each wavefront's two column-sum arrays.
 template <typename T>
-static size_t udtw_lds(bool backward, int nw, bool lc, int N, int M) {
-  size_t n = (size_t)((nw + 1) * kBox + kDump) * (backward ? 8 : 4) * sizeof(T);
+static size_t udtw_lds(bool backward, int nw, bool lc, int N, int M, bool rd = false) {
+  // mailbox record bytes (RD: one double and float values)
+  const size_t rec = rd ? (backward ? sizeof(RecD8) : sizeof(RecD4))
+                        : (backward ? 8 : 4) * sizeof(T);
+  size_t n = (size_t)((nw + 1) * kBox + kDump) * rec;
   if (lc) {
     const size_t ncol = (size_t)M + 2 * (size_t)col_pad(N, nw);
     n += ncol * sizeof(ColRec<T>);
@@ -1145,9 +1351,10 @@ struct PrefetchDepth {
   static constexpr int value = ROWS <= 4 ? 4 : (ROWS == 8 ? 2 : 1);
 };
 
-// MW: the sentinel into the boundary rows (256 g - 1, g >= 1) of R and P.
-template <typename T>
-__global__ void __launch_bounds__(256) mw_fill(T* R, T* P, int B, int N, int M, int G) {
+// MW: the sentinel into the boundary rows (256 g - 1, g >= 1) of R (elements
+// of RT) and P (of T).
+template <typename T, typename RT>
+__global__ void __launch_bounds__(256) mw_fill(RT* R, T* P, int B, int N, int M, int G) {
   const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
   const long long per = (long long)(G - 1) * M;
   if (idx >= (long long)B * per) return;
@@ -1156,13 +1363,23 @@ __global__ void __launch_bounds__(256) mw_fill(T* R, T* P, int B, int N, int M, 
   const int g = 1 + (int)(rem / M), j = (int)(rem % M);
   const int row = g * kMwRows - 1;
   const size_t c = (size_t)b * N * M + diag_soff(row + j, N, M) + row;
-  T v;
-  if constexpr (sizeof(T) == 4)
-    v = __uint_as_float((unsigned)mw_sentinel_bits(4));
-  else
-    v = __longlong_as_double((long long)mw_sentinel_bits(8));
-  R[c] = v;
-  if (P) P[c] = v;
+  auto sentinel = [](auto zero) {
+    using V = decltype(zero);
+    if constexpr (sizeof(V) == 4)
+      return __uint_as_float((unsigned)mw_sentinel_bits(4));
+    else
+      return __longlong_as_double((long long)mw_sentinel_bits(8));
+  };
+  R[c] = sentinel(RT{});
+  if (P) P[c] = sentinel(T{});
+}
+
+// MW backward: every hand-off word to the sentinel.
+// (a template, so that every object including this header may instantiate it)
+template <int = 0>
+__global__ void __launch_bounds__(256) hand_fill(unsigned long long* w, long long n) {
+  const long long idx = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (idx < n) w[idx] = kHandSentinel;
 }
 
 // Several workgroups per pair for the forward when the batch leaves CUs
@@ -1172,89 +1389,146 @@ __global__ void __launch_bounds__(256) mw_fill(T* R, T* P, int B, int N, int M, 
 // so it keeps one workgroup per pair. TORCHWARP_UDTW_MW=0 turns MW off, 1
 // uses it for every source.
 constexpr long long kMwMaxGroups = 512;
-static inline bool mw_enabled(int src) {
+static inline int mw_mode() {
   static const int mode = [] {
     const char* e = getenv("TORCHWARP_UDTW_MW");
     return e ? atoi(e) : 2;
   }();
-  return mode == 1 || (mode == 2 && src != SRC_SQ);
+  const int forced = test_mw_mode();   // a test's choice, -1: none
+  return forced >= 0 ? forced : mode;
+}
+static inline bool mw_enabled(int src) {
+  return mw_mode() == 1 || (mw_mode() == 2 && src != SRC_SQ);
+}
+// Longer sequences than one workgroup holds at one row per thread (1024 rows
+// in float, 512 in double) run with several workgroups per pair in both
+// directions (TORCHWARP_UDTW_MW=0 keeps one workgroup per pair and so limits
+// the length to those rows).
+template <typename T>
+static inline bool mw_long(int N) {
+  return mw_mode() != 0 && N > MaxThreads<T, 1, false, false>::value;
+}
+// Several workgroups per pair in both directions: for sequences longer than
+// one workgroup holds, and, past one group of rows, whenever the batch has
+// fewer pairs than the device has CUs (one workgroup per pair would leave
+// CUs idle: at B = 64, N = M = 1024, D = 16 the step takes 1.98 ms with four
+// workgroups per pair against 2.29 ms with one); mode 1 splits every pair
+// past one group of rows.
+template <typename T>
+static inline bool mw_split(int B, int N) {
+  if (mw_long<T>(N)) return true;
+  if (N <= kMwRows || mw_mode() == 0) return false;
+  return mw_mode() == 1 || B < num_cus();
+}
+template <typename T>
+static inline bool mw_backward(int B, int N) {
+  return mw_split<T>(B, N);
+}
+// Hand-off workspace of the MW backward (bytes): 0 when it runs one
+// workgroup per pair.
+template <typename T>
+static inline size_t mw_hand_bytes(int B, int N, int M) {
+  if (!mw_backward<T>(B, N)) return 0;
+  const long long G = (N + kMwRows - 1) / kMwRows;
+  return (size_t)B * (size_t)(G - 1) * (size_t)M * hand_words(sizeof(T)) * 8;
+}
+
+// One-row-per-thread kernels (LDS columns, several workgroups per pair, or
+// columns by DPP) with R carried in T or, for float with RD, in double.
+template <typename T, int SRC, bool PEN, bool BAND, bool RD>
+static int launch_one_row(bool backward, const UdtwArgs<T>& a, int B, const Shape& sh,
+                          bool longseq, hipStream_t stream, const char* what) {
+  const int nw = sh.threads / 64;
+  dim3 grid(B), block(sh.threads);
+  // one row per thread with column operands: stage the columns in LDS when
+  // they fit in a quarter of it (several workgroups per CU stay resident)
+  if constexpr (SRC != SRC_COST) {
+    const size_t lc_lds = udtw_lds<T>(backward, nw, true, a.N, a.M, RD);
+    if (!longseq && sh.threads <= 256 && lc_lds <= (size_t)max_lds_bytes() / 4) {
+      if (backward)
+        hipLaunchKernelGGL(
+            (udtw_bwd_kernel<T, 1, SRC, PEN, BAND, PrefetchDepth<1>::value, true, RD>), grid,
+            block, lc_lds, stream, a);
+      else
+        hipLaunchKernelGGL(
+            (udtw_fwd_kernel<T, 1, SRC, PEN, BAND, PrefetchDepth<1>::value, true, false, RD>),
+            grid, block, lc_lds, stream, a);
+      return check_launch(what);
+    }
+  }
+  const int G = (a.N + kMwRows - 1) / kMwRows;
+  const bool mw = G > 1 && (longseq || mw_split<T>(B, a.N) ||
+                            (!backward && !BAND && (long long)B * G <= kMwMaxGroups &&
+                             mw_enabled(SRC)));
+  if (mw) {
+    using RT = std::conditional_t<RD, double, T>;
+    UdtwArgs<T> m = a;
+    m.groups = G;
+    m.status = status_word();
+    if (!m.status) return fail(TW_ELAUNCH, "%s: no device status word", what);
+    m.spins = wait_spins(kMwSpins);
+    m.wait_ticks = (unsigned long long)(kMwWaitSeconds * 1e3 * realtime_khz());
+    m.drop_handoff = wait_drop_handoff();
+    const size_t mlds = udtw_lds<T>(backward, kMwRows / 64, false, a.N, a.M, RD);
+    const dim3 mgrid((unsigned)((long long)B * G)), mblock(kMwRows);
+    if (backward) {
+      if (!m.hand) return fail(TW_ESIZE, "%s: internal: no hand-off workspace", what);
+      const long long words = (long long)B * (G - 1) * a.M * hand_words(sizeof(T));
+      hipLaunchKernelGGL((hand_fill<>), dim3((unsigned)((words + 255) / 256)), dim3(256), 0,
+                         stream, m.hand, words);
+      hipLaunchKernelGGL(
+          (udtw_bwd_kernel<T, 1, SRC, PEN, BAND, PrefetchDepth<1>::value, false, RD, true>),
+          mgrid, mblock, mlds, stream, m);
+    } else {
+      const long long fills = (long long)B * (G - 1) * a.M;
+      hipLaunchKernelGGL((mw_fill<T, RT>), dim3((unsigned)((fills + 255) / 256)), dim3(256), 0,
+                         stream, reinterpret_cast<RT*>(m.R), PEN ? m.P : (T*)nullptr, B, a.N,
+                         a.M, G);
+      hipLaunchKernelGGL(
+          (udtw_fwd_kernel<T, 1, SRC, PEN, BAND, PrefetchDepth<1>::value, false, true, RD>),
+          mgrid, mblock, mlds, stream, m);
+    }
+    return check_launch(what);
+  }
+  const size_t lds = udtw_lds<T>(backward, nw, false, a.N, a.M, RD);
+  if (lds > (size_t)max_lds_bytes()) {
+    return fail(TW_ESIZE, "%s: %zu bytes of LDS needed, %d available", what, lds,
+                max_lds_bytes());
+  }
+  // (RD backward at up to 1024 threads: a ring two diagonals deep keeps its
+  // doubles within the 128 registers a lane has there)
+  if (backward)
+    hipLaunchKernelGGL(
+        (udtw_bwd_kernel<T, 1, SRC, PEN, BAND, RD ? 2 : PrefetchDepth<1>::value, false, RD>),
+        grid, block, lds, stream, a);
+  else
+    hipLaunchKernelGGL(
+        (udtw_fwd_kernel<T, 1, SRC, PEN, BAND, PrefetchDepth<1>::value, false, false, RD>), grid,
+        block, lds, stream, a);
+  return check_launch(what);
 }
 
 template <typename T, int SRC, bool PEN, bool BAND>
 static int launch_udtw(bool backward, const UdtwArgs<T>& a, int B, hipStream_t stream,
                        const char* what) {
   if (B == 0) return TW_OK;
-  const Shape sh = pick_shape<T>(a.N, backward);
+  // planes are addressed with 32-bit byte offsets within a pair
+  const long long rbytes = a.rd ? 8 : (long long)sizeof(T);
+  if ((long long)a.N * a.M * rbytes >= (1LL << 31)) {
+    return fail(TW_ESIZE, "%s: one pair's N*M matrix (%d x %d) must stay below 2 GiB", what,
+                a.N, a.M);
+  }
+  const bool longseq = mw_long<T>(a.N);
+  const Shape sh = longseq ? Shape{1, kMwRows} : pick_shape<T>(a.N, backward);
   if (sh.rows == 0) {
-    return fail(TW_ESIZE, "%s: the shorter sequence has %d steps; this build handles up to 16384",
-                what, a.N);
+    return fail(TW_ESIZE, "%s: the shorter sequence has %d steps; one workgroup per pair "
+                "(TORCHWARP_UDTW_MW=0) holds up to %d", what, a.N,
+                MaxThreads<T, 1, false, false>::value);
   }
-  if ((long long)a.N * a.M * (long long)sizeof(T) >= (1LL << 31)) {
-    return fail(TW_ESIZE, "%s: one pair's N*M matrix must stay below 2 GiB", what);
+  if constexpr (sizeof(T) == 4) {
+    if (a.rd) return launch_one_row<T, SRC, PEN, BAND, true>(backward, a, B, sh, longseq, stream, what);
   }
-  const int nw = sh.threads / 64;
-  dim3 grid(B), block(sh.threads);
-  // one row per thread with column operands: stage the columns in LDS when
-  // they fit in a quarter of it (several workgroups per CU stay resident)
-  if constexpr (SRC != SRC_COST) {
-    const size_t lc_lds = udtw_lds<T>(backward, nw, true, a.N, a.M);
-    if (sh.rows == 1 && sh.threads <= 256 && lc_lds <= (size_t)max_lds_bytes() / 4) {
-      if (backward)
-        hipLaunchKernelGGL((udtw_bwd_kernel<T, 1, SRC, PEN, BAND, PrefetchDepth<1>::value, true>),
-                           grid, block, lc_lds, stream, a);
-      else
-        hipLaunchKernelGGL((udtw_fwd_kernel<T, 1, SRC, PEN, BAND, PrefetchDepth<1>::value, true>),
-                           grid, block, lc_lds, stream, a);
-      return check_launch(what);
-    }
-  }
-  if constexpr (!BAND) {
-    const int G = (a.N + kMwRows - 1) / kMwRows;
-    if (!backward && sh.rows == 1 && G > 1 && (long long)B * G <= kMwMaxGroups &&
-        mw_enabled(SRC)) {
-      UdtwArgs<T> m = a;
-      m.groups = G;
-      m.status = status_word();
-      if (!m.status) return fail(TW_ELAUNCH, "%s: no device status word", what);
-      m.spins = wait_spins(kMwSpins);
-      m.drop_handoff = wait_drop_handoff();
-      const long long fills = (long long)B * (G - 1) * a.M;
-      hipLaunchKernelGGL((mw_fill<T>), dim3((unsigned)((fills + 255) / 256)), dim3(256), 0,
-                         stream, m.R, PEN ? m.P : (T*)nullptr, B, a.N, a.M, G);
-      const size_t mlds = udtw_lds<T>(false, kMwRows / 64, false, a.N, a.M);
-      hipLaunchKernelGGL(
-          (udtw_fwd_kernel<T, 1, SRC, PEN, false, PrefetchDepth<1>::value, false, true>),
-          dim3((unsigned)(B * G)), dim3(kMwRows), mlds, stream, m);
-      return check_launch(what);
-    }
-  }
-  const size_t lds = udtw_lds<T>(backward, nw, false, a.N, a.M);
-  if (lds > (size_t)max_lds_bytes()) {
-    return fail(TW_ESIZE, "%s: %zu bytes of LDS needed, %d available", what, lds,
-                max_lds_bytes());
-  }
-#define TW_UDTW_CASE(R_)                                                                     \
-  case R_:                                                                                   \
-    if (backward)                                                                            \
-      hipLaunchKernelGGL(                                                                    \
-          (udtw_bwd_kernel<T, R_, SRC, PEN, BAND, PrefetchDepth<R_>::value, false>), grid,   \
-          block, lds, stream, a);                                                            \
-    else                                                                                     \
-      hipLaunchKernelGGL(                                                                    \
-          (udtw_fwd_kernel<T, R_, SRC, PEN, BAND, PrefetchDepth<R_>::value, false>), grid,   \
-          block, lds, stream, a);                                                            \
-    break;
-  switch (sh.rows) {
-    TW_UDTW_CASE(1)
-    TW_UDTW_CASE(2)
-    TW_UDTW_CASE(4)
-    TW_UDTW_CASE(8)
-    TW_UDTW_CASE(16)
-    default:
-      return fail(TW_EINVAL, "%s: internal: bad row count", what);
-  }
-#undef TW_UDTW_CASE
-  return check_launch(what);
+  return launch_one_row<T, SRC, PEN, BAND, false>(backward, a, B, sh, longseq, stream, what);
 }
 
 // One direction of the sweep for a cost source, with or without the penalty

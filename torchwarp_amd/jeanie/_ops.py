@@ -563,9 +563,11 @@ def fvm_backward(cost: Tensor, temporal: Tensor, R: Tensor, grad_out: Tensor, ga
     _hip.require(cost, backend, "FVM")
     c = cost.contiguous()
     B, K, T, U = c.shape
-    d, ws = torch.empty_like(c), c.new_empty(B, T * U)
+    es = c.element_size()
+    nws = -(-_hip.library().tw_fvm_workspace_bytes(B, K, T, U, es) // es)
+    d, ws = torch.empty_like(c), c.new_empty(nws)
     _hip.call("tw_fvm_cost_bwd", c.dtype, c, temporal, R, grad_out.to(c.dtype).contiguous(), B, K,
-              T, U, gamma, d, ws)
+              T, U, gamma, d, ws, nws * es)
     return d
 
 

@@ -40,7 +40,8 @@ def dp(cost: Tensor, penalty: Tensor, gamma: float, bandwidth: float,
     c = cost.contiguous()
     pen = penalty.numel() > 0
     q = penalty.to(c.dtype).contiguous() if pen else None
-    R = c.new_empty(B, N * M)
+    _hip.check_udtw_plane(N, M, gamma, c.dtype)
+    R = c.new_empty(B, _hip.carry_cols(N, M, gamma, c.dtype))
     P = c.new_empty(B, N * M) if pen else c.new_empty(0)
     out_r, out_p = c.new_empty(B), c.new_empty(B)
     _hip.call("tw_udtw_cost_fwd", c.dtype, c, q, B, N, M, gamma, bandwidth, R, P, out_r, out_p)
@@ -51,7 +52,8 @@ def dp(cost: Tensor, penalty: Tensor, gamma: float, bandwidth: float,
 def _(cost, penalty, gamma, bandwidth, backend):
     B, N, M = cost.shape
     P = cost.new_empty(B, N * M) if penalty.numel() else cost.new_empty(0)
-    return cost.new_empty(B), cost.new_empty(B), cost.new_empty(B, N * M), P
+    R = cost.new_empty(B, _hip.carry_cols(N, M, gamma, cost.dtype))
+    return cost.new_empty(B), cost.new_empty(B), R, P
 
 
 @torch.library.custom_op("twamd_udtw::dp_backward", mutates_args=())
@@ -67,8 +69,10 @@ def dp_backward(cost: Tensor, penalty: Tensor, R: Tensor, P: Tensor, grad_r: Ten
     d_pen = torch.empty_like(c) if pen else c.new_empty(0)
     grads, gs = _hip.per_pair(*((grad_r.to(c.dtype), grad_p.to(c.dtype)) if pen
                                 else (grad_r.to(c.dtype),)))
+    nws = _hip.udtw_cost_workspace_elems(B, N, M, c.dtype)
+    ws = c.new_empty(nws) if nws else c.new_empty(0)
     _hip.call("tw_udtw_cost_bwd", c.dtype, c, q, R, P, grads[0], grads[1] if pen else None,
-              B, N, M, gamma, bandwidth, gs, d_cost, d_pen)
+              B, N, M, gamma, bandwidth, gs, d_cost, d_pen, *_ws_args(ws))
     return d_cost, d_pen
 
 
@@ -88,8 +92,14 @@ register_autocast(dp_backward)
 
 def _feat_ws(X, N, M):
     """The squared-distance plane [B, N*M] of D > 1 (empty for D == 1)."""
-    n = _hip.udtw_workspace_elems(X.shape[0], N, M, X.shape[2])
-    return X.new_empty(X.shape[0], N * M) if n else X.new_empty(0)
+    return X.new_empty(X.shape[0], N * M) if X.shape[2] > 1 else X.new_empty(0)
+
+
+def _feat_bwd_ws(X, N, M):
+    """The backward's workspace: the squared-distance plane (D > 1), then the
+    hand-off records of long sequences (empty when neither is needed)."""
+    n = _hip.udtw_workspace_elems(X.shape[0], N, M, X.shape[2], X.dtype)
+    return X.new_empty(n) if n else X.new_empty(0)
 
 
 def _ws_args(ws):
@@ -110,7 +120,8 @@ def fused(X: Tensor, Y: Tensor, vx: Tensor, vy: Tensor, gamma: float, beta: floa
     M = Y.shape[1]
     X, Y, vx, vy = _hip.dense(X.dtype, X, Y, vx, vy)
     pen = beta != 0.0
-    R = X.new_empty(B, N * M)
+    _hip.check_udtw_plane(N, M, gamma, X.dtype)
+    R = X.new_empty(B, _hip.carry_cols(N, M, gamma, X.dtype))
     P = X.new_empty(B, N * M) if pen else X.new_empty(0)
     out_r, out_p = X.new_empty(B), X.new_empty(B)
     S = _feat_ws(X, N, M)
@@ -124,7 +135,8 @@ def _(X, Y, vx, vy, gamma, beta, eps, bandwidth, backend, sigma):
     B, N, M = X.shape[0], X.shape[1], Y.shape[1]
     P = X.new_empty(B, N * M) if beta != 0.0 else X.new_empty(0)
     S = X.new_empty(B, N * M) if X.shape[2] > 1 else X.new_empty(0)
-    return X.new_empty(B), X.new_empty(B), X.new_empty(B, N * M), P, S
+    R = X.new_empty(B, _hip.carry_cols(N, M, gamma, X.dtype))
+    return X.new_empty(B), X.new_empty(B), R, P, S
 
 
 @torch.library.custom_op("twamd_udtw::fused_backward", mutates_args=())
@@ -139,8 +151,8 @@ def fused_backward(X: Tensor, Y: Tensor, vx: Tensor, vy: Tensor, R: Tensor, P: T
     pen = beta != 0.0
     dX, dY = torch.empty_like(X), torch.empty_like(Y)
     dvx, dvy = torch.empty_like(vx), torch.empty_like(vy)
-    ws = _feat_ws(X, N, M)
-    S = S if (ws.numel() and S.shape == ws.shape and S.dtype == ws.dtype
+    ws = _feat_bwd_ws(X, N, M)
+    S = S if (D > 1 and S.shape == (B, N * M) and S.dtype == X.dtype
               and S.is_contiguous()) else None
     grads, gs = _hip.per_pair(*(_hip.dense(X.dtype, grad_r, grad_p, contiguous=False) if pen
                                 else _hip.dense(X.dtype, grad_r, contiguous=False)))
