@@ -232,6 +232,23 @@ int tw_fvm_cost_bwd_f64(const double* cost, const double* temporal, const double
                         double* d_cost, double* workspace, size_t workspace_bytes,
                         hipStream_t stream);
 
+/* FVM backward that allocates nothing: as tw_fvm_cost_bwd_*, without the
+ * workspace argument. No counterpart in the reference; it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid allocation). Its scratch is a file-scope device array
+ * of tw_noalloc_scratch_bytes() bytes (16 MiB) that each device holds for the
+ * life of the process; calls needing more (tw_fvm_workspace_bytes > that
+ * size) return TW_ESIZE without launching. Every call on a device shares the
+ * array: calls that overlap on one device (other streams, other host
+ * threads) race. Calls no allocating routine. */
+size_t tw_noalloc_scratch_bytes(void);
+int tw_fvm_cost_bwd_noalloc_f32(const float* cost, const float* temporal, const float* R,
+                                const float* grad_out, int B, int K, int T, int U, float gamma,
+                                float* d_cost, hipStream_t stream);
+int tw_fvm_cost_bwd_noalloc_f64(const double* cost, const double* temporal, const double* R,
+                                const double* grad_out, int B, int K, int T, int U, double gamma,
+                                double* d_cost, hipStream_t stream);
+
 /* ------------------------------------------------------- pairwise cost --
  * A [P, R, D] against Bm [P, C, D] -> cost [P, R, C] with a TW_METRIC_*.
  * Replaces euclidean_cost / squared_euclidean_cost (jeanie/distances.py:15-38)

@@ -25,7 +25,7 @@ def _declared():
 def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(_hip.LIB_PATH))
     names = _declared()
-    assert len(names) == 38
+    assert len(names) == 41
     for name in names:
         assert hasattr(lib, name), name
     assert lib.tw_version() == 1
@@ -34,7 +34,8 @@ def test_library_exports_every_declared_symbol():
 def test_binding_covers_every_entry_point():
     bound = {"tw_version", "tw_last_error", "tw_udtw_feat_workspace_bytes", "tw_async_status",
              "tw_test_set_wait", "tw_udtw_carry_bytes",
-             "tw_udtw_cost_workspace_bytes", "tw_test_set_mw", "tw_fvm_workspace_bytes"}
+             "tw_udtw_cost_workspace_bytes", "tw_test_set_mw", "tw_fvm_workspace_bytes",
+             "tw_noalloc_scratch_bytes"}
     for base in _hip.SIGNATURES:
         bound |= {base + "_f32", base + "_f64"}
     bound |= {base + "_f64" for base in _hip.SIGNATURES_F64}
@@ -181,3 +182,15 @@ def test_carry_bytes_query():
     assert q(0, 5, 5, 1.0, 4) == 0
     assert _hip.carry_cols(1024, 1024, 0.1, torch.float32) == 2 * 1024 * 1024
     assert _hip.carry_cols(140, 140, 1.0, torch.float32) == 140 * 140
+
+
+def test_noalloc_entry_rejects_sizes_past_its_scratch():
+    """The FVM backward without allocation checks its fixed scratch before any
+    launch: 4096 pairs of 64 x 64 in float64 need 128 MiB of it."""
+    lib = _hip.library()
+    assert lib.tw_noalloc_scratch_bytes() == 16 << 20
+    rc = lib.tw_fvm_cost_bwd_noalloc_f64(None, None, None, None, 4096, 5, 64, 64, 0.1, None, None)
+    assert rc == 3   # TW_ESIZE
+    assert b"scratch" in lib.tw_last_error()
+    assert lib.tw_fvm_cost_bwd_noalloc_f32(None, None, None, None, 0, 5, 6, 7, 0.1, None,
+                                           None) == 0   # empty batch: no-op

@@ -28,6 +28,7 @@ SIGNATURES = {
     "tw_jeanie_feat_bwd": "ppppppiiiiiiiifippps",
     "tw_fvm_cost_fwd": "piiiifpppps",
     "tw_fvm_cost_bwd": "ppppiiiifppzs",
+    "tw_fvm_cost_bwd_noalloc": "ppppiiiifps",
     "tw_pair_cost_fwd": "ppiiiiips",
     "tw_pair_cost_bwd": "ppppiiiiipps",
     "tw_rbf_cost_fwd": "ppiiiifps",
@@ -67,6 +68,8 @@ def _load():
     lib.tw_version.restype = ctypes.c_int
     lib.tw_udtw_feat_workspace_bytes.restype = ctypes.c_size_t
     lib.tw_udtw_feat_workspace_bytes.argtypes = [ctypes.c_int] * 5
+    lib.tw_noalloc_scratch_bytes.restype = ctypes.c_size_t
+    lib.tw_noalloc_scratch_bytes.argtypes = []
     lib.tw_fvm_workspace_bytes.restype = ctypes.c_size_t
     lib.tw_fvm_workspace_bytes.argtypes = [ctypes.c_int] * 5
     lib.tw_udtw_cost_workspace_bytes.restype = ctypes.c_size_t

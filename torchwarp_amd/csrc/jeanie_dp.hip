@@ -772,6 +772,16 @@ int fvm_bwd(const T* C, const T* tmp, const T* R, const T* gout, int B, int K, i
   return check_launch(what);
 }
 
+template int fvm_bwd<float>(const float*, const float*, const float*, const float*, int, int,
+                            int, int, double, float*, float*, size_t, hipStream_t, const char*);
+template int fvm_bwd<double>(const double*, const double*, const double*, const double*, int,
+                             int, int, int, double, double*, double*, size_t, hipStream_t,
+                             const char*);
+size_t fvm_workspace_bytes(int B, int Tn, int Un, int es) {
+  return es == 4 ? fvm_ws_bytes<float>(B, Tn, Un, nullptr)
+                 : fvm_ws_bytes<double>(B, Tn, Un, nullptr);
+}
+
 // ------------------------------------------------------ JEANIE from features
 
 template <typename T>
