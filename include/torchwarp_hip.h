@@ -117,6 +117,42 @@ int tw_udtw_cost_bwd_f64(const double* cost, const double* pen, const double* R,
                          double* d_cost, double* d_pen, double* workspace,
                          size_t workspace_bytes, hipStream_t stream);
 
+/* Second order of the DP on precomputed matrices: the derivative of the
+ * backward's (d_cost, d_pen) along a direction (t_cost, t_pen, t_grad_dist,
+ * t_grad_pen), and the derivatives of (dist, pen) along (t_cost, t_pen).
+ * Replaces the reference's double backward and forward-mode rule of
+ * torchwarp_udtw::dp_backward (udtw/_ops.py:322-339 DPBackward.backward /
+ * jvp), which run torch.func over udtw/_autograd.py:32-74. Because
+ * (d_cost, d_pen) is a gradient, its Jacobian is symmetric: with
+ * t_grad_* = 0, (t_d_cost, t_d_pen) is also the vector-Jacobian product a
+ * double backward needs, and (t_dist, t_pen_sum) its gradients with respect
+ * to grad_dist and grad_pen.
+ * cost, pen, t_cost, t_pen, t_d_cost, t_d_pen: [B,N,M] (any N, M); pen NULL
+ * means no penalty (then t_pen, grad_pen, t_grad_pen, t_d_pen, t_pen_sum are
+ * unused); t_cost, t_pen, t_grad_* NULL mean zero; grad_dist, grad_pen,
+ * t_grad_*, t_dist, t_pen_sum: [B] (t_dist, t_pen_sum may be NULL). Same
+ * bandwidth convention as the forward. workspace:
+ * tw_udtw_tangent_workspace_bytes(B, N, M, pen != NULL, elem) bytes (the
+ * forward's R, P and their tangents, and for long sequences the diagonals
+ * the sweeps exchange).
+ * Currently switched off: after checking the arguments the calls return
+ * TW_EINVAL without launching (their first run on an MI355X stopped with a
+ * memory aperture violation whose cause is not yet found). */
+size_t tw_udtw_tangent_workspace_bytes(int B, int N, int M, int has_penalty, int elem_size);
+int tw_udtw_cost_tangent_f32(const float* cost, const float* pen, const float* t_cost,
+                             const float* t_pen, const float* grad_dist, const float* grad_pen,
+                             const float* t_grad_dist, const float* t_grad_pen, int B, int N,
+                             int M, float gamma, float bandwidth, float* t_d_cost,
+                             float* t_d_pen, float* t_dist, float* t_pen_sum, float* workspace,
+                             size_t workspace_bytes, hipStream_t stream);
+int tw_udtw_cost_tangent_f64(const double* cost, const double* pen, const double* t_cost,
+                             const double* t_pen, const double* grad_dist,
+                             const double* grad_pen, const double* t_grad_dist,
+                             const double* t_grad_pen, int B, int N, int M, double gamma,
+                             double bandwidth, double* t_d_cost, double* t_d_pen, double* t_dist,
+                             double* t_pen_sum, double* workspace, size_t workspace_bytes,
+                             hipStream_t stream);
+
 /* uDTW straight from the features, N <= M. Replaces udtw_cuda.cu:738-775
  * (fused_forward) / :777-814 (fused_backward) together with the bmm / vecdot /
  * diagonal permutations of the ops torchwarp_udtw::fused / fused_backward

@@ -22,6 +22,13 @@ reference's portable algorithms (paths relative to ``/root/reference``):
 * ``paths``  -- hard (gamma = 0) DP with the backtrack order of
   ``src/torchwarp/paths.py:85-127``.
 * ``brute``  -- brute-force enumeration of every monotone path (tiny sizes).
+* ``udtw_tangent`` -- the second order of the uDTW DP (the derivative of the
+  first-order gradient along a direction), what the reference's
+  ``DPBackward.backward`` / ``jvp`` compute with torch.func over
+  ``src/torchwarp/udtw/_autograd.py:32-74`` (``udtw/_ops.py:322-339``),
+  written as explicit tangent recursions.
+* ``udtw_ld`` -- the feature-path uDTW value and gradients in 80-bit
+  extended precision, the judge of float64 rounding.
 
 How each function is pinned (so that a dropped term, wrong sign, swapped
 index or transposed operand fails a check) -- see ``tests/test_oracle.py``:
@@ -33,7 +40,10 @@ index or transposed operand fails a check) -- see ``tests/test_oracle.py``:
   gradient = path-probability matrix, hard argmin path);
 * closed forms: 1x1 and 1xM grids, gamma -> 0 equals exact DTW, the
   normalize identity, K = 1 / shift 0 reduces JEANIE to soft-DTW;
-* the analytic backward against autograd of the differentiable form.
+* the analytic backward against autograd of the differentiable form;
+* for ``udtw_tangent`` (``tests/test_oracle_tangent.py``): the reference's
+  stored soft-DTW Hessian, double autograd through the differentiable form,
+  finite differences of the analytic backward, Hessian symmetry.
 
 Every function here is pinned by at least one of these; none is "parity
 unpinned".

@@ -25,7 +25,7 @@ def _declared():
 def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(_hip.LIB_PATH))
     names = _declared()
-    assert len(names) == 41
+    assert len(names) == 44
     for name in names:
         assert hasattr(lib, name), name
     assert lib.tw_version() == 1
@@ -35,7 +35,7 @@ def test_binding_covers_every_entry_point():
     bound = {"tw_version", "tw_last_error", "tw_udtw_feat_workspace_bytes", "tw_async_status",
              "tw_test_set_wait", "tw_udtw_carry_bytes",
              "tw_udtw_cost_workspace_bytes", "tw_test_set_mw", "tw_fvm_workspace_bytes",
-             "tw_noalloc_scratch_bytes"}
+             "tw_noalloc_scratch_bytes", "tw_udtw_tangent_workspace_bytes"}
     for base in _hip.SIGNATURES:
         bound |= {base + "_f32", base + "_f64"}
     bound |= {base + "_f64" for base in _hip.SIGNATURES_F64}
@@ -44,6 +44,14 @@ def test_binding_covers_every_entry_point():
 
 def test_workspace_query_is_host_only():
     lib = _hip.library()
+    # second-order sweeps: R, P and their tangents (4 planes; 2 without a
+    # penalty), plus the exchanged diagonals (3 x 8 values per row; 3 x 4)
+    # when they do not fit in the LDS
+    assert lib.tw_udtw_tangent_workspace_bytes(2, 3, 4, 1, 8) == 2 * 4 * 3 * 4 * 8
+    assert lib.tw_udtw_tangent_workspace_bytes(2, 3, 4, 0, 4) == 2 * 2 * 3 * 4 * 4
+    assert lib.tw_udtw_tangent_workspace_bytes(1, 3000, 3100, 1, 8) == \
+        (4 * 3000 * 3100 + 24 * 3000) * 8
+    assert lib.tw_udtw_tangent_workspace_bytes(0, 3, 4, 1, 8) == 0
     assert lib.tw_udtw_feat_workspace_bytes(2, 3, 4, 1, 4) == 0
     assert lib.tw_udtw_feat_workspace_bytes(2, 3, 4, 5, 4) == 2 * 3 * 4 * 4
     # past 1024 rows (float; 512 in double) the backward runs ceil(N / 256)

@@ -20,6 +20,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libtorchwarp_hip.so"
 SIGNATURES = {
     "tw_udtw_cost_fwd": "ppiiiffpppps",
     "tw_udtw_cost_bwd": "ppppppiiiffipppzs",
+    "tw_udtw_cost_tangent": "ppppppppiiiffpppppzs",
     "tw_udtw_feat_fwd": "ppppiiiiffffipppppzs",
     "tw_udtw_feat_bwd": "ppppppppiiiiffffiippppppzs",
     "tw_jeanie_cost_fwd": "piiiiiiiifpps",
@@ -74,6 +75,8 @@ def _load():
     lib.tw_fvm_workspace_bytes.argtypes = [ctypes.c_int] * 5
     lib.tw_udtw_cost_workspace_bytes.restype = ctypes.c_size_t
     lib.tw_udtw_cost_workspace_bytes.argtypes = [ctypes.c_int] * 4
+    lib.tw_udtw_tangent_workspace_bytes.restype = ctypes.c_size_t
+    lib.tw_udtw_tangent_workspace_bytes.argtypes = [ctypes.c_int] * 5
     lib.tw_udtw_carry_bytes.restype = ctypes.c_size_t
     lib.tw_udtw_carry_bytes.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                         ctypes.c_double, ctypes.c_int]
@@ -214,6 +217,15 @@ def udtw_cost_workspace_elems(B, N, M, dtype=torch.float32):
     (the hand-off records between workgroups of long sequences; 0 otherwise)."""
     es = 4 if dtype == torch.float32 else 8
     return -(-library().tw_udtw_cost_workspace_bytes(B, N, M, es) // es)
+
+
+def udtw_tangent_workspace_elems(B, N, M, has_penalty, dtype=torch.float32):
+    """Elements (of ``dtype``) of the workspace of the second-order sweeps
+    (``tw_udtw_cost_tangent``): the forward's R, P and their tangents, and for
+    long sequences the diagonals the sweeps exchange."""
+    es = 4 if dtype == torch.float32 else 8
+    return -(-library().tw_udtw_tangent_workspace_bytes(B, N, M, int(bool(has_penalty)), es)
+             // es)
 
 
 def dense(dtype, *tensors, contiguous=True):
