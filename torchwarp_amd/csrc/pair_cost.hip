@@ -11,14 +11,16 @@
 // (cost > 0), else 0, then
 //   dA = 2 (rowsum(dS) A - dS Bm),  dB = 2 (colsum(dS) Bm - dS^T A).
 //
-// Forward: fp32 with D a multiple of 4 runs on the matrix cores
-// (v_mfma_f32_16x16x4f32, a 16 x 16*TN output strip per wavefront); fp64 and
-// other D on a plain FMA kernel. Backward: when a pair's dS fits in LDS and
-// C <= 64, one fused kernel per pair streams A and B once (threads along D,
-// dB partial sums in registers); otherwise, for D <= 64 (32 in fp64), two
-// tiled passes that each read dS once (dA by row blocks, dB by column
-// blocks), contracting on the matrix cores in fp32, and two FMA kernels
-// beyond.
+// Forward: on the matrix cores in both precisions (v_mfma_f32_16x16x4f32,
+// v_mfma_f64_16x16x4f64; a 16 x 16*TN output strip per wavefront), with
+// 4-element chunk loads when D % 4 == 0 and element loads otherwise; a plain
+// FMA kernel only for blocks whose byte offsets pass 31 bits. Backward: when a
+// pair's dS fits in LDS and C <= 64, one fused kernel per pair streams A and B
+// once (threads along D, dB partial sums in registers); otherwise two tiled
+// passes that each read dS once (dA by row blocks, dB by column blocks), on
+// the matrix cores in fp32 (D > 64 in 64-feature slices) and on FMAs in fp64
+// (D > 32 in 32-feature slices); FMA kernels only past 31-bit offsets in
+// fp32.
 //
 // The uDTW feature path (sqdist_raw / sqdist_raw_bwd) keeps S and dS by
 // anti-diagonals (plane_index), the layout in which the sweeps' per-diagonal
@@ -232,6 +234,8 @@ __global__ void __launch_bounds__(256) pair_bwd_tiled(const T* __restrict__ A,
 // v_mfma_f32_16x16x4f32 operand layout (wave64): A (16x4) lane l holds
 // A[l % 16][l / 16]; B (4x16) lane l holds B[l / 16][l % 16]; the 16x16
 // result gives lane l, register i the element (4 (l / 16) + i, l % 16).
+// v_mfma_f64_16x16x4f64 takes its operands the same way and gives lane l,
+// register i the element (l / 16 + 4 i, l % 16).
 // The reduction index may be permuted consistently in both operands: lane l
 // loads the float4 A[row][k0 + 4 g .. +3] (g = l / 16) and its B row
 // likewise, and MFMA j of a 16-wide k block consumes component j, i.e.
@@ -239,6 +243,30 @@ __global__ void __launch_bounds__(256) pair_bwd_tiled(const T* __restrict__ A,
 // per k block.
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+// The four consecutive elements a lane contributes per k block, and the
+// accumulator of one 16 x 16 MFMA tile (four elements per lane), per type.
+template <typename T> struct Mfma;
+template <> struct Mfma<float> {
+  typedef f32x4 V;
+  // v_mfma_f32_16x16x4f32
+  static __device__ __forceinline__ V op(float a, float b, V c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+  // row of result register i in lane group g (the column is lane % 16)
+  static __device__ __forceinline__ int row(int g, int i) { return 4 * g + i; }
+};
+template <> struct Mfma<double> {
+  typedef f64x4 V;
+  // v_mfma_f64_16x16x4f64: the same operand layout, one double per lane for
+  // A and B; the four result registers of lane group g hold rows g, g + 4,
+  // g + 8, g + 12 (measured on gfx950)
+  static __device__ __forceinline__ V op(double a, double b, V c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ int row(int g, int i) { return g + 4 * i; }
+};
 
 __device__ __forceinline__ f32x4 ld4(const Buf& b, int v, int s) {
   const unsigned int __attribute__((ext_vector_type(4))) w =
@@ -246,24 +274,47 @@ __device__ __forceinline__ f32x4 ld4(const Buf& b, int v, int s) {
   return f32x4{__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z),
                __uint_as_float(w.w)};
 }
+// Four doubles (32 bytes) as two 16-byte loads.
+__device__ __forceinline__ f64x4 ld4d(const Buf& b, int v, int s) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 lo = __builtin_amdgcn_raw_buffer_load_b128(b.r, v, s, 0);
+  const u32x4 hi = __builtin_amdgcn_raw_buffer_load_b128(b.r, v == kOob ? kOob : v + 16, s, 0);
+  auto dbl = [](unsigned int x, unsigned int y) {
+    return __longlong_as_double((long long)(((unsigned long long)y << 32) | x));
+  };
+  return f64x4{dbl(lo.x, lo.y), dbl(lo.z, lo.w), dbl(hi.x, hi.y), dbl(hi.z, hi.w)};
+}
 
-// Elements k..k+3 of the row at byte offset v as four single-dword loads
-// (rows of any D are only 4-byte aligned); elements at or past D, and every
-// element of a row at kOob, read 0.
-__device__ __forceinline__ f32x4 ld4_dwords(const Buf& b, int v, int k, int D) {
+// Elements k..k+3 of the row at byte offset v as four single loads (rows of
+// any D are only element-aligned); elements at or past D, and every element
+// of a row at kOob, read 0.
+__device__ __forceinline__ f32x4 ld4_elems(const Buf& b, int v, int k, int D, float) {
   f32x4 x;
 #pragma unroll
   for (int j = 0; j < 4; ++j) x[j] = b.ldf(v == kOob || k + j >= D ? kOob : v + (k + j) * 4, 0);
   return x;
 }
+__device__ __forceinline__ f64x4 ld4_elems(const Buf& b, int v, int k, int D, double) {
+  f64x4 x;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) x[j] = b.ldd(v == kOob || k + j >= D ? kOob : v + (k + j) * 8, 0);
+  return x;
+}
+__device__ __forceinline__ f32x4 ld4_chunk(const Buf& b, int v, int s, float) { return ld4(b, v, s); }
+__device__ __forceinline__ f64x4 ld4_chunk(const Buf& b, int v, int s, double) {
+  return ld4d(b, v, s);
+}
 
-// D4: D % 4 == 0, each row's chunk is one 16-byte load; otherwise four
-// single-dword loads with the tail masked.
-template <int MET, int TN, bool DG, bool D4>
-__global__ void __launch_bounds__(256) pair_fwd_mfma(const float* __restrict__ A,
-                                                     const float* __restrict__ Bm,
-                                                     float* __restrict__ out, int R, int C,
+// D4: D % 4 == 0, each row's chunk is one aligned 4-element load; otherwise
+// four single-element loads with the tail masked. Byte offsets within a
+// pair's blocks fit 31 bits (the launcher checks).
+template <typename T, int MET, int TN, bool DG, bool D4>
+__global__ void __launch_bounds__(256) pair_fwd_mfma(const T* __restrict__ A,
+                                                     const T* __restrict__ Bm,
+                                                     T* __restrict__ out, int R, int C,
                                                      int D) {
+  typedef typename Mfma<T>::V V;
+  constexpr int ES = (int)sizeof(T);
   const int p = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int strip = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -277,32 +328,34 @@ __global__ void __launch_bounds__(256) pair_fwd_mfma(const float* __restrict__ A
   bb.init(Bm + (size_t)p * C * D, (long long)C * D);
   const int ra = r0 + li;
   // D4: offset of the lane's chunk; else of its row
-  const int va = ra < R ? (ra * D + (D4 ? 4 * g : 0)) * 4 : kOob;
+  const int va = ra < R ? (ra * D + (D4 ? 4 * g : 0)) * ES : kOob;
   int vb[TN];
 #pragma unroll
   for (int t = 0; t < TN; ++t) {
     const int cb = c0 + 16 * t + li;
-    vb[t] = cb < C ? (cb * D + (D4 ? 4 * g : 0)) * 4 : kOob;
+    vb[t] = cb < C ? (cb * D + (D4 ? 4 * g : 0)) * ES : kOob;
   }
-  f32x4 acc[TN];
-  float na = 0.f, nb[TN];
+  V acc[TN];
+  T na = 0, nb[TN];
 #pragma unroll
   for (int t = 0; t < TN; ++t) {
-    acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    nb[t] = 0.f;
+    acc[t] = V{0, 0, 0, 0};
+    nb[t] = 0;
   }
   for (int k0 = 0; k0 < D; k0 += 16) {
     const bool kin = k0 + 4 * g < D;   // D % 4 == 0: a chunk is all in or all out
-    const f32x4 a4 = D4 ? ld4(ba, kin ? va : kOob, k0 * 4) : ld4_dwords(ba, va, k0 + 4 * g, D);
+    const V a4 = D4 ? ld4_chunk(ba, kin ? va : kOob, k0 * ES, T(0))
+                    : ld4_elems(ba, va, k0 + 4 * g, D, T(0));
     na += a4.x * a4.x + a4.y * a4.y + a4.z * a4.z + a4.w * a4.w;
 #pragma unroll
     for (int t = 0; t < TN; ++t) {
-      const f32x4 b4 = D4 ? ld4(bb, kin ? vb[t] : kOob, k0 * 4) : ld4_dwords(bb, vb[t], k0 + 4 * g, D);
+      const V b4 = D4 ? ld4_chunk(bb, kin ? vb[t] : kOob, k0 * ES, T(0))
+                      : ld4_elems(bb, vb[t], k0 + 4 * g, D, T(0));
       nb[t] += b4.x * b4.x + b4.y * b4.y + b4.z * b4.z + b4.w * b4.w;
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.x, b4.x, acc[t], 0, 0, 0);
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.y, b4.y, acc[t], 0, 0, 0);
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.z, b4.z, acc[t], 0, 0, 0);
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.w, b4.w, acc[t], 0, 0, 0);
+      acc[t] = Mfma<T>::op(a4.x, b4.x, acc[t]);
+      acc[t] = Mfma<T>::op(a4.y, b4.y, acc[t]);
+      acc[t] = Mfma<T>::op(a4.z, b4.z, acc[t]);
+      acc[t] = Mfma<T>::op(a4.w, b4.w, acc[t]);
     }
   }
   // squared norms: sum the four k groups of each row (lanes li, li+16, li+32, li+48)
@@ -313,16 +366,16 @@ __global__ void __launch_bounds__(256) pair_fwd_mfma(const float* __restrict__ A
     nb[t] += __shfl_xor(nb[t], 16);
     nb[t] += __shfl_xor(nb[t], 32);
   }
-  float* o = out + (size_t)p * R * C;
+  T* o = out + (size_t)p * R * C;
   if (!DG) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int r = r0 + 4 * g + i;
-      const float nr = __shfl(na, 4 * g + i);   // lane 4g+i holds row 4g+i's norm
+      const int rt = Mfma<T>::row(g, i), r = r0 + rt;
+      const T nr = __shfl(na, rt);   // lane rt holds row rt's norm
 #pragma unroll
       for (int t = 0; t < TN; ++t) {
         const int c = c0 + 16 * t + li;
-        if (r < R && c < C) o[(size_t)r * C + c] = finish_cost<float, MET>(nr + nb[t] - 2.f * acc[t][i]);
+        if (r < R && c < C) o[(size_t)r * C + c] = finish_cost<T, MET>(nr + nb[t] - T(2) * acc[t][i]);
       }
     }
     return;
@@ -332,14 +385,15 @@ __global__ void __launch_bounds__(256) pair_fwd_mfma(const float* __restrict__ A
   // contiguous run of up to 16 cells. Only this wavefront touches its tile,
   // and its LDS operations complete in order.
   constexpr int W = 16 * TN, PITCH = W + 2;   // pitch W + 2: a diagonal's cells in distinct banks
-  __shared__ float tile[4][16][PITCH];
-  float(*tl)[PITCH] = tile[threadIdx.x >> 6];
+  __shared__ T tile[4][16][PITCH];
+  T(*tl)[PITCH] = tile[threadIdx.x >> 6];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float nr = __shfl(na, 4 * g + i);
+    const int rt = Mfma<T>::row(g, i);
+    const T nr = __shfl(na, rt);
 #pragma unroll
     for (int t = 0; t < TN; ++t)
-      tl[4 * g + i][16 * t + li] = finish_cost<float, MET>(nr + nb[t] - 2.f * acc[t][i]);
+      tl[rt][16 * t + li] = finish_cost<T, MET>(nr + nb[t] - T(2) * acc[t][i]);
   }
   if ((long long)R * C < (1LL << 31)) {
     // Lane l holds the run starts (plane_index minus the row) of tile
@@ -376,32 +430,35 @@ __global__ void __launch_bounds__(256) pair_fwd_mfma(const float* __restrict__ A
 
 // ---------------------------------------------------------- MFMA backward
 //
-// fp32: the tiled backward's two passes (dA by 64-row blocks, dB by
-// 64-column blocks, each reading dS once) with the contraction on the matrix
-// cores. A launch covers the features k0 .. k0 + 16NB - 1 (NB <= 4); larger
-// D takes one launch pair per 64-feature slice. A workgroup owns 64 indices of one side; per 64-wide tile of the
-// streamed side it stages dS as ds[owned][streamed] and the other operand
-// transposed, opT[d][streamed], both with rows of 68 floats (16-byte aligned
-// for the float4 reads; the diagonal stores of the DG loader step 67 banks
+// The tiled backward's two passes (dA by 64-row blocks, dB by 64-column
+// blocks, each reading dS once) with the contraction on the matrix cores
+// (v_mfma_f32_16x16x4f32 / v_mfma_f64_16x16x4f64). A launch covers the
+// features k0 .. k0 + 16NB - 1 (NB <= 4 in fp32, 2 in fp64, which keeps the
+// static LDS below 64 KB); larger D takes one launch pair per 64- (32-)
+// feature slice. A workgroup owns 64 indices of one side; per 64-wide tile of
+// the streamed side it stages dS as ds[owned][streamed] and the other operand
+// transposed, opT[d][streamed], both with rows of 68 elements (aligned for
+// the 4-element reads; the diagonal stores of the DG loader step 67 elements
 // per lane, so they do not conflict). Wavefront w owns rows 16w..16w+15 and
-// accumulates its 16 x 16NB block of dS . other with v_mfma_f32_16x16x4f32,
-// lane l reading the float4s ds[16w + l % 16][kb + 4 (l / 16)] and
+// accumulates its 16 x 16NB block of dS . other, lane l reading the
+// 4-element vectors ds[16w + l % 16][kb + 4 (l / 16)] and
 // opT[16n + l % 16][kb + 4 (l / 16)] (the k-permuted operand layout of the
-// forward). The row sums of dS come from the same float4s. The next tile's
+// forward). The row sums of dS come from the same vectors. The next tile's
 // dS is loaded into registers before the MFMAs of this one. Workgroups are
 // numbered so that the tiles of one pair run on one XCD (the hardware
 // assigns workgroup i to XCD i % 8): the runs of a diagonal-major tile share
 // their end cache lines with the neighbouring tiles.
-template <int MET, bool COLS, int NB, bool DG>
-__global__ void __launch_bounds__(256) pair_bwd_mfma(const float* __restrict__ A,
-                                                     const float* __restrict__ Bm,
-                                                     const float* __restrict__ cost,
-                                                     const float* __restrict__ dcost,
-                                                     float* __restrict__ dOut, int P, int R,
+template <typename T, int MET, bool COLS, int NB, bool DG>
+__global__ void __launch_bounds__(256) pair_bwd_mfma(const T* __restrict__ A,
+                                                     const T* __restrict__ Bm,
+                                                     const T* __restrict__ cost,
+                                                     const T* __restrict__ dcost,
+                                                     T* __restrict__ dOut, int P, int R,
                                                      int C, int D, int k0) {
-  constexpr int TL = 64, PT = TL + 4;
-  __shared__ __align__(16) float ds[TL][PT];
-  __shared__ __align__(16) float opT[16 * NB][PT];
+  typedef typename Mfma<T>::V V;
+  constexpr int TL = 64, PT = TL + 4, ES = (int)sizeof(T);
+  __shared__ __align__(32) T ds[TL][PT];
+  __shared__ __align__(32) T opT[16 * NB][PT];
   const int nown = COLS ? C : R, nstr = COLS ? R : C;
   const int gx = (nown + TL - 1) / TL;
   const unsigned total = (unsigned)gx * P, L = blockIdx.x;
@@ -410,8 +467,8 @@ __global__ void __launch_bounds__(256) pair_bwd_mfma(const float* __restrict__ A
   const int tid = threadIdx.x, ln = tid & 63, lr = ln & 15, lg = ln >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const size_t prc = (size_t)p * R * C;
-  const float* other = COLS ? A + (size_t)p * R * D : Bm + (size_t)p * C * D;
-  const float* self = COLS ? Bm + (size_t)p * C * D : A + (size_t)p * R * D;
+  const T* other = COLS ? A + (size_t)p * R * D : Bm + (size_t)p * C * D;
+  const T* self = COLS ? Bm + (size_t)p * C * D : A + (size_t)p * R * D;
 
   // The next tile goes into registers while this one is contracted: dS (DG
   // by the tile's 127 anti-diagonals, four per pass, one per wavefront, each
@@ -423,7 +480,7 @@ __global__ void __launch_bounds__(256) pair_bwd_mfma(const float* __restrict__ A
   Buf bd, bo;
   bd.init(dcost + prc, (long long)R * C);
   bo.init(other, (long long)nstr * D);
-  float v[NV], w[NW];
+  T v[NV], w[NW];
   auto load = [&](int s0) {
     const int r0 = COLS ? s0 : own0, c0 = COLS ? own0 : s0;
     int run[2] = {0, 0};
@@ -445,25 +502,26 @@ __global__ void __launch_bounds__(256) pair_bwd_mfma(const float* __restrict__ A
         r = r0 + rr;
         c = c0 + cc;
         ok = dd < 2 * TL - 1 && rr < TL && cc >= 0;
-        so = __builtin_amdgcn_readlane(run[it < 16 ? 0 : 1], dd & 63) * 4;
+        so = __builtin_amdgcn_readlane(run[it < 16 ? 0 : 1], dd & 63) * ES;
       } else {
         const int e = it * 256 + tid;
         r = r0 + (e >> 6);
         c = c0 + (e & 63);
         ok = true;
       }
-      const int vo = !(ok && r < R && c < C) ? kOob : (DG ? r : r * C + c) * 4;
+      const int vo = !(ok && r < R && c < C) ? kOob : (DG ? r : r * C + c) * ES;
       if (MET == MET_RAW) {
-        v[it] = bd.ldf(vo, so);
+        v[it] = bd.template ld<T>(vo, so);
       } else {
         const size_t oo = prc + (size_t)r * C + c;
-        v[it] = vo == kOob ? 0.f : cost_adjoint<float, MET>(dcost[oo], cost[oo]);
+        v[it] = vo == kOob ? T(0) : cost_adjoint<T, MET>(dcost[oo], cost[oo]);
       }
     }
 #pragma unroll
     for (int it = 0; it < NW; ++it) {
       const int e = it * 256 + tid, si = e & 63, dcol = e >> 6;
-      w[it] = bo.ldf(s0 + si < nstr && k0 + dcol < D ? ((s0 + si) * D + k0 + dcol) * 4 : kOob, 0);
+      w[it] = bo.template ld<T>(
+          s0 + si < nstr && k0 + dcol < D ? ((s0 + si) * D + k0 + dcol) * ES : kOob, 0);
     }
   };
   auto stash = [&]() {
@@ -496,10 +554,10 @@ __global__ void __launch_bounds__(256) pair_bwd_mfma(const float* __restrict__ A
     }
   };
 
-  f32x4 acc[NB];
+  V acc[NB];
 #pragma unroll
-  for (int n = 0; n < NB; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float rs = 0.f;
+  for (int n = 0; n < NB; ++n) acc[n] = V{0, 0, 0, 0};
+  T rs = 0;
   load(0);
   for (int s0 = 0; s0 < nstr; s0 += TL) {
     __syncthreads();   // the previous tile's LDS reads are done
@@ -508,15 +566,15 @@ __global__ void __launch_bounds__(256) pair_bwd_mfma(const float* __restrict__ A
     if (s0 + TL < nstr) load(s0 + TL);
 #pragma unroll
     for (int kb = 0; kb < TL; kb += 16) {
-      const f32x4 a4 = *reinterpret_cast<const f32x4*>(&ds[16 * wv + lr][kb + 4 * lg]);
+      const V a4 = *reinterpret_cast<const V*>(&ds[16 * wv + lr][kb + 4 * lg]);
       rs += (a4.x + a4.y) + (a4.z + a4.w);
 #pragma unroll
       for (int n = 0; n < NB; ++n) {
-        const f32x4 b4 = *reinterpret_cast<const f32x4*>(&opT[16 * n + lr][kb + 4 * lg]);
-        acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.x, b4.x, acc[n], 0, 0, 0);
-        acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.y, b4.y, acc[n], 0, 0, 0);
-        acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.z, b4.z, acc[n], 0, 0, 0);
-        acc[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.w, b4.w, acc[n], 0, 0, 0);
+        const V b4 = *reinterpret_cast<const V*>(&opT[16 * n + lr][kb + 4 * lg]);
+        acc[n] = Mfma<T>::op(a4.x, b4.x, acc[n]);
+        acc[n] = Mfma<T>::op(a4.y, b4.y, acc[n]);
+        acc[n] = Mfma<T>::op(a4.z, b4.z, acc[n]);
+        acc[n] = Mfma<T>::op(a4.w, b4.w, acc[n]);
       }
     }
   }
@@ -525,13 +583,13 @@ __global__ void __launch_bounds__(256) pair_bwd_mfma(const float* __restrict__ A
   rs += __shfl_xor(rs, 32);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int o = own0 + 16 * wv + 4 * lg + i;   // result row of register i
-    const float so = __shfl(rs, 4 * lg + i);
+    const int rt = Mfma<T>::row(lg, i), o = own0 + 16 * wv + rt;   // result row of register i
+    const T so = __shfl(rs, rt);
 #pragma unroll
     for (int n = 0; n < NB; ++n) {
       const int d = k0 + 16 * n + lr;
       if (o < nown && d < D)
-        dOut[((size_t)p * nown + o) * D + d] = 2.f * (so * self[(size_t)o * D + d] - acc[n][i]);
+        dOut[((size_t)p * nown + o) * D + d] = T(2) * (so * self[(size_t)o * D + d] - acc[n][i]);
     }
   }
 }
@@ -635,22 +693,21 @@ static int pair_cost_fwd_impl(const T* A, const T* Bm, int P, int R, int C, int 
     }
     return TW_OK;
   }
-  if (sizeof(T) == 4) {
+  // the MFMA kernel addresses a pair's blocks with 31-bit byte offsets
+  const long long lim = (1LL << 31) / (long long)sizeof(T);
+  if ((long long)R * D < lim && (long long)C * D < lim) {
     // TN column tiles of 16 per wavefront share the A operand
     const int TN = C > 32 ? 4 : (C > 16 ? 2 : 1);
     const long long strips = (long long)((R + 15) / 16) * ((C + 16 * TN - 1) / (16 * TN));
     dim3 grid((unsigned)((strips + 3) / 4), P), block(256);
-    const float* Af = reinterpret_cast<const float*>(A);
-    const float* Bf = reinterpret_cast<const float*>(Bm);
-    float* of = reinterpret_cast<float*>(out);
-#define TW_PAIR_MFMA(MET_, TN_)                                                              \
-  do {                                                                                       \
-    if (D % 4 == 0)                                                                          \
-      hipLaunchKernelGGL((pair_fwd_mfma<MET_, TN_, DG, true>), grid, block, 0, s, Af, Bf, of, \
-                         R, C, D);                                                           \
-    else                                                                                     \
-      hipLaunchKernelGGL((pair_fwd_mfma<MET_, TN_, DG, false>), grid, block, 0, s, Af, Bf,    \
-                         of, R, C, D);                                                       \
+#define TW_PAIR_MFMA(MET_, TN_)                                                                \
+  do {                                                                                         \
+    if (D % 4 == 0)                                                                            \
+      hipLaunchKernelGGL((pair_fwd_mfma<T, MET_, TN_, DG, true>), grid, block, 0, s, A, Bm,    \
+                         out, R, C, D);                                                        \
+    else                                                                                       \
+      hipLaunchKernelGGL((pair_fwd_mfma<T, MET_, TN_, DG, false>), grid, block, 0, s, A, Bm,   \
+                         out, R, C, D);                                                        \
   } while (0)
 #define TW_PAIR_MFMA_TN(MET_)          \
   if (TN == 4) TW_PAIR_MFMA(MET_, 4);  \
@@ -721,27 +778,33 @@ static int pair_cost_bwd_impl(const T* A, const T* Bm, const T* cost, const T* d
 #undef TW_PAIR_SMALL
     return check_launch(what);
   }
-  if constexpr (sizeof(T) == 4) {
-    // (byte offsets within a pair's plane and operands fit 31 bits)
+  {
+    // byte offsets within a pair's plane and operands fit 31 bits
+    constexpr long long lim = (1LL << 31) / (long long)sizeof(T);
+    constexpr int slice = sizeof(T) == 4 ? 64 : 32;
     const long long big = (long long)(R > C ? R : C) * D;
-    if ((long long)R * C < (1LL << 29) && big < (1LL << 29)) {
+    if ((long long)R * C < lim && big < lim) {
       const unsigned ga = (unsigned)((R + 63) / 64) * P, gb = (unsigned)((C + 63) / 64) * P;
-#define TW_PAIR_MFMA(MET_, NB_)                                                                \
-  hipLaunchKernelGGL((pair_bwd_mfma<MET_, false, NB_, DG>), dim3(ga), dim3(256), 0, s, A, Bm,  \
-                     cost, dcost, dA, P, R, C, D, k0);                                         \
-  hipLaunchKernelGGL((pair_bwd_mfma<MET_, true, NB_, DG>), dim3(gb), dim3(256), 0, s, A, Bm,   \
+#define TW_PAIR_MFMA(MET_, NB_)                                                                  \
+  hipLaunchKernelGGL((pair_bwd_mfma<T, MET_, false, NB_, DG>), dim3(ga), dim3(256), 0, s, A, Bm, \
+                     cost, dcost, dA, P, R, C, D, k0);                                           \
+  hipLaunchKernelGGL((pair_bwd_mfma<T, MET_, true, NB_, DG>), dim3(gb), dim3(256), 0, s, A, Bm,  \
                      cost, dcost, dB, P, R, C, D, k0);
-#define TW_PAIR_MFMA_D(MET_)                 \
-  switch (nb) {                              \
-    case 1: TW_PAIR_MFMA(MET_, 1) break;     \
-    case 2: TW_PAIR_MFMA(MET_, 2) break;     \
-    case 3: TW_PAIR_MFMA(MET_, 3) break;     \
-    default: TW_PAIR_MFMA(MET_, 4) break;    \
+#define TW_PAIR_MFMA_D(MET_)                                      \
+  if constexpr (sizeof(T) == 4) {                                 \
+    switch (nb) {                                                 \
+      case 1: TW_PAIR_MFMA(MET_, 1) break;                        \
+      case 2: TW_PAIR_MFMA(MET_, 2) break;                        \
+      case 3: TW_PAIR_MFMA(MET_, 3) break;                        \
+      default: TW_PAIR_MFMA(MET_, 4) break;                       \
+    }                                                             \
+  } else {                                                        \
+    if (nb == 1) { TW_PAIR_MFMA(MET_, 1) } else { TW_PAIR_MFMA(MET_, 2) } \
   }
-      // the passes are separable over features: D > 64 runs as 64-feature
-      // slices, each reading dS again
-      for (int k0 = 0; k0 < D; k0 += 64) {
-        const int nb = ((D - k0 < 64 ? D - k0 : 64) + 15) / 16;
+      // the passes are separable over features: larger D runs as slices,
+      // each reading dS again
+      for (int k0 = 0; k0 < D; k0 += slice) {
+        const int nb = ((D - k0 < slice ? D - k0 : slice) + 15) / 16;
         if (metric == MET_RAW) { TW_PAIR_MFMA_D(MET_RAW) }
         else if constexpr (!DG) {
           if (metric == MET_SQ) { TW_PAIR_MFMA_D(MET_SQ) }
@@ -753,8 +816,8 @@ static int pair_cost_bwd_impl(const T* A, const T* Bm, const T* cost, const T* d
       return check_launch(what);
     }
   }
-  // float64 tiles (a pass with 64 features would need 66 KB of static LDS):
-  // the passes are separable over features, D > 32 runs as 32-feature slices
+  // float64 past 31-bit offsets: FMA tiles (a pass with 64 features would
+  // need 66 KB of static LDS), D > 32 as 32-feature slices
   if (sizeof(T) == 8) {
     const dim3 ga((R + 63) / 64, P), gb((C + 63) / 64, P), block(256);
 #define TW_PAIR_TILED(MET_, DPT_)                                                               \
