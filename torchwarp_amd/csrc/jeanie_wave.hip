@@ -16,19 +16,22 @@
 // (K <= 32). At step v of a row pair, half h computes column u = v - h, one
 // column behind the other half (U + 1 steps per row pair). Per cell:
 //  * the window softmins gather neighbouring viewpoints of the same cell:
-//    stride 1 by DPP wave shifts, stride K2 by ds_bpermute;
+//    stride 1 by DPP wave shifts, stride K2 by DPP row shifts joined across
+//    16-lane rows by v_permlane16_swap (K2 = 5; other strides by
+//    ds_bpermute);
 //  * the temporal predecessors are Rw values of the lane's own viewpoint:
 //    "left" is its own last step; half 1's "up" is half 0's last step, handed
 //    over by v_permlane32_swap at the end of every step; half 0's "up" is the
 //    row above the pair, which half 1 produced during the previous row pair:
-//    half 0 receives it in the same swap and parks it in an LDS row buffer
-//    (two buffers, by row-pair parity) until the next row pair reads it;
+//    half 0 receives it in the same swap and keeps it, by column, in a
+//    register array until the next row pair reads it;
 //  * the cost (and in the backward R and dL/dR) of a row pair is loaded into
 //    a register ring during the previous row pair, and each result is
 //    stored as soon as it is known.
-// Nothing crosses wavefronts, so there is no barrier: a wavefront's LDS
-// operations complete in order. The backward runs the same sweep on the
-// grid flipped in t and u, so its "predecessors" are the cell's successors.
+// Nothing crosses wavefronts and nothing goes through the LDS. The backward
+// runs the same sweep on the grid flipped in t and u, so its "predecessors"
+// are the cell's successors. The padded-lane variants below (windows of one
+// neighbour each way) drop the per-neighbour masks.
 //
 // Work per pair: ceil(T/2) (U + 1) steps of one cell per lane, against
 // T + U - 1 diagonal steps of the workgroup-per-pair kernels (jeanie_dp.hip)
@@ -74,6 +77,59 @@ __device__ __forceinline__ double bperm(double v, int idx) {
   const int lo = __builtin_amdgcn_ds_bpermute(idx, (int)b);
   const int hi = __builtin_amdgcn_ds_bpermute(idx, (int)(b >> 32));
   return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+// The value of lane l - K / l + K (0 < K < 16) within each 32-lane half,
+// without the LDS: a DPP row shift serves the lanes whose source lies in their
+// own 16-lane row, and the rest take a row shift by 16 - K of the
+// neighbouring row, moved across by v_permlane16_swap. Lanes whose source is
+// outside their half get an unspecified value (the window masks them).
+template <int K>
+__device__ __forceinline__ unsigned lane_minus(unsigned v) {
+  static_assert(K > 0 && K < 16, "row shifts reach 15 lanes");
+  const unsigned a = __builtin_amdgcn_update_dpp(0u, v, 0x110 + K, 0xf, 0xf, false);       // row_shr:K
+  const unsigned b = __builtin_amdgcn_update_dpp(0u, v, 0x100 + 16 - K, 0xf, 0xf, false);  // row_shl:16-K
+  const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false);  // r[0]: odd rows <- even rows
+  return (__lane_id() & 15) >= K ? a : r[0];
+}
+template <int K>
+__device__ __forceinline__ unsigned lane_plus(unsigned v) {
+  static_assert(K > 0 && K < 16, "row shifts reach 15 lanes");
+  const unsigned a = __builtin_amdgcn_update_dpp(0u, v, 0x100 + K, 0xf, 0xf, false);       // row_shl:K
+  const unsigned c = __builtin_amdgcn_update_dpp(0u, v, 0x110 + 16 - K, 0xf, 0xf, false);  // row_shr:16-K
+  const auto r = __builtin_amdgcn_permlane16_swap(c, c, false, false);  // r[1]: even rows <- odd rows
+  return (__lane_id() & 15) < 16 - K ? a : r[1];
+}
+template <int K>
+__device__ __forceinline__ float lane_shift(float v, bool up) {
+  const unsigned x = __float_as_uint(v);
+  return __uint_as_float(up ? lane_plus<K>(x) : lane_minus<K>(x));
+}
+template <int K>
+__device__ __forceinline__ double lane_shift(double v, bool up) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const unsigned lo = (unsigned)b, hi = (unsigned)(b >> 32);
+  const unsigned rl = up ? lane_plus<K>(lo) : lane_minus<K>(lo);
+  const unsigned rh = up ? lane_plus<K>(hi) : lane_minus<K>(hi);
+  return __longlong_as_double((long long)(((unsigned long long)rh << 32) | rl));
+}
+
+// Neighbour o (|o| <= 2) along viewpoint axis 1, whose stride is K2: with a
+// compile-time stride KS (1: DPP wave shifts; 2..7: lane_shift), else by
+// ds_bpermute with the lane's precomputed byte index.
+template <typename T, int KS>
+__device__ __forceinline__ T nbk(T v, int o, int idx) {
+  if constexpr (KS == 1) {
+    return nb1(v, o);
+  } else if constexpr (KS > 1) {
+    static_assert(2 * KS < 16, "two strides within a row shift");
+    if (o == -1) return lane_shift<KS>(v, false);
+    if (o == 1) return lane_shift<KS>(v, true);
+    if (o == -2) return lane_shift<2 * KS>(v, false);
+    return lane_shift<2 * KS>(v, true);
+  } else {
+    return bperm(v, idx);
+  }
 }
 
 // The halves of a wavefront exchanged: lanes 0-31 take lanes 32-63 and back
@@ -134,17 +190,17 @@ __device__ __forceinline__ T win2(T v, const J3Win& w, int s2) {
   for (int q = 0; q < 5; ++q) s += ex2(m - x[q]);
   return m - lg2(s);
 }
-template <typename T, int SMAX>
+template <typename T, int SMAX, int KS>
 __device__ __forceinline__ T win1(T v, const J3Win& w, int s1) {
   const T INF = inf_v<T>();
   if (s1 == 0) return v;
   if (SMAX == 1) {
-    const T lo = bperm(v, w.idx1[1]), hi = bperm(v, w.idx1[3]);
+    const T lo = nbk<T, KS>(v, -1, w.idx1[1]), hi = nbk<T, KS>(v, 1, w.idx1[3]);
     return softmin3h(w.a1[1] ? lo : INF, v, w.a1[3] ? hi : INF);
   }
   T x[5];
 #pragma unroll
-  for (int q = 0; q < 5; ++q) x[q] = q == 2 ? v : bperm(v, w.idx1[q]);
+  for (int q = 0; q < 5; ++q) x[q] = q == 2 ? v : nbk<T, KS>(v, q - 2, w.idx1[q]);
   T m = INF;
 #pragma unroll
   for (int q = 0; q < 5; ++q) {
@@ -160,14 +216,14 @@ __device__ __forceinline__ T win1(T v, const J3Win& w, int s1) {
 // Adjoints of the window stages: sum over the window's neighbours q of
 // g[q] 2^(hq[q] - x) (the window is symmetric, so the lanes whose window holds
 // this lane are its window neighbours).
-template <typename T, int SMAX>
+template <typename T, int SMAX, int KS>
 __device__ __forceinline__ T win1_adj(T g, T hq, T x, const J3Win& w, int s1) {
   if (s1 == 0) return g;
   T acc = g * ex2(hq - x);
 #pragma unroll
   for (int q = 0; q < 5; ++q) {
     if (q == 2 || (SMAX == 1 && (q == 0 || q == 4))) continue;
-    const T gq = bperm(g, w.idx1[q]), hh = bperm(hq, w.idx1[q]);
+    const T gq = nbk<T, KS>(g, q - 2, w.idx1[q]), hh = nbk<T, KS>(hq, q - 2, w.idx1[q]);
     acc += w.a1[q] ? gq * ex2(hh - x) : (T)0;
   }
   return acc;
@@ -221,9 +277,8 @@ struct J3Lane {
   }
 };
 
-template <typename T, int SMAX, int UC>
+template <typename T, int SMAX, int UC, int KS>
 __global__ void __launch_bounds__(64) jeanie3_fwd_kernel(JeanieArgs<T> a) {
-  extern __shared__ __align__(16) unsigned char smem_raw[];
   constexpr int SPR = UC + 1;
   const int b = blockIdx.x;
   const int lane = threadIdx.x, h = lane >> 5, n = lane & 31;
@@ -241,10 +296,13 @@ __global__ void __launch_bounds__(64) jeanie3_fwd_kernel(JeanieArgs<T> a) {
   bC.init(a.C + (size_t)b * K * plane, (long long)K * plane);
   bR.init(a.Rw + (size_t)b * K * plane, (long long)K * plane);
 
-  // LDS: row buffers [2][SPR][32] holding Rw of the row above a row pair
-  // (entries of columns >= U stay +inf), then a scratch row for half 1's stores
-  T* rows = reinterpret_cast<T*>(smem_raw);
-  for (int e = lane; e < 3 * SPR * 32; e += 64) rows[e] = INF;
+  // Rw of the row above a row pair, by column, in registers (half 0 reads
+  // column v + 1 at step v before it overwrites column v - 1 with the row
+  // below, which half 1 produced a step earlier; entries of columns >= U stay
+  // +inf). Half 1 keeps a copy it never reads.
+  T ub[SPR];
+#pragma unroll
+  for (int v = 0; v < SPR; ++v) ub[v] = INF;
 
   // register ring: the cost of one row pair, loaded during the previous one
   T cr[SPR];
@@ -256,9 +314,6 @@ __global__ void __launch_bounds__(64) jeanie3_fwd_kernel(JeanieArgs<T> a) {
   T left = INF, pup = INF, xch = INF, lup = INF, rlast = INF;
   for (int r = 0; r < nrp; ++r) {
     const int vb = g.base(r), vbn = g.base(r + 1);
-    T* const rd = rows + (r & 1) * SPR * 32 + n;
-    T* const rdn = rows + ((r + 1) & 1) * SPR * 32 + n;
-    T* const wr = h == 0 ? rdn : rows + 2 * SPR * 32 + n;
 #pragma unroll
     for (int v = 0; v < SPR; ++v) {
       const bool valid = vb != kOob && g.col_ok(v);
@@ -266,19 +321,19 @@ __global__ void __launch_bounds__(64) jeanie3_fwd_kernel(JeanieArgs<T> a) {
       // temporal predecessors: up (t-1, u), left (t, u-1), diagonal (t-1, u-1)
       const T up = h ? xch : lup;
       const T dg = v == 0 ? ((r == 0 && h == 0) ? (T)0 : INF) : pup;
-      lup = v < UC ? rd[(v + 1) * 32] : rdn[0];   // half 0's next "up"
+      lup = ub[v < UC ? v + 1 : 0];   // half 0's next "up"
       T rh = ch + softmin3h(up, left, dg);
       rh = valid ? rh : INF;
       const T s2h = win2<T, SMAX>(rh, w, a.s2);
-      T rw = win1<T, SMAX>(s2h, w, a.s1);
+      T rw = win1<T, SMAX, KS>(s2h, w, a.s1);
       rw = valid ? rw : INF;
       bR.st(rh * a.inv_k, valid ? g.at(vb, v) : kOob, 0);
       if (r == nrp - 1 && v == Un - 1 + hl) rlast = rh;   // cell (T-1, U-1) in half hl
       left = rw;
       pup = up;
       xch = swap_halves(rw);
-      // half 0 parks the row below it (half 1's Rw at column v - 1) for the next row pair
-      if (v >= 1) wr[(v - 1) * 32] = xch;
+      // half 0 keeps the row below it (half 1's Rw at column v - 1) for the next row pair
+      if (v >= 1) ub[v - 1] = xch;
       cr[v] = bC.ld<T>(g.at(vbn, v), 0);
     }
   }
@@ -297,9 +352,8 @@ struct alignas(2 * sizeof(T)) FG {
   T f, g;   // F = Rh - Ch and G = Rbar of a cell
 };
 
-template <typename T, int SMAX, int UC>
+template <typename T, int SMAX, int UC, int KS>
 __global__ void __launch_bounds__(64) jeanie3_bwd_kernel(JeanieArgs<T> a) {
-  extern __shared__ __align__(16) unsigned char smem_raw[];
   constexpr int SPR = UC + 1;
   const int b = blockIdx.x;
   const int lane = threadIdx.x, h = lane >> 5, n = lane & 31;
@@ -322,11 +376,11 @@ __global__ void __launch_bounds__(64) jeanie3_bwd_kernel(JeanieArgs<T> a) {
   bG.init(has_gr ? a.gR + pb : a.C, has_gr ? (long long)K * plane : 0);   // empty: loads read 0
   bD.init(a.dC + pb, (long long)K * plane);
 
-  // LDS: row buffers [2][SPR][32] of (F, G) of the row below a row pair (the
-  // row above in the flipped grid; columns >= U stay (-inf, 0)), then a
-  // scratch row for half 1's stores
-  FG<T>* rows = reinterpret_cast<FG<T>*>(smem_raw);
-  for (int e = lane; e < 3 * SPR * 32; e += 64) rows[e] = {-INF, (T)0};
+  // (F, G) of the row below a row pair (the row above in the flipped grid;
+  // columns >= U stay (-inf, 0)), by column, in registers, as in the forward
+  FG<T> ub[SPR];
+#pragma unroll
+  for (int v = 0; v < SPR; ++v) ub[v] = {-INF, (T)0};
 
   T rr[SPR], rc[SPR], rg[SPR];
   {
@@ -343,9 +397,6 @@ __global__ void __launch_bounds__(64) jeanie3_bwd_kernel(JeanieArgs<T> a) {
   FG<T> left = none, pup = none, xch = none, lup = none;
   for (int r = 0; r < nrp; ++r) {
     const int vb = g.base(r), vbn = g.base(r + 1);
-    FG<T>* const rd = rows + (r & 1) * SPR * 32 + n;
-    FG<T>* const rdn = rows + ((r + 1) & 1) * SPR * 32 + n;
-    FG<T>* const wr = h == 0 ? rdn : rows + 2 * SPR * 32 + n;
 #pragma unroll
     for (int v = 0; v < SPR; ++v) {
       const bool valid = vb != kOob && g.col_ok(v);
@@ -354,12 +405,12 @@ __global__ void __launch_bounds__(64) jeanie3_bwd_kernel(JeanieArgs<T> a) {
       // successors (t+1, u), (t, u+1), (t+1, u+1) of the cell
       const FG<T> up = h ? xch : lup;
       const FG<T> dg = v == 0 ? none : pup;
-      lup = v < UC ? rd[(v + 1) * 32] : rdn[0];
+      lup = ub[v < UC ? v + 1 : 0];
       const T s2h = win2<T, SMAX>(rh, w, a.s2);
-      const T rwh = win1<T, SMAX>(s2h, w, a.s1);
+      const T rwh = win1<T, SMAX, KS>(s2h, w, a.s1);
       T wbar = up.g * ex2(up.f - rwh) + left.g * ex2(left.f - rwh) + dg.g * ex2(dg.f - rwh);
       wbar = valid ? wbar : (T)0;
-      const T s2bar = win1_adj<T, SMAX>(wbar, valid ? rwh : (T)0, s2h, w, a.s1);
+      const T s2bar = win1_adj<T, SMAX, KS>(wbar, valid ? rwh : (T)0, s2h, w, a.s1);
       T rbar = win2_adj<T, SMAX>(valid ? s2bar : (T)0, valid ? s2h : (T)0, rh, w, a.s2);
       if (v == 0 && r == 0) {
         // the last cell (T-1, U-1) (half 0): seed with grad_out * softmax_n(-R/g)
@@ -378,7 +429,246 @@ __global__ void __launch_bounds__(64) jeanie3_bwd_kernel(JeanieArgs<T> a) {
       left = cur;
       pup = up;
       xch = {swap_halves(cur.f), swap_halves(cur.g)};
-      if (v >= 1) wr[(v - 1) * 32] = xch;
+      if (v >= 1) ub[v - 1] = xch;
+      const int o = g.at(vbn, v);
+      rr[v] = bR.ld<T>(o, 0);
+      rc[v] = bC.ld<T>(o, 0);
+      rg[v] = bG.ld<T>(o, 0);
+    }
+  }
+}
+
+// ------------------------------------------------- padded-lane kernels
+//
+// For windows of at most one viewpoint each way (s1, s2 <= 1) the lanes of a
+// half hold the viewpoints with one unused lane after each axis-2 row
+// (lane n1 P + n2, P = K2 + s2, K1 P < 32). Every window neighbour a cell
+// has then sits in its own viewpoint row or in an unused lane, and the
+// kernels need no per-neighbour masks:
+//  * in the forward direction cells outside the grid, and unused lanes, hold
+//    the finite sentinel BIG = 2^100 (scaled domain) both before and after
+//    the axis-2 window: 2^(x - BIG) underflows
+//    to exactly 0 for every value x a cell in the grid takes, so a softmin
+//    with such neighbours equals the softmin without them, and a softmin of
+//    sentinels stays finite (no inf - inf);
+//  * in the adjoint direction they hold a zero adjoint, so their terms
+//    vanish;
+//  * lanes shifted in from outside a 32-lane half receive BIG (values) or 0
+//    (adjoints) from the shift itself (DPP old value / bound_ctrl fill, and
+//    v_permlane16_swap against a fill register).
+// The arithmetic of a cell is that of the general kernels above.
+
+template <typename T>
+__device__ __forceinline__ T big_v() {
+  return (T)0x1p100;
+}
+
+// Lane l - 1 / l + 1 across the wavefront (DPP wave shifts); the lane without
+// a source takes `fill`, or 0 for the zero-filled form.
+__device__ __forceinline__ unsigned wsh(unsigned v, bool up, unsigned fill) {
+  return up ? __builtin_amdgcn_update_dpp(fill, v, 0x130, 0xf, 0xf, false)    // wave_shl:1
+            : __builtin_amdgcn_update_dpp(fill, v, 0x138, 0xf, 0xf, false);   // wave_shr:1
+}
+__device__ __forceinline__ unsigned wsh0(unsigned v, bool up) {
+  return up ? __builtin_amdgcn_update_dpp(0u, v, 0x130, 0xf, 0xf, true)
+            : __builtin_amdgcn_update_dpp(0u, v, 0x138, 0xf, 0xf, true);
+}
+// Lane l - K / l + K (0 < K < 16) within each 32-lane half: a DPP row shift for
+// the lanes whose source is in their own 16-lane row, whose old value is
+// the complementary row shift of the neighbouring row, brought over by
+// v_permlane16_swap against a register of `fill` (which the lanes whose
+// source lies outside the half keep).
+template <int K>
+__device__ __forceinline__ unsigned rsh(unsigned v, bool up, unsigned fill) {
+  static_assert(K > 0 && K < 16, "row shifts reach 15 lanes");
+  if (up) {
+    const unsigned c = __builtin_amdgcn_update_dpp(0u, v, 0x110 + 16 - K, 0xf, 0xf, true);
+    const auto r = __builtin_amdgcn_permlane16_swap(c, fill, false, false);
+    // r[1]: rows 0, 2 <- rows 1, 3 of c; rows 1, 3 keep fill
+    return __builtin_amdgcn_update_dpp(r[1], v, 0x100 + K, 0xf, 0xf, false);   // row_shl:K
+  }
+  const unsigned b = __builtin_amdgcn_update_dpp(0u, v, 0x100 + 16 - K, 0xf, 0xf, true);
+  const auto r = __builtin_amdgcn_permlane16_swap(fill, b, false, false);
+  // r[0]: rows 1, 3 <- rows 0, 2 of b; rows 0, 2 keep fill
+  return __builtin_amdgcn_update_dpp(r[0], v, 0x110 + K, 0xf, 0xf, false);     // row_shr:K
+}
+
+// Neighbour across an axis in the padded layout: stride 1 (axis 2, or axis 1
+// when P = 1) or P (axis 1), with the fill of a value (BIG) or of an adjoint
+// (0).
+template <int STRIDE>
+__device__ __forceinline__ unsigned pshift(unsigned v, bool up, unsigned fill, bool zero) {
+  if constexpr (STRIDE == 1) return zero ? wsh0(v, up) : wsh(v, up, fill);
+  else return rsh<STRIDE>(v, up, zero ? 0u : fill);
+}
+template <int STRIDE>
+__device__ __forceinline__ float pnb(float v, bool up, bool zero) {
+  const unsigned f = __float_as_uint(big_v<float>());
+  return __uint_as_float(pshift<STRIDE>(__float_as_uint(v), up, f, zero));
+}
+template <int STRIDE>
+__device__ __forceinline__ double pnb(double v, bool up, bool zero) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(v);
+  const unsigned long long f = (unsigned long long)__double_as_longlong(big_v<double>());
+  const unsigned lo = pshift<STRIDE>((unsigned)b, up, (unsigned)f, zero);
+  const unsigned hi = pshift<STRIDE>((unsigned)(b >> 32), up, (unsigned)(f >> 32), zero);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+// softmin of the window of one neighbour each way (values; no masks)
+template <int STRIDE, typename T>
+__device__ __forceinline__ T pwin(T v) {
+  return softmin3h(pnb<STRIDE>(v, false, false), v, pnb<STRIDE>(v, true, false));
+}
+// its adjoint: g 2^(hq - x) summed over the window's lanes (adjoints; no masks)
+template <int STRIDE, typename T>
+__device__ __forceinline__ T pwin_adj(T g, T hq, T x) {
+  const T gl = pnb<STRIDE>(g, false, true), hl = pnb<STRIDE>(hq, false, true);
+  const T gr = pnb<STRIDE>(g, true, true), hr = pnb<STRIDE>(hq, true, true);
+  return g * ex2(hq - x) + gl * ex2(hl - x) + gr * ex2(hr - x);
+}
+
+// Viewpoint of a lane of a half in the padded layout, and whether it is one.
+__device__ __forceinline__ int pview(int n, int P, int K1, int K2, bool* ok) {
+  const int n1 = n / P, n2 = n - n1 * P;
+  *ok = n1 < K1 && n2 < K2;
+  return *ok ? n1 * K2 + n2 : 0;
+}
+
+template <typename T, int UC, int P>
+__global__ void __launch_bounds__(64) jeanie3p_fwd_kernel(JeanieArgs<T> a) {
+  constexpr int SPR = UC + 1;
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x, h = lane >> 5;
+  const int Tn = a.Tn, Un = a.Un, K = a.K;
+  bool vn;
+  const int n = pview(lane & 31, P, a.K1, a.K2, &vn);
+  const T BIG = big_v<T>(), INF = inf_v<T>();
+  const int plane = Tn * Un, nrp = (Tn + 1) / 2, hl = (Tn - 1) & 1;
+  const bool w1 = a.s1 > 0, w2 = a.s2 > 0;
+
+  J3Lane<T> g;
+  g.init(n, h, a, false);
+  g.vn = vn;
+  Buf bC, bR;
+  bC.init(a.C + (size_t)b * K * plane, (long long)K * plane);
+  bR.init(a.Rw + (size_t)b * K * plane, (long long)K * plane);
+
+  T ub[SPR];
+#pragma unroll
+  for (int v = 0; v < SPR; ++v) ub[v] = BIG;
+  T cr[SPR];
+  {
+    const int vb = g.base(0);
+#pragma unroll
+    for (int v = 0; v < SPR; ++v) cr[v] = bC.ld<T>(g.at(vb, v), 0);
+  }
+  T left = BIG, pup = BIG, xch = BIG, lup = BIG, rlast = BIG;
+  for (int r = 0; r < nrp; ++r) {
+    const int vb = g.base(r), vbn = g.base(r + 1);
+#pragma unroll
+    for (int v = 0; v < SPR; ++v) {
+      const bool valid = vb != kOob && g.col_ok(v);
+      const T ch = cr[v] * a.k;
+      const T up = h ? xch : lup;
+      const T dg = v == 0 ? ((r == 0 && h == 0) ? (T)0 : BIG) : pup;
+      lup = ub[v < UC ? v + 1 : 0];
+      T rh = ch + softmin3h(up, left, dg);
+      rh = valid ? rh : BIG;
+      // (the stride-1 shifts cross between the halves: unused lane 31 would
+      // take lane 32's value into its window, and axis 1 reads lane 31)
+      const T s2h = w2 ? (valid ? pwin<1>(rh) : BIG) : rh;
+      const T rw = w1 ? pwin<P>(s2h) : s2h;
+      bR.st(rh * a.inv_k, valid ? g.at(vb, v) : kOob, 0);
+      if (r == nrp - 1 && v == Un - 1 + hl) rlast = rh;
+      left = rw;
+      pup = up;
+      xch = swap_halves(rw);
+      if (v >= 1) ub[v - 1] = xch;
+      cr[v] = bC.ld<T>(g.at(vbn, v), 0);
+    }
+  }
+  T m = vn ? rlast : INF;
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) m = fmin(m, __shfl_xor(m, o));
+  T s = (vn && m < INF) ? ex2(m - rlast) : (T)0;
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) s += __shfl_xor(s, o);
+  if (h == hl && lane % 32 == 0) a.out[b] = (m - lg2(s)) * a.inv_k;
+}
+
+template <typename T, int UC, int P>
+__global__ void __launch_bounds__(64) jeanie3p_bwd_kernel(JeanieArgs<T> a) {
+  constexpr int SPR = UC + 1;
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x, h = lane >> 5;
+  const int Tn = a.Tn, K = a.K;
+  bool vn;
+  const int n = pview(lane & 31, P, a.K1, a.K2, &vn);
+  const T BIG = big_v<T>(), INF = inf_v<T>();
+  const int plane = Tn * a.Un, nrp = (Tn + 1) / 2;
+  const T gout = a.gout[b];
+  const bool has_gr = a.gR != nullptr;
+  const bool w1 = a.s1 > 0, w2 = a.s2 > 0;
+
+  J3Lane<T> g;
+  g.init(n, h, a, true);
+  g.vn = vn;
+  const size_t pb = (size_t)b * K * plane;
+  Buf bC, bR, bG, bD;
+  bC.init(a.C + pb, (long long)K * plane);
+  bR.init(a.R + pb, (long long)K * plane);
+  bG.init(has_gr ? a.gR + pb : a.C, has_gr ? (long long)K * plane : 0);
+  bD.init(a.dC + pb, (long long)K * plane);
+
+  const FG<T> none = {-INF, (T)0};
+  FG<T> ub[SPR];
+#pragma unroll
+  for (int v = 0; v < SPR; ++v) ub[v] = none;
+  T rr[SPR], rc[SPR], rg[SPR];
+  {
+    const int vb = g.base(0);
+#pragma unroll
+    for (int v = 0; v < SPR; ++v) {
+      const int o = g.at(vb, v);
+      rr[v] = bR.ld<T>(o, 0);
+      rc[v] = bC.ld<T>(o, 0);
+      rg[v] = bG.ld<T>(o, 0);
+    }
+  }
+  FG<T> left = none, pup = none, xch = none, lup = none;
+  for (int r = 0; r < nrp; ++r) {
+    const int vb = g.base(r), vbn = g.base(r + 1);
+#pragma unroll
+    for (int v = 0; v < SPR; ++v) {
+      const bool valid = vb != kOob && g.col_ok(v);
+      const T rh = valid ? rr[v] * a.k : BIG;
+      const T ch = rc[v] * a.k;
+      const FG<T> up = h ? xch : lup;
+      const FG<T> dg = v == 0 ? none : pup;
+      lup = ub[v < UC ? v + 1 : 0];
+      const T s2h = w2 ? (valid ? pwin<1>(rh) : BIG) : rh;
+      const T rwh = w1 ? pwin<P>(s2h) : s2h;
+      const T wbar = up.g * ex2(up.f - rwh) + left.g * ex2(left.f - rwh) + dg.g * ex2(dg.f - rwh);
+      const T s2bar = w1 ? pwin_adj<P>(wbar, valid ? rwh : (T)0, s2h) : wbar;
+      T rbar = w2 ? pwin_adj<1>(s2bar, valid ? s2h : (T)0, rh) : s2bar;
+      if (v == 0 && r == 0) {
+        // the last cell (T-1, U-1) (half 0): seed with grad_out * softmax_n(-R/g)
+        T m = valid ? rh : INF;
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) m = fmin(m, __shfl_xor(m, o));
+        T s = valid ? ex2(m - rh) : (T)0;
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) s += __shfl_xor(s, o);
+        rbar += valid ? gout * ex2(m - lg2(s) - rh) : (T)0;
+      }
+      if (has_gr) rbar += rg[v];
+      const FG<T> cur = {valid ? rh - ch : -INF, rbar};
+      bD.st(rbar, valid ? g.at(vb, v) : kOob, 0);
+      left = cur;
+      pup = up;
+      xch = {swap_halves(cur.f), swap_halves(cur.g)};
+      if (v >= 1) ub[v - 1] = xch;
       const int o = g.at(vbn, v);
       rr[v] = bR.ld<T>(o, 0);
       rc[v] = bC.ld<T>(o, 0);
@@ -396,29 +686,54 @@ static int j3_uc(int Un) {
   return Un <= 8 ? 8 : (Un <= 16 ? 16 : (Un <= umax ? umax : 0));
 }
 
-template <typename T>
-static size_t j3_lds(int uc, bool bwd) {
-  return (size_t)3 * (uc + 1) * 32 * sizeof(T) * (bwd ? 2 : 1);
-}
-
-template <typename T, int SMAX, int UC>
+template <typename T, int SMAX, int UC, int KS>
 static void j3_launch(bool bwd, const JeanieArgs<T>& a, int B, hipStream_t s) {
-  const size_t lds = j3_lds<T>(UC, bwd);
   if (bwd)
-    hipLaunchKernelGGL((jeanie3_bwd_kernel<T, SMAX, UC>), dim3(B), dim3(64), lds, s, a);
+    hipLaunchKernelGGL((jeanie3_bwd_kernel<T, SMAX, UC, KS>), dim3(B), dim3(64), 0, s, a);
   else
-    hipLaunchKernelGGL((jeanie3_fwd_kernel<T, SMAX, UC>), dim3(B), dim3(64), lds, s, a);
+    hipLaunchKernelGGL((jeanie3_fwd_kernel<T, SMAX, UC, KS>), dim3(B), dim3(64), 0, s, a);
 }
 
-template <typename T, int SMAX>
+template <typename T, int SMAX, int KS>
 static void j3_launch_uc(bool bwd, int uc, const JeanieArgs<T>& a, int B, hipStream_t s) {
   switch (uc) {
-    case 8: j3_launch<T, SMAX, 8>(bwd, a, B, s); break;
-    case 16: j3_launch<T, SMAX, 16>(bwd, a, B, s); break;
+    case 8: j3_launch<T, SMAX, 8, KS>(bwd, a, B, s); break;
+    case 16: j3_launch<T, SMAX, 16, KS>(bwd, a, B, s); break;
     default:
-      if constexpr (sizeof(T) == 4) j3_launch<T, SMAX, 32>(bwd, a, B, s);
+      if constexpr (sizeof(T) == 4) j3_launch<T, SMAX, 32, KS>(bwd, a, B, s);
       break;
   }
+}
+
+// Axis-1 strides with LDS-free neighbour moves: 1 (one viewpoint axis) and 5
+// (5 x 5 viewpoints); other strides exchange through ds_bpermute.
+template <typename T, int SMAX>
+static void j3_launch_ks(bool bwd, int uc, const JeanieArgs<T>& a, int B, hipStream_t s) {
+  if (a.K2 == 1)
+    j3_launch_uc<T, SMAX, 1>(bwd, uc, a, B, s);
+  else if (a.K2 == 5)
+    j3_launch_uc<T, SMAX, 5>(bwd, uc, a, B, s);
+  else
+    j3_launch_uc<T, SMAX, 0>(bwd, uc, a, B, s);
+}
+
+template <typename T, int P>
+static void j3p_launch_uc(bool bwd, int uc, const JeanieArgs<T>& a, int B, hipStream_t s) {
+#define TW_J3P(UC_)                                                                              \
+  do {                                                                                           \
+    if (bwd)                                                                                     \
+      hipLaunchKernelGGL((jeanie3p_bwd_kernel<T, UC_, P>), dim3(B), dim3(64), 0, s, a);          \
+    else                                                                                         \
+      hipLaunchKernelGGL((jeanie3p_fwd_kernel<T, UC_, P>), dim3(B), dim3(64), 0, s, a);          \
+  } while (0)
+  switch (uc) {
+    case 8: TW_J3P(8); break;
+    case 16: TW_J3P(16); break;
+    default:
+      if constexpr (sizeof(T) == 4) TW_J3P(32);
+      break;
+  }
+#undef TW_J3P
 }
 
 template <typename T>
@@ -426,10 +741,22 @@ static int j3_run(bool bwd, const JeanieArgs<T>& a, int B, hipStream_t s, const 
   const int uc = j3_uc<T>(a.Un);
   if (a.K > 32 || uc == 0 || a.s1 > 2 || a.s2 > 2) return kJ3Unsupported;
   if (B == 0) return TW_OK;
+  // padded lanes: windows of one neighbour each way, one unused lane after
+  // each axis-2 row when that axis has a window, and lane 31 of each half
+  // unused (the stride-1 wave shifts cross from one half into the other);
+  // strides 1 and 6 built (one viewpoint axis, and 5 x 5 viewpoints)
+  const int P = a.K2 + (a.s2 > 0 ? 1 : 0);
+  if (a.s1 <= 1 && a.s2 <= 1 && a.K1 * P < 32 && (P == 1 || P == 6)) {
+    if (P == 1)
+      j3p_launch_uc<T, 1>(bwd, uc, a, B, s);
+    else
+      j3p_launch_uc<T, 6>(bwd, uc, a, B, s);
+    return check_launch(what);
+  }
   if (a.s1 > 1 || a.s2 > 1)
-    j3_launch_uc<T, 2>(bwd, uc, a, B, s);
+    j3_launch_ks<T, 2>(bwd, uc, a, B, s);
   else
-    j3_launch_uc<T, 1>(bwd, uc, a, B, s);
+    j3_launch_ks<T, 1>(bwd, uc, a, B, s);
   return check_launch(what);
 }
 
