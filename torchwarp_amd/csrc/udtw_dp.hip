@@ -3,6 +3,7 @@
 // launchers are in udtw_sweep.hpp.
 
 #include "udtw_sweep.hpp"
+#include "udtw_band.hpp"
 #include "../../include/torchwarp_hip.h"
 
 namespace tw {
@@ -95,6 +96,7 @@ static int cost_fwd(const T* C, const T* Q, int B, int N, int M, double gamma, d
   a.M = M;
   a.rd = allow_rd && carry_double<T>(N, M, gamma);
   set_hyper(a, gamma, 0.0, 1.0, band);
+  if (band_path(N, M, band)) return band_sweep<T>(false, a, B, s, what);
   return launch_pen<T, SRC_COST>(Q != nullptr, false, a, B, s, what);
 }
 
@@ -127,6 +129,7 @@ static int cost_bwd(const T* C, const T* Q, const T* R, const T* P, const T* gr,
     return fail(TW_ESIZE, "%s: workspace of %zu bytes needed", what, need);
   a.hand = need ? reinterpret_cast<unsigned long long*>(ws) : nullptr;
   set_hyper(a, gamma, 0.0, 1.0, band);
+  if (band_path(N, M, band)) return band_sweep<T>(true, a, B, s, what);
   return launch_pen<T, SRC_COST>(pen, true, a, B, s, what);
 }
 
