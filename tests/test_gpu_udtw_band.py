@@ -80,3 +80,45 @@ def test_banded_sweep_matches_oracle(case):
     j = torch.arange(M).view(1, -1)
     out = ((i - j).abs() > band).to("cuda")
     assert float(c.grad[:, out].abs().max()) == 0.0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, f64], ids=["f32", "f64"])
+def test_banded_backward_with_gradients_at_odd_offsets(dtype):
+    """The banded backward stores the gradients in aligned pairs of cells,
+    chosen by the parity of each cell's address. Here d_cost starts at an odd
+    element offset and d_pen at an even one, with N M odd (the pairs' parity
+    alternates between batch entries), through the C ABI; against the oracle."""
+    from torchwarp_amd import _hip
+    B, N, M, gamma, band = 3, 151, 163, 0.5, 20.0
+    g = torch.Generator().manual_seed(7)
+    C = 3.0 * torch.rand(B, N, M, generator=g, dtype=f64)
+    Q = 0.5 * torch.rand(B, N, M, generator=g, dtype=f64)
+    wr = torch.rand(B, generator=g, dtype=f64) + 0.5
+    wp = torch.rand(B, generator=g, dtype=f64) + 0.5
+    rc, rq = C.clone().requires_grad_(True), Q.clone().requires_grad_(True)
+    rd, rp = OU.udtw_from_cost(rc, rq, gamma=gamma, bandwidth=band)
+    (rd * wr + rp * wp).sum().backward()
+
+    dev = lambda t: t.to("cuda", dtype).contiguous()
+    c, q = dev(C), dev(Q)
+    R = torch.empty(B, _hip.carry_cols(N, M, gamma, dtype), device="cuda", dtype=dtype)
+    P = torch.empty(B, N * M, device="cuda", dtype=dtype)
+    d = torch.empty(B, device="cuda", dtype=dtype)
+    p = torch.empty(B, device="cuda", dtype=dtype)
+    _hip.call("tw_udtw_cost_fwd", dtype, c, q, B, N, M, gamma, band, R, P, d, p)
+    n = B * N * M
+    buf_c = torch.full((n + 3,), 7.0, device="cuda", dtype=dtype)
+    buf_q = torch.full((n + 4,), 7.0, device="cuda", dtype=dtype)
+    dc, dq = buf_c[1:1 + n], buf_q[2:2 + n]
+    ws_n = _hip.udtw_cost_workspace_elems(B, N, M, dtype)
+    ws = torch.empty(max(ws_n, 1), device="cuda", dtype=dtype)
+    _hip.call("tw_udtw_cost_bwd", dtype, c, q, R, P, dev(wr), dev(wp), B, N, M, gamma, band, 1,
+              dc, dq, ws if ws_n else None, ws_n * ws.element_size())
+    torch.cuda.synchronize()
+    tol = 1e-10 if dtype == f64 else 2e-3
+    assert _maxnorm(d, rd) < (1e-10 if dtype == f64 else 1e-5)
+    assert _maxnorm(dc.view(B, N, M), rc.grad) < tol
+    assert _maxnorm(dq.view(B, N, M), rq.grad) < tol
+    # the elements around the planes are untouched
+    assert float(buf_c[0]) == 7.0 and float(buf_c[-2]) == 7.0
+    assert float(buf_q[1]) == 7.0 and float(buf_q[-2]) == 7.0

@@ -43,6 +43,8 @@
 // G (of R, seeded with grad_r) and A (of P, seeded with grad_p),
 //   G_k = sum_s w_s (G_s - A_s (P_k - Pbar_s) / gamma),  A_k = sum_s w_s A_s,
 // w_s = exp((Rbar_s - R_k) / gamma), Rbar_s = R_s - C_s, Pbar_s = P_s - Q_s.
+#include <type_traits>
+
 #include "tw_capi.hpp"
 #include "tw_common.hpp"
 #include "udtw_band.hpp"
@@ -105,6 +107,57 @@ struct SlotCells {
     return (int)(raw | (out & 0x80000000u));
   }
 };
+
+// The backward stores the gradients in pairs along rows: the cell (i, j)
+// of a slot takes (i, j) and (i, j + 1), its right successor, whose G the
+// step holds already, as one aligned 8-byte (float) or 16-byte (double)
+// store, when the absolute element index of (i, j) is even; a cell with an
+// odd index is taken by its left neighbour's pair. The pairs of one store
+// instruction cover half the cache lines that one cell per lane would.
+// Pair writers are the cells of band offsets l in [0, 2w + 1] (l = 2w + 1 is
+// outside the band: it writes the zero there and the band's cell to its
+// right) with i in [0, N - 1], j in [0, M - 2], i.e. the steps d in [lo, hi].
+// Left over are the cells with an odd index in column 0 and those with an
+// even index in column M - 1, stored one by one (at steps dj0 and djm).
+struct PairCells : SlotCells {
+  int dj0, djm;
+  __device__ __forceinline__ void init(int m, int p, int w, int N, int M) {
+    const int l = 2 * m + p;
+    lo = l - w > w - l ? l - w : w - l;
+    const int hi1 = 2 * N - 2 + w - l, hi2 = 2 * M - 4 + l - w;
+    hi = hi1 < hi2 ? hi1 : hi2;
+    if (l > 2 * w + 1) {
+      lo = 1;
+      hi = 0;
+    }
+    a = (unsigned)((l - w) * (M - 1));
+    dj0 = l >= w ? l - w : -(1 << 30);   // the step of its cell in column 0
+    djm = 2 * M - 2 + l - w;             // ... in column M - 1
+  }
+  // byte offset of the pair, or one past 2^31 where the cell writes no pair
+  // (par: parity of the plane's element index at offset 0)
+  __device__ __forceinline__ int pair_off(int d, int M, int esh, unsigned par) const {
+    const unsigned raw = ((unsigned)d * (unsigned)(M + 1) + a) >> 1;   // element index
+    const unsigned out = (unsigned)(((d - lo) | (hi - d)) >> 31) | ((raw ^ par) & 1u);
+    return (int)((raw << esh) | (out << 31));
+  }
+};
+
+// Two values of T at byte offset o (aligned to their size) as one store.
+template <typename T>
+__device__ __forceinline__ void st_pair(const Buf& b, int o, T x0, T x1) {
+  if constexpr (sizeof(T) == 4) {
+    typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+    const u2 v = {__float_as_uint(x0), __float_as_uint(x1)};
+    __builtin_amdgcn_raw_buffer_store_b64(v, b.r, o, 0, 0);
+  } else {
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    const unsigned long long u0 = (unsigned long long)__double_as_longlong(x0);
+    const unsigned long long u1 = (unsigned long long)__double_as_longlong(x1);
+    const u4 v = {(unsigned)u0, (unsigned)(u0 >> 32), (unsigned)u1, (unsigned)(u1 >> 32)};
+    __builtin_amdgcn_raw_buffer_store_b128(v, b.r, o, 0, 0);
+  }
+}
 
 // x where keep is all ones, fill where it is zero (bitwise).
 __device__ __forceinline__ float bsel(float x, float fill, unsigned keep) {
@@ -314,7 +367,7 @@ constexpr int slot_accesses() {
 }
 template <typename T, typename RT, int S, bool PEN>
 constexpr int band_bwd_depth() {
-  // R, Rbar, P, Pbar of the band planes loaded, dC and dQ stored
+  // R, Rbar, P, Pbar of the band planes loaded, pairs of dC and dQ stored
   const int ops = 2 * slot_accesses<RT, S>() + (PEN ? 2 * slot_accesses<T, S>() : 0) +
                   (PEN ? 2 : 1) * S;
   const int pd = 2 * (28 / ops);
@@ -379,6 +432,16 @@ __global__ void __launch_bounds__(64) udtw_band_bwd(BandArgs<T, RT> a) {
     sc[0][s].init(m0 + s, 0, w, N, M);
     sc[1][s].init(m0 + s, 1, w, N, M);
   }
+  PairCells pc[2][S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    pc[0][s].init(m0 + s, 0, w, N, M);
+    pc[1][s].init(m0 + s, 1, w, N, M);
+  }
+  constexpr int esh = sizeof(T) == 4 ? 2 : 3;
+  // parities of the planes' element indices at this pair's offset 0
+  const unsigned par_c = (unsigned)((((size_t)a.dC >> esh) + (size_t)b * nm) & 1);
+  const unsigned par_q = has_dq ? (unsigned)((((size_t)a.dQ >> esh) + (size_t)b * nm) & 1) : 0u;
   // successor state of the slots at steps d + 1 and d + 2: Rbar = R - C
   // (NEG outside the grid: weight 0), Pbar = P - Q, and the adjoints G, A.
   // The end cell's diagonal successor is a virtual cell with Rbar = R and
@@ -421,7 +484,10 @@ __global__ void __launch_bounds__(64) udtw_band_bwd(BandArgs<T, RT> a) {
     fetch(D - 1 - u, u);   // in ring order, as in the forward
     __builtin_amdgcn_sched_barrier(0);
   }
-  for (int d1 = D - 1; d1 >= 0; d1 -= PD) {
+  // One block of PD steps from d1 down; CUTS: with the single stores at the
+  // grid's first and last columns, which only the first and last steps need.
+  auto block = [&](int d1, auto cuts) {
+    constexpr bool CUTS = decltype(cuts)::value;
 #pragma unroll
     for (int u = 0; u < PD; ++u) {
       const int d = d1 - u;
@@ -462,9 +528,24 @@ __global__ void __launch_bounds__(64) udtw_band_bwd(BandArgs<T, RT> a) {
           G -= (wdn * adn * (pk - bdn) + wrt * art * (pk - brt) + wdg * adg * (pk - bdg)) *
                a.inv_gamma;
         }
-        const int o = sc[p][s].off_bits(d, M, es);
-        bdc.st(G, o, 0);
-        if (PEN) bdq.st(A, o, 0);
+        // (i, j) and its right successor (i, j + 1), G = grt, A = art
+        st_pair<T>(bdc, pc[p][s].pair_off(d, M, esh, par_c), G, grt);
+        if (PEN) {
+          const T art = p ? a1[s] : (s > 0 ? a1[s - 1] : alo);
+          st_pair<T>(bdq, pc[p][s].pair_off(d, M, esh, par_q), A, art);
+        }
+        if constexpr (CUTS) {   // the cells left over at columns 0 and M - 1
+          const unsigned raw = sc[p][s].ok(d) ? (unsigned)sc[p][s].off(d, M, es) >> esh : 0u;
+          const bool ok = sc[p][s].ok(d);
+          const bool one_c = ok && ((d == pc[p][s].dj0 && ((raw ^ par_c) & 1u)) ||
+                                    (d == pc[p][s].djm && !((raw ^ par_c) & 1u)));
+          const bool one_q = PEN && ok && ((d == pc[p][s].dj0 && ((raw ^ par_q) & 1u)) ||
+                                           (d == pc[p][s].djm && !((raw ^ par_q) & 1u)));
+          if (__builtin_amdgcn_ballot_w64(one_c || one_q)) {
+            bdc.st(G, one_c ? (int)(raw << esh) : kOob, 0);
+            if (PEN) bdq.st(A, one_q ? (int)(raw << esh) : kOob, 0);
+          }
+        }
         ne[s] = bsel(rbr[u][s], NEG, keep);
         ng[s] = G;
         na[s] = A;
@@ -497,7 +578,15 @@ __global__ void __launch_bounds__(64) udtw_band_bwd(BandArgs<T, RT> a) {
       fetch(d - PD, u);
       __builtin_amdgcn_sched_barrier(0);   // ring order, as in the prologue
     }
-  }
+  };
+  // A slot meets column 0 at d = l - w <= w and column M - 1 at
+  // d = 2M - 2 + l - w >= 2N - 2 - w (N <= M): the blocks between take no
+  // single stores.
+  const int a_lo = 2 * N - w - 3, c_hi = w + 1;
+  int d1 = D - 1;
+  for (; d1 >= 0 && d1 >= a_lo; d1 -= PD) block(d1, std::true_type());
+  for (; d1 - PD + 1 > c_hi; d1 -= PD) block(d1, std::false_type());
+  for (; d1 >= 0; d1 -= PD) block(d1, std::true_type());
 }
 
 int band_slots(int w) {
