@@ -39,7 +39,12 @@ METRIC = ("DP cells/sec & pairs/sec fwd+bwd (uDTW B=256 N=M=140; JEANIE K=25), "
 SETTLE_S = 0.25    # minimum untimed warm-up per config (seconds)
 LAST_TIMES = {}   # label -> mean ms of every kernel timed by the last _hip_call_times
 EAGER_MS = {}     # config -> ms per eagerly run step (run_config with mode "eager"/"both")
-CONFIGS = ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5a", "cfg5b")
+CONFIGS = ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5a", "cfg5b", "cost", "cost_band")
+# The cost-path workloads beside the BASELINE configs: uDTW on precomputed
+# matrices, B = 64, N = M = 1024, gamma = 1, without a band ("cost") and with
+# a Sakoe-Chiba band of 102 ("cost_band", the banded sweep; its cells are the
+# band's cells).
+BAND = 102
 
 
 # ------------------------------------------------------------------ inputs
@@ -68,6 +73,8 @@ def make_inputs(name, device="cpu", dtype=torch.float32):
         t = (q, s)
     elif name in ("cfg5a", "cfg5b"):
         t = (4.0 * torch.rand(1024, 25, 16, 16, generator=g),)
+    elif name in ("cost", "cost_band"):
+        t = (torch.rand(64, 1024, 1024, generator=g), 0.1 * torch.rand(64, 1024, 1024, generator=g))
     else:
         raise ValueError(name)
     return tuple(x.to(device=device, dtype=dtype) for x in t)
@@ -84,6 +91,8 @@ def work(name):
         "cfg4": dict(cells=400 * 9 * 8 * 8, pairs=400),
         "cfg5a": dict(cells=1024 * 25 * 16 * 16, pairs=1024),
         "cfg5b": dict(cells=1024 * 16 * 16, pairs=1024),
+        "cost": dict(cells=64 * 1024 * 1024, pairs=64),
+        "cost_band": dict(cells=64 * (1024 * (2 * BAND + 1) - BAND * (BAND + 1)), pairs=64),
     }[name]
 
 
@@ -108,6 +117,15 @@ def step_fn(name, inputs):
         def f():
             xs = [t.detach().requires_grad_(True) for t in (X, Y, sx, sy)]
             d, p = m(*xs)
+            (d + p).mean().backward()
+        return f
+    if name in ("cost", "cost_band"):
+        C, Q = inputs
+        band = BAND if name == "cost_band" else None
+
+        def f():
+            c, q = C.detach().requires_grad_(True), Q.detach().requires_grad_(True)
+            d, p = TF.udtw_from_cost(c, q, gamma=1.0, bandwidth=band)
             (d + p).mean().backward()
         return f
     if name == "cfg4":
@@ -174,6 +192,27 @@ def _hip_call_times(name, inputs, iters):
         calls.append(("udtw_bwd", lambda: _hip.call(
             "tw_udtw_feat_bwd", f32, X, Y, vx, vy, R, P, g, g if pen else None, B, N, M, D, gamma,
             beta, 1e-8, 0.0, 1, 1, dX, dY, dvx, dvy, None, ws, wsb), 2 * io + carried))
+    elif name in ("cost", "cost_band"):
+        C, Q = inputs
+        B, N, M = C.shape
+        band = float(BAND) if name == "cost_band" else 0.0
+        R = C.new_empty(B, _hip.carry_cols(N, M, 1.0, C.dtype))
+        P = C.new_empty(B, N * M)
+        o1, o2 = C.new_empty(B), C.new_empty(B)
+        nws = _hip.udtw_cost_workspace_elems(B, N, M, C.dtype)
+        ws = C.new_empty(nws) if nws else None
+        wsb = 0 if ws is None else nws * 4
+        g = torch.full((B,), 1.0 / B, device=dev)
+        dC, dQ = torch.empty_like(C), torch.empty_like(Q)
+        # the cells the sweep visits: C, Q read and R, P written (forward),
+        # R, P read (backward) at 4 B each; the gradients are written in full
+        # (zero outside the band)
+        cells = work(name)["cells"]
+        calls.append(("udtw_fwd", lambda: _hip.call(
+            "tw_udtw_cost_fwd", f32, C, Q, B, N, M, 1.0, band, R, P, o1, o2), 16 * cells))
+        calls.append(("udtw_bwd", lambda: _hip.call(
+            "tw_udtw_cost_bwd", f32, C, Q, R, P, g, g, B, N, M, 1.0, band, 1, dC, dQ, ws, wsb),
+            8 * cells + 8 * B * N * M))
     elif name == "cfg5a":
         (c,) = inputs
         B = c.shape[0]
@@ -261,6 +300,12 @@ def cpu_baseline(name, budget_s=10.0):
             OJ.backward(c, R, torch.full((1024,), 1 / 1024), 1, 1, 0.1)
         elif name == "cfg5b":
             OJ.fvm_backward(inp[0], torch.full((1024,), 1 / 1024), 0.1)
+        elif name in ("cost", "cost_band"):
+            # a bounded sample: 2 of the 64 pairs (cells scaled below)
+            C, Q = (t[:2].clone().requires_grad_(True) for t in inp)
+            d, p = OU.udtw_from_cost(C, Q, gamma=1.0,
+                                     bandwidth=BAND if name == "cost_band" else None)
+            (d + p).sum().backward()
         else:
             q, s = inp
             c = OJ.euclidean_cost(q.requires_grad_(True), s.requires_grad_(True))
@@ -274,11 +319,12 @@ def cpu_baseline(name, budget_s=10.0):
         el = time.perf_counter() - t0
         if el >= budget_s or n >= 50:
             break
-    return {"value": w["cells"] * n / el, "unit": "cells/s", "cores": cores,
+    share = 2 / 64 if name in ("cost", "cost_band") else 1.0   # pairs of the batch run
+    return {"value": w["cells"] * share * n / el, "unit": "cells/s", "cores": cores,
             "kind": "port", "cpu_model": _cpu_model(),
-            "pairs_per_s": w["pairs"] * n / el,
-            "sample": "{}: full batch fwd+bwd x{} in {:.1f} s, fp32, oracle/ on {} threads"
-                      .format(name, n, el, cores)}
+            "pairs_per_s": w["pairs"] * share * n / el,
+            "sample": "{}: {} fwd+bwd x{} in {:.1f} s, fp32, oracle/ on {} threads"
+                      .format(name, "full batch" if share == 1.0 else "2 pairs", n, el, cores)}
 
 
 def _cpu_model():
