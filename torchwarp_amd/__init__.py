@@ -6,7 +6,7 @@ A drop-in for torchwarp's public API (``src/torchwarp/__init__.py:1-21``):
     import torchwarp_amd.functional as TF
 """
 
-from . import functional, paths
+from . import _reference_ops, functional, paths  # noqa: F401  (registers the reference's op names)
 from ._hip import check_async_status
 from .jeanie import FVM, JEANIE, euclidean_cost, rbf_cost, squared_euclidean_cost
 from .sdtw import SoftDTW
