@@ -597,7 +597,11 @@ __global__ void __launch_bounds__(64) jeanie3p_fwd_kernel(JeanieArgs<T> a) {
   if (h == hl && lane % 32 == 0) a.out[b] = (m - lg2(s)) * a.inv_k;
 }
 
-template <typename T, int UC, int P>
+// PS: rows of exactly UC columns (U = UC), not transposed, dC's element
+// index even at offset 0: each lane stores its cells in aligned pairs of row
+// neighbours, the pair of steps v - 1 and v at step v (half 0: v odd, half 1:
+// v even, v >= 2), so a store instruction covers half the cache lines.
+template <typename T, int UC, int P, bool PS>
 __global__ void __launch_bounds__(64) jeanie3p_bwd_kernel(JeanieArgs<T> a) {
   constexpr int SPR = UC + 1;
   const int b = blockIdx.x;
@@ -664,7 +668,15 @@ __global__ void __launch_bounds__(64) jeanie3p_bwd_kernel(JeanieArgs<T> a) {
       }
       if (has_gr) rbar += rg[v];
       const FG<T> cur = {valid ? rh - ch : -INF, rbar};
-      bD.st(rbar, valid ? g.at(vb, v) : kOob, 0);
+      if constexpr (PS) {
+        // step v's cell is column UC - 1 + h - v: the lower address of the
+        // pair it forms with step v - 1 (one column to its right) when that
+        // column is even
+        const bool pair = ((h + v) & 1) && v >= 1 + h;
+        st_pair<T>(bD, (valid && pair) ? g.at(vb, v) : kOob, rbar, left.g);
+      } else {
+        bD.st(rbar, valid ? g.at(vb, v) : kOob, 0);
+      }
       left = cur;
       pup = up;
       xch = {swap_halves(cur.f), swap_halves(cur.g)};
@@ -719,10 +731,14 @@ static void j3_launch_ks(bool bwd, int uc, const JeanieArgs<T>& a, int B, hipStr
 
 template <typename T, int P>
 static void j3p_launch_uc(bool bwd, int uc, const JeanieArgs<T>& a, int B, hipStream_t s) {
+  // pair stores of dC: full rows, not transposed, even element index at dC
+  const bool ps = a.Un == uc && !a.swap && (((size_t)a.dC / sizeof(T)) & 1) == 0;
 #define TW_J3P(UC_)                                                                              \
   do {                                                                                           \
-    if (bwd)                                                                                     \
-      hipLaunchKernelGGL((jeanie3p_bwd_kernel<T, UC_, P>), dim3(B), dim3(64), 0, s, a);          \
+    if (bwd && ps)                                                                               \
+      hipLaunchKernelGGL((jeanie3p_bwd_kernel<T, UC_, P, true>), dim3(B), dim3(64), 0, s, a);    \
+    else if (bwd)                                                                                \
+      hipLaunchKernelGGL((jeanie3p_bwd_kernel<T, UC_, P, false>), dim3(B), dim3(64), 0, s, a);   \
     else                                                                                         \
       hipLaunchKernelGGL((jeanie3p_fwd_kernel<T, UC_, P>), dim3(B), dim3(64), 0, s, a);          \
   } while (0)

@@ -143,22 +143,6 @@ struct PairCells : SlotCells {
   }
 };
 
-// Two values of T at byte offset o (aligned to their size) as one store.
-template <typename T>
-__device__ __forceinline__ void st_pair(const Buf& b, int o, T x0, T x1) {
-  if constexpr (sizeof(T) == 4) {
-    typedef unsigned int u2 __attribute__((ext_vector_type(2)));
-    const u2 v = {__float_as_uint(x0), __float_as_uint(x1)};
-    __builtin_amdgcn_raw_buffer_store_b64(v, b.r, o, 0, 0);
-  } else {
-    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
-    const unsigned long long u0 = (unsigned long long)__double_as_longlong(x0);
-    const unsigned long long u1 = (unsigned long long)__double_as_longlong(x1);
-    const u4 v = {(unsigned)u0, (unsigned)(u0 >> 32), (unsigned)u1, (unsigned)(u1 >> 32)};
-    __builtin_amdgcn_raw_buffer_store_b128(v, b.r, o, 0, 0);
-  }
-}
-
 // x where keep is all ones, fill where it is zero (bitwise).
 __device__ __forceinline__ float bsel(float x, float fill, unsigned keep) {
   return __uint_as_float((__float_as_uint(x) & keep) | (__float_as_uint(fill) & ~keep));
