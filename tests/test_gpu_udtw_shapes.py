@@ -26,7 +26,7 @@ SHAPES = [  # (B, N, M, D, gamma)
     (2, 250, 260, 4, 1.0),     # ragged row and column tails of the cost tiles
     (1, 64, 1000, 4, 1.0),     # few rows against long columns
     (2, 150, 170, 3, 1.0),     # D not a multiple of 4: single-element cost loads
-    (1, 100, 130, 75, 1.0),    # D > 64: the FMA cost backward
+    (1, 100, 130, 75, 1.0),    # D > 64: cost kernels in feature slices (64 float32, 32 float64)
     (1, 1100, 1030, 1, 1.0),   # beyond 1024 rows: several rows per thread
 ]
 
