@@ -2,8 +2,10 @@
 
 The launcher picks the kernel from the shape: the wavefront-per-pair kernels
 (K <= 32 viewpoints, rows of up to 8 / 16 / 32 steps, 16 in float64, shifts
-up to 2), the workgroup-per-pair kernels (K <= 64, shifts <= 2, longer rows)
-and the general ones (more viewpoints or larger shifts). The shapes below put
+up to 2; with windows of one neighbour their padded-lane variants, which run
+several wavefronts per pair for small batches), the workgroup-per-pair
+kernels (K <= 64, shifts <= 2, longer rows) and the general ones (more
+viewpoints or larger shifts). The shapes below put
 each family (and each compiled row length) under the forward and the
 backward, with one and two viewpoint axes, T > U (the transposed
 orientation) and odd T (a half-empty last row pair).
@@ -28,6 +30,12 @@ CASES = [  # (B, K1, K2, T, U, (s1, s2), gamma)
     (2, 2, 3, 10, 40, (1, 1), 0.1),    # rows of 40: workgroup-per-pair kernels
     (2, 9, 9, 5, 6, (1, 1), 0.1),      # 81 viewpoints: general kernels
     (2, 7, 1, 5, 8, (3, 0), 0.2),      # shift 3: general kernels
+    # padded-lane windows (5 x 5 with shifts 1, or one axis with shift 1):
+    # small batches run several wavefronts per pair (odd T: a half-empty row
+    # pair), batches past half the SIMDs one wavefront per pair
+    (3, 9, 1, 9, 8, (1, 0), 0.2),      # one axis, several wavefronts
+    (600, 9, 1, 8, 8, (1, 0), 0.2),    # one axis, one wavefront per pair
+    (600, 5, 5, 12, 16, (1, 1), 0.1),  # 5 x 5, one wavefront per pair
 ]
 
 

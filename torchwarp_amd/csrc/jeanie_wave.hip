@@ -689,6 +689,204 @@ __global__ void __launch_bounds__(64) jeanie3p_bwd_kernel(JeanieArgs<T> a) {
   }
 }
 
+// ------------------------------------ several wavefronts per pair
+//
+// The padded-lane sweeps with the row pairs of a pair spread over the W
+// wavefronts of a workgroup: wavefront w walks row pairs w, w + W, ..., and
+// row pair r runs L = 2 steps behind row pair r - 1. Half 0's "up" (the row
+// above the pair) is the previous wavefront's half 1, which writes each
+// column to an LDS slot one step after computing it; the lag leaves one
+// step between the write and the read. Every wavefront takes the same
+// number of steps, each ending in a workgroup barrier (LDS operations
+// complete, then s_barrier; global stores are not waited for), so a pair
+// takes L (W - 1) + ceil(nrp / W) max(U + 1, L W) steps instead of
+// nrp (U + 1): with one wavefront per SIMD the single-wavefront sweep is
+// bound by the latency of its dependent chain, and several wavefronts
+// per SIMD fill each other's waits. The arithmetic of a cell is that of the
+// padded kernels; only the source of half 0's "up" changes.
+constexpr int kJ3mLag = 2;     // steps between consecutive row pairs
+constexpr int kJ3mWaves = 8;   // wavefronts per workgroup at most
+
+__device__ __forceinline__ void j3_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <typename T, int UC, int P>
+__global__ void __launch_bounds__(64 * kJ3mWaves) jeanie3m_fwd_kernel(JeanieArgs<T> a) {
+  constexpr int SPR = UC + 1, L = kJ3mLag;
+  extern __shared__ __align__(16) unsigned char j3m_lds[];
+  const int b = blockIdx.x;
+  const int W = (int)blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const int Tn = a.Tn, Un = a.Un, K = a.K;
+  bool vn;
+  const int n = pview(l32, P, a.K1, a.K2, &vn);
+  const T BIG = big_v<T>(), INF = inf_v<T>();
+  const int plane = Tn * Un, nrp = (Tn + 1) / 2, hl = (Tn - 1) & 1;
+  const bool w1 = a.s1 > 0, w2 = a.s2 > 0;
+  const int KR = (nrp + W - 1) / W, PER = SPR > L * W ? SPR : L * W;
+
+  // LDS: [W][SPR][32] slots (wavefront w reads block w, written by w - 1),
+  // then 64 slots that take half 0's stores
+  T* const hand = reinterpret_cast<T*>(j3m_lds);
+  T* const in_slot = hand + (size_t)wave * SPR * 32 + l32;
+  T* const out_slot = h ? hand + (size_t)(wave + 1 == W ? 0 : wave + 1) * SPR * 32 + l32
+                        : hand + (size_t)W * SPR * 32 + lane;
+
+  J3Lane<T> g;
+  g.init(n, h, a, false);
+  g.vn = vn;
+  Buf bC, bR;
+  bC.init(a.C + (size_t)b * K * plane, (long long)K * plane);
+  bR.init(a.Rw + (size_t)b * K * plane, (long long)K * plane);
+
+  T cr[SPR];
+  {
+    const int vb = g.base(wave);
+#pragma unroll
+    for (int v = 0; v < SPR; ++v) cr[v] = bC.ld<T>(g.at(vb, v), 0);
+  }
+  T rlast = BIG;
+  for (int i = 0; i < L * wave; ++i) j3_barrier();
+  for (int k = 0; k < KR; ++k) {
+    const int r = wave + k * W;
+    const int vb = g.base(r), vbn = g.base(r + W);
+    T left = BIG, pup = BIG, xch = BIG;
+#pragma unroll
+    for (int v = 0; v < SPR; ++v) {
+      const bool valid = vb != kOob && g.col_ok(v);
+      const T ch = cr[v] * a.k;
+      // half 0: the row above at column v (none above row 0, nor at column
+      // UC, outside every row)
+      const T up = h ? xch : ((r == 0 || v == UC) ? BIG : in_slot[v * 32]);
+      const T dg = v == 0 ? ((r == 0 && h == 0) ? (T)0 : BIG) : pup;
+      T rh = ch + softmin3h(up, left, dg);
+      rh = valid ? rh : BIG;
+      const T s2h = w2 ? (valid ? pwin<1>(rh) : BIG) : rh;
+      const T rw = w1 ? pwin<P>(s2h) : s2h;
+      bR.st(rh * a.inv_k, valid ? g.at(vb, v) : kOob, 0);
+      if (r == nrp - 1 && v == Un - 1 + hl) rlast = rh;
+      left = rw;
+      pup = up;
+      xch = swap_halves(rw);
+      // half 1: column v - 1 of its row, for the next row pair's half 0
+      if (v >= 1) *(h ? out_slot + (v - 1) * 32 : out_slot) = rw;
+      cr[v] = bC.ld<T>(g.at(vbn, v), 0);
+      j3_barrier();
+    }
+    for (int i = SPR; i < PER; ++i) j3_barrier();
+  }
+  for (int i = 0; i < L * (W - 1 - wave); ++i) j3_barrier();
+  if (wave != (nrp - 1) % W) return;
+  T m = vn ? rlast : INF;
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) m = fmin(m, __shfl_xor(m, o));
+  T s = (vn && m < INF) ? ex2(m - rlast) : (T)0;
+#pragma unroll
+  for (int o = 1; o < 32; o <<= 1) s += __shfl_xor(s, o);
+  if (h == hl && lane % 32 == 0) a.out[b] = (m - lg2(s)) * a.inv_k;
+}
+
+template <typename T, int UC, int P, bool PS>
+__global__ void __launch_bounds__(64 * kJ3mWaves) jeanie3m_bwd_kernel(JeanieArgs<T> a) {
+  constexpr int SPR = UC + 1, L = kJ3mLag;
+  extern __shared__ __align__(16) unsigned char j3m_lds[];
+  const int b = blockIdx.x;
+  const int W = (int)blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const int Tn = a.Tn, K = a.K;
+  bool vn;
+  const int n = pview(l32, P, a.K1, a.K2, &vn);
+  const T BIG = big_v<T>(), INF = inf_v<T>();
+  const int plane = Tn * a.Un, nrp = (Tn + 1) / 2;
+  const T gout = a.gout[b];
+  const bool has_gr = a.gR != nullptr;
+  const bool w1 = a.s1 > 0, w2 = a.s2 > 0;
+  const int KR = (nrp + W - 1) / W, PER = SPR > L * W ? SPR : L * W;
+
+  FG<T>* const hand = reinterpret_cast<FG<T>*>(j3m_lds);
+  FG<T>* const in_slot = hand + (size_t)wave * SPR * 32 + l32;
+  FG<T>* const out_slot = h ? hand + (size_t)(wave + 1 == W ? 0 : wave + 1) * SPR * 32 + l32
+                            : hand + (size_t)W * SPR * 32 + lane;
+
+  J3Lane<T> g;
+  g.init(n, h, a, true);
+  g.vn = vn;
+  const size_t pb = (size_t)b * K * plane;
+  Buf bC, bR, bG, bD;
+  bC.init(a.C + pb, (long long)K * plane);
+  bR.init(a.R + pb, (long long)K * plane);
+  bG.init(has_gr ? a.gR + pb : a.C, has_gr ? (long long)K * plane : 0);
+  bD.init(a.dC + pb, (long long)K * plane);
+
+  const FG<T> none = {-INF, (T)0};
+  T rr[SPR], rc[SPR], rg[SPR];
+  {
+    const int vb = g.base(wave);
+#pragma unroll
+    for (int v = 0; v < SPR; ++v) {
+      const int o = g.at(vb, v);
+      rr[v] = bR.ld<T>(o, 0);
+      rc[v] = bC.ld<T>(o, 0);
+      rg[v] = bG.ld<T>(o, 0);
+    }
+  }
+  for (int i = 0; i < L * wave; ++i) j3_barrier();
+  for (int k = 0; k < KR; ++k) {
+    const int r = wave + k * W;
+    const int vb = g.base(r), vbn = g.base(r + W);
+    FG<T> left = none, pup = none, xch = none;
+#pragma unroll
+    for (int v = 0; v < SPR; ++v) {
+      const bool valid = vb != kOob && g.col_ok(v);
+      const T rh = valid ? rr[v] * a.k : BIG;
+      const T ch = rc[v] * a.k;
+      // (selected by component: a select of the structs would take their
+      // addresses and put xch in scratch memory)
+      FG<T> lu = none;
+      if (r != 0 && v != UC) lu = in_slot[v * 32];
+      const FG<T> up = {h ? xch.f : lu.f, h ? xch.g : lu.g};
+      const FG<T> dg = v == 0 ? none : pup;
+      const T s2h = w2 ? (valid ? pwin<1>(rh) : BIG) : rh;
+      const T rwh = w1 ? pwin<P>(s2h) : s2h;
+      const T wbar = up.g * ex2(up.f - rwh) + left.g * ex2(left.f - rwh) + dg.g * ex2(dg.f - rwh);
+      const T s2bar = w1 ? pwin_adj<P>(wbar, valid ? rwh : (T)0, s2h) : wbar;
+      T rbar = w2 ? pwin_adj<1>(s2bar, valid ? s2h : (T)0, rh) : s2bar;
+      if (v == 0 && r == 0) {
+        // the last cell (T-1, U-1) (half 0): seed with grad_out * softmax_n(-R/g)
+        T m = valid ? rh : INF;
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) m = fmin(m, __shfl_xor(m, o));
+        T s = valid ? ex2(m - rh) : (T)0;
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) s += __shfl_xor(s, o);
+        rbar += valid ? gout * ex2(m - lg2(s) - rh) : (T)0;
+      }
+      if (has_gr) rbar += rg[v];
+      const FG<T> cur = {valid ? rh - ch : -INF, rbar};
+      if constexpr (PS) {
+        const bool pair = ((h + v) & 1) && v >= 1 + h;
+        st_pair<T>(bD, (valid && pair) ? g.at(vb, v) : kOob, rbar, left.g);
+      } else {
+        bD.st(rbar, valid ? g.at(vb, v) : kOob, 0);
+      }
+      left = cur;
+      pup = up;
+      xch = {swap_halves(cur.f), swap_halves(cur.g)};
+      if (v >= 1) *(h ? out_slot + (v - 1) * 32 : out_slot) = cur;
+      const int o = g.at(vbn, v);
+      rr[v] = bR.ld<T>(o, 0);
+      rc[v] = bC.ld<T>(o, 0);
+      rg[v] = bG.ld<T>(o, 0);
+      j3_barrier();
+    }
+    for (int i = SPR; i < PER; ++i) j3_barrier();
+  }
+  for (int i = 0; i < L * (W - 1 - wave); ++i) j3_barrier();
+}
+
 // Row length the kernels are compiled for: the smallest of 8, 16, 32 that
 // holds U (16 in float64), 0 beyond. Longer rows would not unroll into
 // registers; they use the workgroup-per-pair kernels.
@@ -752,6 +950,42 @@ static void j3p_launch_uc(bool bwd, int uc, const JeanieArgs<T>& a, int B, hipSt
 #undef TW_J3P
 }
 
+// Several wavefronts per pair (W of them, 2 <= W <= kJ3mWaves).
+template <typename T, int P>
+static void j3m_launch_uc(bool bwd, int uc, int W, const JeanieArgs<T>& a, int B, hipStream_t s) {
+  const bool ps = a.Un == uc && !a.swap && (((size_t)a.dC / sizeof(T)) & 1) == 0;
+  const size_t elem = bwd ? 2 * sizeof(T) : sizeof(T);
+  const size_t lds = ((size_t)W * (uc + 1) * 32 + 64) * elem;
+  const dim3 grid((unsigned)B), block((unsigned)(64 * W));
+#define TW_J3M(UC_)                                                                              \
+  do {                                                                                           \
+    if (bwd && ps)                                                                               \
+      hipLaunchKernelGGL((jeanie3m_bwd_kernel<T, UC_, P, true>), grid, block, lds, s, a);        \
+    else if (bwd)                                                                                \
+      hipLaunchKernelGGL((jeanie3m_bwd_kernel<T, UC_, P, false>), grid, block, lds, s, a);       \
+    else                                                                                         \
+      hipLaunchKernelGGL((jeanie3m_fwd_kernel<T, UC_, P>), grid, block, lds, s, a);              \
+  } while (0)
+  switch (uc) {
+    case 8: TW_J3M(8); break;
+    case 16: TW_J3M(16); break;
+    default:
+      if constexpr (sizeof(T) == 4) TW_J3M(32);
+      break;
+  }
+#undef TW_J3M
+}
+
+// TORCHWARP_JEANIE_MW: 0 keeps one wavefront per pair in the padded-lane
+// sweeps; otherwise (unset) pairs of two row pairs or more take several.
+static int j3m_mode() {
+  static const int mode = [] {
+    const char* e = getenv("TORCHWARP_JEANIE_MW");
+    return e ? atoi(e) : -1;
+  }();
+  return mode;
+}
+
 template <typename T>
 static int j3_run(bool bwd, const JeanieArgs<T>& a, int B, hipStream_t s, const char* what) {
   const int uc = j3_uc<T>(a.Un);
@@ -763,10 +997,30 @@ static int j3_run(bool bwd, const JeanieArgs<T>& a, int B, hipStream_t s, const 
   // strides 1 and 6 built (one viewpoint axis, and 5 x 5 viewpoints)
   const int P = a.K2 + (a.s2 > 0 ? 1 : 0);
   if (a.s1 <= 1 && a.s2 <= 1 && a.K1 * P < 32 && (P == 1 || P == 6)) {
-    if (P == 1)
+    // Wavefronts per pair: one while the batch fills half the SIMDs with a
+    // wavefront per pair (lockstep wavefronts sharing SIMDs with other
+    // workgroups' measured slower than one wavefront walking the whole pair:
+    // cfg5a, 1024 pairs, W = 2: backward 50.9 -> 55.7 us); below that about
+    // two per SIMD over the batch, at most one per row pair (cfg4, 400 pairs,
+    // W = 4: 0.066 -> 0.059 ms per step).
+    const int nrp = (a.Tn + 1) / 2;
+    const long long simds = 4LL * num_cus();
+    int W = 1;
+    if (2LL * B <= simds) {
+      const long long w = (2 * simds + B - 1) / (B > 0 ? B : 1);
+      W = (int)(w < nrp ? w : nrp);
+      W = W < kJ3mWaves ? W : kJ3mWaves;
+    }
+    if (W >= 2 && j3m_mode() != 0) {
+      if (P == 1)
+        j3m_launch_uc<T, 1>(bwd, uc, W, a, B, s);
+      else
+        j3m_launch_uc<T, 6>(bwd, uc, W, a, B, s);
+    } else if (P == 1) {
       j3p_launch_uc<T, 1>(bwd, uc, a, B, s);
-    else
+    } else {
       j3p_launch_uc<T, 6>(bwd, uc, a, B, s);
+    }
     return check_launch(what);
   }
   if (a.s1 > 1 || a.s2 > 1)
