@@ -82,21 +82,23 @@ def test_banded_sweep_matches_oracle(case):
     assert float(c.grad[:, out].abs().max()) == 0.0
 
 
+@pytest.mark.parametrize("band", [20.0, 0.0], ids=["banded", "general"])
 @pytest.mark.parametrize("dtype", [torch.float32, f64], ids=["f32", "f64"])
-def test_banded_backward_with_gradients_at_odd_offsets(dtype):
-    """The banded backward stores the gradients in aligned pairs of cells,
+def test_backward_with_gradients_at_odd_offsets(dtype, band):
+    """The cost-path backwards (the banded sweep, and the general sweep
+    without a band) store the gradients in aligned pairs of row neighbours,
     chosen by the parity of each cell's address. Here d_cost starts at an odd
     element offset and d_pen at an even one, with N M odd (the pairs' parity
     alternates between batch entries), through the C ABI; against the oracle."""
     from torchwarp_amd import _hip
-    B, N, M, gamma, band = 3, 151, 163, 0.5, 20.0
+    B, N, M, gamma = 3, 151, 163, 0.5
     g = torch.Generator().manual_seed(7)
     C = 3.0 * torch.rand(B, N, M, generator=g, dtype=f64)
     Q = 0.5 * torch.rand(B, N, M, generator=g, dtype=f64)
     wr = torch.rand(B, generator=g, dtype=f64) + 0.5
     wp = torch.rand(B, generator=g, dtype=f64) + 0.5
     rc, rq = C.clone().requires_grad_(True), Q.clone().requires_grad_(True)
-    rd, rp = OU.udtw_from_cost(rc, rq, gamma=gamma, bandwidth=band)
+    rd, rp = OU.udtw_from_cost(rc, rq, gamma=gamma, bandwidth=band or None)
     (rd * wr + rp * wp).sum().backward()
 
     dev = lambda t: t.to("cuda", dtype).contiguous()

@@ -114,19 +114,20 @@ struct Buf {
 template <> __device__ __forceinline__ float Buf::ld<float>(int v, int s) const { return ldf(v, s); }
 template <> __device__ __forceinline__ double Buf::ld<double>(int v, int s) const { return ldd(v, s); }
 
-// Two consecutive elements x0 (at byte offset v) and x1 as one store, which
-// must be aligned to its size (8 bytes for float, 16 for double).
+// Two consecutive elements x0 (at byte offset v + s, s wave-uniform) and x1
+// as one store, which must be aligned to its size (8 bytes for float, 16 for
+// double).
 template <typename T>
-__device__ __forceinline__ void st_pair(const Buf& b, int v, T x0, T x1) {
+__device__ __forceinline__ void st_pair(const Buf& b, int v, T x0, T x1, int s = 0) {
   if constexpr (sizeof(T) == 4) {
     const u32x2 w = {__float_as_uint(x0), __float_as_uint(x1)};
-    __builtin_amdgcn_raw_buffer_store_b64(w, b.r, v, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b64(w, b.r, v, s, 0);
   } else {
     typedef unsigned int u4 __attribute__((ext_vector_type(4)));
     const unsigned long long u0 = (unsigned long long)__double_as_longlong(x0);
     const unsigned long long u1 = (unsigned long long)__double_as_longlong(x1);
     const u4 w = {(unsigned)u0, (unsigned)(u0 >> 32), (unsigned)u1, (unsigned)(u1 >> 32)};
-    __builtin_amdgcn_raw_buffer_store_b128(w, b.r, v, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(w, b.r, v, s, 0);
   }
 }
 

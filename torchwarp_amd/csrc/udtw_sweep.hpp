@@ -794,10 +794,18 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true, MW>::value)) ud
   T g1[ROWS], g2[ROWS], h1[ROWS], h2[ROWS], a1[ROWS], a2[ROWS];
   T yc[ROWS], hyc[ROWS], cy[ROWS], cvy[ROWS];
   int vst[ROWS], vsr[ROWS], vnat[ROWS], jb[ROWS], vrow0[ROWS];
+  // SRC_COST: parity of the element index of (i, d - i) in dC / dQ, less d
+  // (the gradients leave in aligned pairs of row neighbours)
+  int cpar[ROWS], qpar[ROWS];
 #pragma unroll
   for (int k = 0; k < ROWS; ++k) {
     const int i = row0 + k;
     const bool in = i >= 0 && i < N;
+    if (SRC == SRC_COST) {
+      const size_t rowc = (size_t)b * NM + (size_t)(in ? i : 0) * (M - 1);
+      cpar[k] = (int)((((size_t)a.dC / ES) + rowc) & 1);
+      qpar[k] = want_dq ? (int)((((size_t)a.dQ / ES) + rowc) & 1) : 0;
+    }
     xr[k] = (SRC == SRC_FEAT1 && in) ? a.X[(size_t)b * N + i] : (T)0;
     hxr[k] = (COLS && in) ? half_var(a, a.VX[(size_t)b * N + i]) : (T)0.5;
     dxr[k] = dvr[k] = (T)0;
@@ -1183,8 +1191,19 @@ __global__ void __launch_bounds__((MaxThreads<T, ROWS, LC, true, MW>::value)) ud
 
           const int vn = valid ? vnat[k] : kOob;
           if (SRC == SRC_COST) {
-            bdC.st(g, vn, so_n);
-            if (PEN) bdQ.st(h, vn, so_n);
+            // (i, j) with an even element index stores itself and (i, j + 1),
+            // the lane's previous cell (g1, h1), as one aligned store; an odd
+            // one is stored by (i, j - 1)'s pair; left over: even cells in
+            // column M - 1 and odd ones in column 0, stored alone
+            const int j = d + jb[k];
+            const bool ec = ((cpar[k] ^ d) & 1) == 0;
+            st_pair<T>(bdC, (valid && ec && j + 1 < M) ? vn : kOob, g, g1[k], so_n);
+            bdC.st(g, (valid && (ec ? j == M - 1 : j == 0)) ? vn : kOob, so_n);
+            if (PEN) {
+              const bool eq = ((qpar[k] ^ d) & 1) == 0;
+              st_pair<T>(bdQ, (valid && eq && j + 1 < M) ? vn : kOob, h, h1[k], so_n);
+              bdQ.st(h, (valid && (eq ? j == M - 1 : j == 0)) ? vn : kOob, so_n);
+            }
           } else {
             if (SRC == SRC_SQ)
               bdC.st(dsq, valid ? vst[k] : kOob, __builtin_amdgcn_readlane(so_sd, t0 + u));
