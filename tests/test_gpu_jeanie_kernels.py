@@ -36,6 +36,9 @@ CASES = [  # (B, K1, K2, T, U, (s1, s2), gamma)
     (3, 9, 1, 9, 8, (1, 0), 0.2),      # one axis, several wavefronts
     (600, 9, 1, 8, 8, (1, 0), 0.2),    # one axis, one wavefront per pair
     (600, 5, 5, 12, 16, (1, 1), 0.1),  # 5 x 5, one wavefront per pair
+    # full rows (U equal to the compiled row length): dC in pairs of cells
+    (2, 3, 4, 6, 16, (1, 1), 0.1),     # general wavefront kernel, stride-4 exchange
+    (2, 2, 5, 7, 8, (2, 1), 0.2),      # general wavefront kernel, shift 2
 ]
 
 

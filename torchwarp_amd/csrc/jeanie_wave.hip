@@ -352,7 +352,8 @@ struct alignas(2 * sizeof(T)) FG {
   T f, g;   // F = Rh - Ch and G = Rbar of a cell
 };
 
-template <typename T, int SMAX, int UC, int KS>
+// PS: dC in aligned pairs of row neighbours (as jeanie3p_bwd_kernel's PS).
+template <typename T, int SMAX, int UC, int KS, bool PS>
 __global__ void __launch_bounds__(64) jeanie3_bwd_kernel(JeanieArgs<T> a) {
   constexpr int SPR = UC + 1;
   const int b = blockIdx.x;
@@ -425,7 +426,12 @@ __global__ void __launch_bounds__(64) jeanie3_bwd_kernel(JeanieArgs<T> a) {
       if (has_gr) rbar += rg[v];
       rbar = valid ? rbar : (T)0;
       const FG<T> cur = {valid ? rh - ch : -INF, rbar};
-      bD.st(rbar, valid ? g.at(vb, v) : kOob, 0);
+      if constexpr (PS) {
+        const bool pair = ((h + v) & 1) && v >= 1 + h;
+        st_pair<T>(bD, (valid && pair) ? g.at(vb, v) : kOob, rbar, left.g);
+      } else {
+        bD.st(rbar, valid ? g.at(vb, v) : kOob, 0);
+      }
       left = cur;
       pup = up;
       xch = {swap_halves(cur.f), swap_halves(cur.g)};
@@ -898,8 +904,12 @@ static int j3_uc(int Un) {
 
 template <typename T, int SMAX, int UC, int KS>
 static void j3_launch(bool bwd, const JeanieArgs<T>& a, int B, hipStream_t s) {
-  if (bwd)
-    hipLaunchKernelGGL((jeanie3_bwd_kernel<T, SMAX, UC, KS>), dim3(B), dim3(64), 0, s, a);
+  // pair stores of dC: full rows, not transposed, even element index at dC
+  const bool ps = a.Un == UC && !a.swap && (((size_t)a.dC / sizeof(T)) & 1) == 0;
+  if (bwd && ps)
+    hipLaunchKernelGGL((jeanie3_bwd_kernel<T, SMAX, UC, KS, true>), dim3(B), dim3(64), 0, s, a);
+  else if (bwd)
+    hipLaunchKernelGGL((jeanie3_bwd_kernel<T, SMAX, UC, KS, false>), dim3(B), dim3(64), 0, s, a);
   else
     hipLaunchKernelGGL((jeanie3_fwd_kernel<T, SMAX, UC, KS>), dim3(B), dim3(64), 0, s, a);
 }
