@@ -44,6 +44,11 @@ CASES = {
                  lambda xs: tw.SoftDTW(gamma=0.5)(*xs).mean()),
     "udtw_from_cost": ([((3, 17, 23), 1), ((3, 17, 23), 1)],
                        lambda xs: sum(TF.udtw_from_cost(xs[0], xs[1], gamma=0.3)).sum()),
+    # a band narrower than the grid: the banded sweep (band-compressed planes,
+    # the zeroing workgroups in the backward's launch)
+    "udtw_from_cost_band": ([((3, 40, 44), 1), ((3, 40, 44), 1)],
+                            lambda xs: sum(TF.udtw_from_cost(xs[0], xs[1], gamma=0.3,
+                                                             bandwidth=6.0)).sum()),
     # N > 256 and a small batch: several workgroups per pair in the forward
     # (sentinel fill kernel, polled hand-off between workgroups)
     "udtw_d1_groups": ([((2, 600, 1), 0), ((2, 620, 1), 0), ((2, 600, 1), 1),
