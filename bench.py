@@ -39,11 +39,12 @@ METRIC = ("DP cells/sec & pairs/sec fwd+bwd (uDTW B=256 N=M=140; JEANIE K=25), "
 SETTLE_S = 0.25    # minimum untimed warm-up per config (seconds)
 LAST_TIMES = {}   # label -> mean ms of every kernel timed by the last _hip_call_times
 EAGER_MS = {}     # config -> ms per eagerly run step (run_config with mode "eager"/"both")
-CONFIGS = ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5a", "cfg5b", "cost", "cost_band")
+CONFIGS = ("cfg1", "cfg2", "cfg3", "cfg4", "cfg5a", "cfg5b", "cost", "cost_band", "cfg3_band")
 # The cost-path workloads beside the BASELINE configs: uDTW on precomputed
 # matrices, B = 64, N = M = 1024, gamma = 1, without a band ("cost") and with
 # a Sakoe-Chiba band of 102 ("cost_band", the banded sweep; its cells are the
-# band's cells).
+# band's cells). "cfg3_band": cfg3's features with the same band (the banded
+# feature path; its cells are the band's cells).
 BAND = 102
 
 
@@ -63,7 +64,7 @@ def make_inputs(name, device="cpu", dtype=torch.float32):
         X, Y = _walk(g, 256, 140), _walk(g, 256, 140)
         sx, sy = 0.5 + torch.rand(256, 140, 1, generator=g), 0.5 + torch.rand(256, 140, 1, generator=g)
         t = (X, Y, sx, sy)
-    elif name == "cfg3":
+    elif name in ("cfg3", "cfg3_band"):
         X, Y = torch.randn(64, 1024, 16, generator=g), torch.randn(64, 1024, 16, generator=g)
         sx, sy = 0.5 + torch.rand(64, 1024, 1, generator=g), 0.5 + torch.rand(64, 1024, 1, generator=g)
         t = (X, Y, sx, sy)
@@ -93,6 +94,7 @@ def work(name):
         "cfg5b": dict(cells=1024 * 16 * 16, pairs=1024),
         "cost": dict(cells=64 * 1024 * 1024, pairs=64),
         "cost_band": dict(cells=64 * (1024 * (2 * BAND + 1) - BAND * (BAND + 1)), pairs=64),
+        "cfg3_band": dict(cells=64 * (1024 * (2 * BAND + 1) - BAND * (BAND + 1)), pairs=64),
     }[name]
 
 
@@ -109,9 +111,9 @@ def step_fn(name, inputs):
             x = X.detach().requires_grad_(True)
             m(x, Y).mean().backward()
         return f
-    if name in ("cfg2", "cfg3"):
+    if name in ("cfg2", "cfg3", "cfg3_band"):
         gamma = 1.0 if name == "cfg2" else 0.1
-        m = tw.UDTW(gamma=gamma, beta=1.0)
+        m = tw.UDTW(gamma=gamma, beta=1.0, bandwidth=BAND if name == "cfg3_band" else None)
         X, Y, sx, sy = inputs
 
         def f():
@@ -159,7 +161,7 @@ def _hip_call_times(name, inputs, iters):
     stream = torch.cuda.current_stream(dev)
     f32 = torch.float32
     calls = []
-    if name in ("cfg1", "cfg2", "cfg3"):
+    if name in ("cfg1", "cfg2", "cfg3", "cfg3_band"):
         # standard deviations, squared inside the kernels (as the public API calls them)
         if name == "cfg1":
             X, Y = inputs
@@ -173,6 +175,7 @@ def _hip_call_times(name, inputs, iters):
         B, N, D = X.shape
         M = Y.shape[1]
         pen = beta != 0
+        band = float(BAND) if name == "cfg3_band" else 0.0
         R = X.new_empty(B, _hip.carry_cols(N, M, gamma, X.dtype))
         P = X.new_empty(B, N * M) if pen else None
         o1, o2 = X.new_empty(B), X.new_empty(B)
@@ -185,13 +188,18 @@ def _hip_call_times(name, inputs, iters):
         # R and P at 4 B/cell each (fp32); where the kernels keep R in double
         # precision (long sequences, small gamma) its extra 4 B/cell count as
         # overhead, not as algorithmic bytes
-        carried = 4 * B * N * M * (2 if pen else 1)
+        # (with a band: of the band's cells)
+        carried = 4 * work(name)["cells"] * (2 if pen else 1)
+        # the banded path's backward reads the forward's band planes, as the
+        # public API passes them (fwd_ws)
+        fwd_ws = X.new_empty(nws) if band > 0 else None
+        bwd_ws = ws if fwd_ws is None else X.new_empty(nws)
         calls.append(("udtw_fwd", lambda: _hip.call(
-            "tw_udtw_feat_fwd", f32, X, Y, vx, vy, B, N, M, D, gamma, beta, 1e-8, 0.0, 1, R, P,
-            o1, o2, ws, wsb), io + carried))
+            "tw_udtw_feat_fwd", f32, X, Y, vx, vy, B, N, M, D, gamma, beta, 1e-8, band, 1, R, P,
+            o1, o2, ws if fwd_ws is None else fwd_ws, wsb), io + carried))
         calls.append(("udtw_bwd", lambda: _hip.call(
             "tw_udtw_feat_bwd", f32, X, Y, vx, vy, R, P, g, g if pen else None, B, N, M, D, gamma,
-            beta, 1e-8, 0.0, 1, 1, dX, dY, dvx, dvy, None, ws, wsb), 2 * io + carried))
+            beta, 1e-8, band, 1, 1, dX, dY, dvx, dvy, fwd_ws, bwd_ws, wsb), 2 * io + carried))
     elif name in ("cost", "cost_band"):
         C, Q = inputs
         B, N, M = C.shape
@@ -280,7 +288,12 @@ def cpu_baseline(name, budget_s=10.0):
     w = work(name)
 
     def once():
-        if name in ("cfg1", "cfg2", "cfg3"):
+        if name == "cfg3_band":
+            # a bounded sample: 2 of the 64 pairs (cells scaled below)
+            X, Y, sx, sy = (t[:2].clone().requires_grad_(True) for t in inp)
+            d, p = OU.udtw(X, Y, sx, sy, gamma=0.1, beta=1.0, bandwidth=BAND)
+            (d + p).sum().backward()
+        elif name in ("cfg1", "cfg2", "cfg3"):
             if name == "cfg1":
                 X, Y = inp
                 vx = torch.ones(X.shape[:2])
@@ -319,7 +332,7 @@ def cpu_baseline(name, budget_s=10.0):
         el = time.perf_counter() - t0
         if el >= budget_s or n >= 50:
             break
-    share = 2 / 64 if name in ("cost", "cost_band") else 1.0   # pairs of the batch run
+    share = 2 / 64 if name in ("cost", "cost_band", "cfg3_band") else 1.0   # pairs run
     return {"value": w["cells"] * share * n / el, "unit": "cells/s", "cores": cores,
             "kind": "port", "cpu_model": _cpu_model(),
             "pairs_per_s": w["pairs"] * share * n / el,

@@ -220,16 +220,19 @@ __device__ __forceinline__ int end_slot(int N, int M, int w) { return (N - M + w
 
 // ------------------------------------------------------------ forward
 
-template <typename T, typename RT, int S, bool PEN, int WP>
+// BIO: C and Q in the band layout [B][D][NS] (slot m of diagonal d at
+// d NS + m) instead of [B, N, M].
+template <typename T, typename RT, int S, bool PEN, int WP, bool BIO>
 __global__ void __launch_bounds__(64) udtw_band_fwd(BandArgs<T, RT> a) {
   constexpr int PD = 8;   // prefetch distance (steps) = unroll of the step loop
   const int b = blockIdx.x, lane = threadIdx.x;
   const int N = a.N, M = a.M, w = a.w, NS = a.NS, D = a.D;
   const RT BIG = band_big<RT>();
   const size_t nm = (size_t)N * M, bsz = (size_t)2 * D * NS;
+  const size_t isz = BIO ? (size_t)D * NS : nm;
   Buf bc, bq, br, bp;
-  bc.init(a.C + b * nm, (long long)nm);
-  if (PEN) bq.init(a.Q + b * nm, (long long)nm);
+  bc.init(a.C + b * isz, (long long)isz);
+  if (PEN) bq.init(a.Q + b * isz, (long long)isz);
   br.init(a.R + b * bsz, (long long)bsz);
   if (PEN) bp.init(a.P + b * bsz, (long long)bsz);
   constexpr int es = (int)sizeof(T), rs = (int)sizeof(RT);
@@ -255,12 +258,19 @@ __global__ void __launch_bounds__(64) udtw_band_fwd(BandArgs<T, RT> a) {
   // ring of the inputs PD steps ahead: [step mod PD][slot]
   T cr[PD][S], qr[PD][S];
   auto fetch = [&](int d, int u) {
-    const int p = (u & 1) ^ WP;
+    if constexpr (BIO) {
+      // the lane's S slots as one access; rows d >= D lie past the planes
+      const int o = lane_in ? (d * NS + m0) * es : kOob;
+      ld_slots<T, S>(bc, o, cr[u]);
+      if (PEN) ld_slots<T, S>(bq, o, qr[u]);
+    } else {
+      const int p = (u & 1) ^ WP;
 #pragma unroll
-    for (int s = 0; s < S; ++s) {
-      const int o = sc[p][s].off(d, M, es);
-      cr[u][s] = bc.ld<T>(o, 0);
-      if (PEN) qr[u][s] = bq.ld<T>(o, 0);
+      for (int s = 0; s < S; ++s) {
+        const int o = sc[p][s].off(d, M, es);
+        cr[u][s] = bc.ld<T>(o, 0);
+        if (PEN) qr[u][s] = bq.ld<T>(o, 0);
+      }
     }
   };
   // in ring order: the loop's first use of each entry then waits only for
@@ -379,10 +389,13 @@ __device__ void band_zero_rows(T* dC, T* dQ, int B, int N, int M, int w, int z, 
   }
 }
 
-template <typename T, typename RT, int S, bool PEN, int WP>
+// BIO: dC and dQ in the band layout [B][D][NS], every slot of every
+// diagonal written (0 off the grid), and no zeroing outside the band.
+template <typename T, typename RT, int S, bool PEN, int WP, bool BIO>
 __global__ void __launch_bounds__(64) udtw_band_bwd(BandArgs<T, RT> a) {
   if ((int)blockIdx.x >= a.B) {
-    band_zero_rows<T>(a.dC, a.dQ, a.B, a.N, a.M, a.w, (int)blockIdx.x - a.B, a.nzero);
+    if constexpr (!BIO)
+      band_zero_rows<T>(a.dC, a.dQ, a.B, a.N, a.M, a.w, (int)blockIdx.x - a.B, a.nzero);
     return;
   }
   // prefetch distance (steps, even): as deep as the memory counter (63
@@ -392,13 +405,14 @@ __global__ void __launch_bounds__(64) udtw_band_bwd(BandArgs<T, RT> a) {
   const int N = a.N, M = a.M, w = a.w, NS = a.NS, D = a.D;
   const RT NEG = -band_big<RT>();
   const size_t nm = (size_t)N * M, bsz = (size_t)2 * D * NS;
+  const size_t osz = BIO ? (size_t)D * NS : nm;
   Buf br, bp, bdc, bdq;
   br.init(a.R + b * bsz, (long long)bsz);
   if (PEN) bp.init(a.P + b * bsz, (long long)bsz);
-  bdc.init(a.dC + b * nm, (long long)nm);
+  bdc.init(a.dC + b * osz, (long long)osz);
   // without dQ, an empty range: its stores are dropped
   const bool has_dq = PEN && a.dQ != nullptr;
-  if (PEN) bdq.init(has_dq ? a.dQ + b * nm : a.dC, has_dq ? (long long)nm : 0LL);
+  if (PEN) bdq.init(has_dq ? a.dQ + b * osz : a.dC, has_dq ? (long long)osz : 0LL);
   constexpr int es = (int)sizeof(T), rs = (int)sizeof(RT);
   const T gR = a.gr[(size_t)b * a.gstride];
   const T gP = PEN ? a.gp[(size_t)b * a.gstride] : (T)0;
@@ -512,6 +526,7 @@ __global__ void __launch_bounds__(64) udtw_band_bwd(BandArgs<T, RT> a) {
           G -= (wdn * adn * (pk - bdn) + wrt * art * (pk - brt) + wdg * adg * (pk - bdg)) *
                a.inv_gamma;
         }
+        if constexpr (!BIO) {
         // (i, j) and its right successor (i, j + 1), G = grt, A = art
         st_pair<T>(bdc, pc[p][s].pair_off(d, M, esh, par_c), G, grt);
         if (PEN) {
@@ -530,10 +545,18 @@ __global__ void __launch_bounds__(64) udtw_band_bwd(BandArgs<T, RT> a) {
             if (PEN) bdq.st(A, one_q ? (int)(raw << esh) : kOob, 0);
           }
         }
+        }
         ne[s] = bsel(rbr[u][s], NEG, keep);
         ng[s] = G;
         na[s] = A;
         nb[s] = PEN ? pbr[u][s] : (T)0;
+      }
+      if constexpr (BIO) {
+        // the lane's S slots as one access; rows d < 0 have negative
+        // offsets, out of the buffer's range as unsigned
+        const int o = lane_in ? (d * NS + m0) * es : kOob;
+        st_slots<T, S>(bdc, o, ng);
+        if (PEN) st_slots<T, S>(bdq, o, na);
       }
 #pragma unroll
       for (int s = 0; s < S; ++s) {
@@ -578,32 +601,33 @@ int band_slots(int w) {
   return ns <= 64 ? 1 : (ns <= 128 ? 2 : (ns <= 256 ? 4 : 0));
 }
 
-template <typename T, typename RT, int S, bool PEN>
+template <typename T, typename RT, int S, bool PEN, bool BIO>
 int band_launch(bool bwd, const BandArgs<T, RT>& a, int B, hipStream_t s) {
   // parity of step 0 (forward) / of step D - 1 (backward)
   const int wp = bwd ? ((a.D - 1 + a.w) & 1) : (a.w & 1);
   if (bwd) {
     // The sweep's waves issue one dependent step after another: a wave of
     // the zeroing role beside one on its SIMD would take issue cycles from
-    // it. An LDS reservation (unused) of over half a CU's LDS keeps every
-    // workgroup on a CU of its own.
+    // it. While the sweep's workgroups leave CUs free, an LDS reservation
+    // (unused) of over half a CU's LDS keeps every workgroup on a CU of its
+    // own; with more pairs than CUs it would serialise the sweeps instead.
     const dim3 grid((unsigned)(B + a.nzero));
-    const size_t lds = (size_t)max_lds_bytes() / 2 + 256;
+    const size_t lds = a.nzero > 0 && B <= num_cus() ? (size_t)max_lds_bytes() / 2 + 256 : 0;
     if (wp)
-      hipLaunchKernelGGL((udtw_band_bwd<T, RT, S, PEN, 1>), grid, dim3(64), lds, s, a);
+      hipLaunchKernelGGL((udtw_band_bwd<T, RT, S, PEN, 1, BIO>), grid, dim3(64), lds, s, a);
     else
-      hipLaunchKernelGGL((udtw_band_bwd<T, RT, S, PEN, 0>), grid, dim3(64), lds, s, a);
+      hipLaunchKernelGGL((udtw_band_bwd<T, RT, S, PEN, 0, BIO>), grid, dim3(64), lds, s, a);
   } else {
     if (wp)
-      hipLaunchKernelGGL((udtw_band_fwd<T, RT, S, PEN, 1>), dim3(B), dim3(64), 0, s, a);
+      hipLaunchKernelGGL((udtw_band_fwd<T, RT, S, PEN, 1, BIO>), dim3(B), dim3(64), 0, s, a);
     else
-      hipLaunchKernelGGL((udtw_band_fwd<T, RT, S, PEN, 0>), dim3(B), dim3(64), 0, s, a);
+      hipLaunchKernelGGL((udtw_band_fwd<T, RT, S, PEN, 0, BIO>), dim3(B), dim3(64), 0, s, a);
   }
   return TW_OK;
 }
 
 template <typename T, typename RT>
-int band_run(bool bwd, const UdtwArgs<T>& u, int B, hipStream_t s, const char* what) {
+int band_run(bool bwd, bool bio, const UdtwArgs<T>& u, int B, hipStream_t s, const char* what) {
   BandArgs<T, RT> a;
   a.C = u.C;
   a.Q = u.Q;
@@ -627,14 +651,18 @@ int band_run(bool bwd, const UdtwArgs<T>& u, int B, hipStream_t s, const char* w
   a.B = B;
   // zeroing workgroups: at least 4 rows each, at most 1024
   const long long rows = (long long)B * u.N;
-  a.nzero = bwd ? (int)((rows + 3) / 4 < 1024 ? (rows + 3) / 4 : 1024) : 0;
+  a.nzero = bwd && !bio ? (int)((rows + 3) / 4 < 1024 ? (rows + 3) / 4 : 1024) : 0;
   a.k = u.k;
   a.inv_k = u.inv_k;
   a.inv_gamma = u.inv_gamma;
-  const bool pen = u.Q != nullptr;
-#define TW_BAND(S_)                                                       \
-  (pen ? band_launch<T, RT, S_, true>(bwd, a, B, s)                       \
-       : band_launch<T, RT, S_, false>(bwd, a, B, s))
+  // the penalty: given as Q on the cost path; from features (band_io) it is
+  // built when beta != 0, and the backward reads no Q
+  const bool pen = bio ? u.beta != (T)0 : u.Q != nullptr;
+#define TW_BAND(S_)                                                             \
+  (bio ? (pen ? band_launch<T, RT, S_, true, true>(bwd, a, B, s)                \
+              : band_launch<T, RT, S_, false, true>(bwd, a, B, s))              \
+       : (pen ? band_launch<T, RT, S_, true, false>(bwd, a, B, s)               \
+              : band_launch<T, RT, S_, false, false>(bwd, a, B, s)))
   if (S == 1)
     TW_BAND(1);
   else if (S == 2)
@@ -672,7 +700,8 @@ bool band_path(int N, int M, double band) {
 }
 
 template <typename T>
-int band_sweep(bool bwd, const UdtwArgs<T>& a, int B, hipStream_t s, const char* what) {
+int band_sweep(bool bwd, const UdtwArgs<T>& a, int B, hipStream_t s, const char* what,
+               bool band_io) {
   if (B == 0) return TW_OK;
   // planes are addressed with 32-bit byte offsets within a pair
   const long long rbytes = a.rd ? 8 : (long long)sizeof(T);
@@ -680,11 +709,467 @@ int band_sweep(bool bwd, const UdtwArgs<T>& a, int B, hipStream_t s, const char*
     return fail(TW_ESIZE, "%s: one pair's N*M matrix (%d x %d) must stay below 2 GiB", what,
                 a.N, a.M);
   }
-  if (sizeof(T) == 4 && a.rd) return band_run<T, double>(bwd, a, B, s, what);
-  return band_run<T, T>(bwd, a, B, s, what);
+  if (sizeof(T) == 4 && a.rd) return band_run<T, double>(bwd, band_io, a, B, s, what);
+  return band_run<T, T>(bwd, band_io, a, B, s, what);
 }
 
-template int band_sweep<float>(bool, const UdtwArgs<float>&, int, hipStream_t, const char*);
-template int band_sweep<double>(bool, const UdtwArgs<double>&, int, hipStream_t, const char*);
+template int band_sweep<float>(bool, const UdtwArgs<float>&, int, hipStream_t, const char*, bool);
+template int band_sweep<double>(bool, const UdtwArgs<double>&, int, hipStream_t, const char*,
+                                bool);
+
+// ----------------------------------------------------- from features (F > 1)
+//
+// The band's cost C = max(S, 0) / var and penalty Q = beta ln var, S the
+// squared distance of rows i and j, var = max(h(vx_i) + h(vy_j), eps), are
+// built only inside the band, in the band layout the sweep reads: element
+// d NS + m of a pair's plane holds the cell of slot m on diagonal d (0 off
+// the grid). The backward sweep leaves dC / dQ in the same layout, and the
+// feature gradients are reduced from them row by row and column by column.
+
+namespace {
+
+template <typename T>
+struct BandFeat {
+  const T *X, *Y, *VX, *VY;   // [B,N,F], [B,M,F], [B,N], [B,M]
+  T *Cb, *Qb;                 // band layout [B][D][NS] (Qb null without a penalty)
+  const T *dCb, *dQb;         // the backward sweep's gradients, same layout
+  T *dX, *dY, *dVX, *dVY;     // dVX / dVY may be null
+  int N, M, F, w, NS, D;
+  T hv1, hv0, eps, beta, beta_ln2;
+  int sigma;
+};
+
+template <typename T>
+__device__ __forceinline__ T bf_hvar(const BandFeat<T>& a, T v) {
+  return v * fma(a.hv1, v, a.hv0);
+}
+
+constexpr int kBfDiags = 32;   // diagonals per workgroup of the builder
+
+// A row of F <= FM features into registers: 16-byte loads where the rows
+// are 16-byte aligned (V16), else one element at a time.
+template <typename T, int FM, bool V16>
+__device__ __forceinline__ void bf_row(const T* p, int F, T (&r)[FM]) {
+  if constexpr (V16) {
+    constexpr int EV = 16 / (int)sizeof(T);
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int q = 0; q < FM / EV; ++q) {
+      if (q * EV < F) {
+        const u4 w = *reinterpret_cast<const u4*>(p + q * EV);
+        if constexpr (sizeof(T) == 4) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) r[q * 4 + e] = __uint_as_float(w[e]);
+        } else {
+          r[q * 2] = __longlong_as_double((long long)(((unsigned long long)w[1] << 32) | w[0]));
+          r[q * 2 + 1] =
+              __longlong_as_double((long long)(((unsigned long long)w[3] << 32) | w[2]));
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < FM; ++k)
+      if (k < F) r[k] = p[k];
+  }
+}
+
+// One lane per slot m, walking kBfDiags diagonals. From one diagonal to the
+// next a slot's cell moves down a row (offset parity 0) or right a column
+// (parity 1), so each step loads one new row of X or of Y, and the lanes of
+// a wavefront load consecutive rows and store consecutive elements.
+// F <= FM; the squared distance sums the features in order with fma.
+template <typename T, bool PEN, int FM, bool V16>
+__global__ void __launch_bounds__(64) band_feat_build(BandFeat<T> a, int b0) {
+  const int m = blockIdx.x * 64 + threadIdx.x;
+  const int b = b0 + (int)blockIdx.z;
+  if (m >= a.NS) return;
+  const int N = a.N, M = a.M, F = a.F, w = a.w, NS = a.NS;
+  const T* X = a.X + (size_t)b * N * F;
+  const T* Y = a.Y + (size_t)b * M * F;
+  const T* VX = a.VX + (size_t)b * N;
+  const T* VY = a.VY + (size_t)b * M;
+  const size_t pb = (size_t)b * a.D * NS;
+  const int d0 = blockIdx.y * kBfDiags;
+  const int d1 = d0 + kBfDiags < a.D ? d0 + kBfDiags : a.D;
+  // the slot's cell at d0 (2i, 2j), and the rows it holds (clamped to the grid)
+  int i2 = d0 + 2 * m + ((d0 + w) & 1) - w;
+  int j2 = 2 * d0 - i2;
+  T x[FM], y[FM];
+#pragma unroll
+  for (int k = 0; k < FM; ++k) x[k] = y[k] = (T)0;
+  auto clampi = [](int v, int n) { return v < 0 ? 0 : (v > n - 1 ? n - 1 : v); };
+  bf_row<T, FM, V16>(X + (size_t)clampi(i2 >> 1, N) * F, F, x);
+  bf_row<T, FM, V16>(Y + (size_t)clampi(j2 >> 1, M) * F, F, y);
+  for (int d = d0; d < d1; ++d) {
+    const int l = 2 * m + ((d + w) & 1);
+    if (d > d0) {
+      // parity 0 at d - 1: the cell moved down a row, else right a column
+      if (((d - 1 + w) & 1) == 0) {
+        i2 += 2;
+        bf_row<T, FM, V16>(X + (size_t)clampi(i2 >> 1, N) * F, F, x);
+      } else {
+        j2 += 2;
+        bf_row<T, FM, V16>(Y + (size_t)clampi(j2 >> 1, M) * F, F, y);
+      }
+    }
+    T c = (T)0, q = (T)0;
+    if (l <= 2 * w && i2 >= 0 && j2 >= 0 && i2 < 2 * N && j2 < 2 * M) {
+      const int i = i2 >> 1, j = j2 >> 1;
+      T sq = (T)0;
+#pragma unroll
+      for (int k = 0; k < FM; ++k) {
+        if (k < F) {
+          const T df = x[k] - y[k];
+          sq = fma(df, df, sq);
+        }
+      }
+      const T var = fmax(bf_hvar(a, VX[i]) + bf_hvar(a, VY[j]), a.eps);
+      c = (sq > (T)0 ? sq : (T)0) * rcp(var);
+      if (PEN) q = a.beta_ln2 * lg2(var);
+    }
+    const size_t o = pb + (size_t)d * NS + m;
+    a.Cb[o] = c;
+    if (PEN) a.Qb[o] = q;
+  }
+}
+
+// Any F (features summed in order with fma, as above): both rows loaded per
+// cell.
+template <typename T, bool PEN>
+__global__ void __launch_bounds__(64) band_feat_build_any(BandFeat<T> a, int b0) {
+  const int m = blockIdx.x * 64 + threadIdx.x;
+  const int b = b0 + (int)blockIdx.z;
+  if (m >= a.NS) return;
+  const int N = a.N, M = a.M, F = a.F, w = a.w, NS = a.NS;
+  const T* X = a.X + (size_t)b * N * F;
+  const T* Y = a.Y + (size_t)b * M * F;
+  const size_t pb = (size_t)b * a.D * NS;
+  const int d0 = blockIdx.y * kBfDiags;
+  const int d1 = d0 + kBfDiags < a.D ? d0 + kBfDiags : a.D;
+  for (int d = d0; d < d1; ++d) {
+    const int l = 2 * m + ((d + w) & 1);
+    const int i2 = d + l - w, j2 = d - l + w;   // 2i and 2j
+    T c = (T)0, q = (T)0;
+    if (l <= 2 * w && i2 >= 0 && j2 >= 0 && i2 < 2 * N && j2 < 2 * M) {
+      const int i = i2 >> 1, j = j2 >> 1;
+      const T* xr = X + (size_t)i * F;
+      const T* yr = Y + (size_t)j * F;
+      T sq = (T)0;
+      for (int k = 0; k < F; ++k) {
+        const T df = xr[k] - yr[k];
+        sq = fma(df, df, sq);
+      }
+      const T var =
+          fmax(bf_hvar(a, a.VX[(size_t)b * N + i]) + bf_hvar(a, a.VY[(size_t)b * M + j]), a.eps);
+      c = (sq > (T)0 ? sq : (T)0) * rcp(var);
+      if (PEN) q = a.beta_ln2 * lg2(var);
+    }
+    const size_t o = pb + (size_t)d * NS + m;
+    a.Cb[o] = c;
+    if (PEN) a.Qb[o] = q;
+  }
+}
+
+// The reducer walks, per lane, the cells of its row (or column) "own" in
+// order: step t in [0, 2w] is the cell with the other index own - w + t, on
+// diagonal 2 own - w + t, in slot (2w - t) / 2 (rows) or t / 2 (columns).
+// The 64 lanes of a workgroup take 64 consecutive rows (columns) and kBgT
+// steps at a time. Their cells lie in a tile of 127 + kBgT diagonals by
+// kBgT / 2 + 1 slots of the band planes, and their other indices in 63 +
+// kBgT consecutive rows of the other side's features: the workgroup loads
+// both into LDS with contiguous reads (a lane's own cells are spread one per
+// diagonal, one cache line each), and the steps read only LDS.
+constexpr int kBgT = 32;
+constexpr int kBgTD = 127 + kBgT;       // diagonals of a tile
+constexpr int kBgTS = kBgT / 2 + 1;     // slots of a tile (odd: LDS rows 2 apart
+                                        // start on different banks)
+constexpr int kBgTR = 63 + kBgT;        // other-side rows of a tile
+constexpr int kBfChunk = 16;            // features per pass
+
+// Workgroups [0, nrb) take rows i, the others columns j: the lane of row i
+// sums its band cells (i, j) for j ascending, the lane of column j its cells
+// (i, j) for i ascending (a fixed order: deterministic). Per cell, as the
+// general sweep's backward: dS = dC / var where S > 0, and
+// dvar = (beta dQ - dC C) / var, half of it to each side's half variance.
+template <typename T, bool PEN>
+__global__ void __launch_bounds__(64) band_feat_grad(BandFeat<T> a, int nrb, int b0) {
+  constexpr int NPL = PEN ? 3 : 2;
+  // feature rows padded by 16 bytes: the 16-byte reads of consecutive rows
+  // by consecutive lanes fall on distinct banks
+  constexpr int YP = kBfChunk + 16 / (int)sizeof(T);
+  __shared__ T tile[NPL][kBgTD * kBgTS];
+  __shared__ __align__(16) T yt[kBgTR * YP];
+  __shared__ T hvt[kBgTR];
+  const int b = b0 + (int)blockIdx.y;
+  const bool rows = (int)blockIdx.x < nrb;
+  const int lane = threadIdx.x;
+  const int o0 = ((int)blockIdx.x - (rows ? 0 : nrb)) * 64;
+  const int own = o0 + lane;
+  const int N = a.N, M = a.M, F = a.F, w = a.w, NS = a.NS, D = a.D;
+  const int n_own = rows ? N : M, n_oth = rows ? M : N;
+  const bool lane_in = own < n_own;
+  const int ownc = lane_in ? own : n_own - 1;
+  const T* xown = (rows ? a.X + (size_t)b * N * F : a.Y + (size_t)b * M * F) + (size_t)ownc * F;
+  const T* oth = rows ? a.Y + (size_t)b * M * F : a.X + (size_t)b * N * F;
+  const T* vown = rows ? a.VX + (size_t)b * N : a.VY + (size_t)b * M;
+  const T* voth = rows ? a.VY + (size_t)b * M : a.VX + (size_t)b * N;
+  const size_t pb = (size_t)b * D * NS;
+  Buf bpl[NPL], bo;
+  bpl[0].init(a.Cb + pb, (long long)D * NS);
+  bpl[1].init(a.dCb + pb, (long long)D * NS);
+  if (PEN) bpl[NPL - 1].init(a.dQb + pb, (long long)D * NS);
+  bo.init(oth, (long long)n_oth * F);
+  constexpr int es = (int)sizeof(T);
+  const T hv = bf_hvar(a, vown[ownc]);
+  T dv = (T)0;
+  for (int f0 = 0; f0 < F; f0 += kBfChunk) {
+    const int fc = F - f0 < kBfChunk ? F - f0 : kBfChunk;
+    T acc[kBfChunk], xo[kBfChunk];
+#pragma unroll
+    for (int k = 0; k < kBfChunk; ++k) {
+      acc[k] = (T)0;
+      xo[k] = k < fc ? xown[f0 + k] : (T)0;
+    }
+    for (int t0 = 0; t0 <= 2 * w; t0 += kBgT) {
+      // the tile: diagonals from 2 o0 - w + t0, slots from ms, other-side
+      // rows from ub
+      const int dbase = 2 * o0 - w + t0;
+      const int ms = rows ? (2 * w - t0 - kBgT + 1) >> 1 : t0 >> 1;
+      const int ub = o0 - w + t0;
+      __syncthreads();
+      // batches of loads in flight before their LDS stores; cells off the
+      // planes (and rows off the grid) load 0 by the buffer's range check
+      constexpr int TE = kBgTD * kBgTS, TB = 11;
+      for (int e0 = 0; e0 < TE; e0 += 64 * TB) {
+        T v[NPL][TB];
+#pragma unroll
+        for (int k = 0; k < TB; ++k) {
+          const int e = e0 + 64 * k + lane;
+          const int dd = e / kBgTS, ss = e - dd * kBgTS;
+          const int d = dbase + dd, m = ms + ss;
+          const int o = (e < TE && d >= 0 && d < D && m >= 0 && m < NS) ? (d * NS + m) * es : kOob;
+#pragma unroll
+          for (int q = 0; q < NPL; ++q) v[q][k] = bpl[q].template ld<T>(o, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < TB; ++k) {
+          const int e = e0 + 64 * k + lane;
+          if (e < TE) {
+#pragma unroll
+            for (int q = 0; q < NPL; ++q) tile[q][e] = v[q][k];
+          }
+        }
+      }
+      constexpr int YE = kBgTR * kBfChunk, YB = (YE + 63) / 64;
+      {
+        T v[YB];
+#pragma unroll
+        for (int k = 0; k < YB; ++k) {
+          const int e = 64 * k + lane;
+          const int rr = e / kBfChunk, kk = e - rr * kBfChunk;
+          const int u = ub + rr;
+          const int o = (e < YE && u >= 0 && u < n_oth && kk < fc) ? (u * F + f0 + kk) * es : kOob;
+          v[k] = bo.ld<T>(o, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < YB; ++k) {
+          const int e = 64 * k + lane;
+          const int rr = e / kBfChunk, kk = e - rr * kBfChunk;
+          if (e < YE) yt[rr * YP + kk] = v[k];
+        }
+      }
+      for (int rr = lane; rr < kBgTR; rr += 64) {
+        const int u = ub + rr;
+        hvt[rr] = (u >= 0 && u < n_oth) ? bf_hvar(a, voth[u]) : (T)0;
+      }
+      __syncthreads();
+      const int t1 = t0 + kBgT < 2 * w + 1 ? t0 + kBgT : 2 * w + 1;
+      for (int t = t0; t < t1; ++t) {
+        const int u = own - w + t;   // the other index
+        if (!lane_in || u < 0 || u >= n_oth) continue;
+        const int m = rows ? (2 * w - t) >> 1 : t >> 1;
+        const int e = (2 * lane + t - t0) * kBgTS + (m - ms);
+        const int rr = lane + t - t0;
+        const T c = tile[0][e], g = tile[1][e];
+        const T var_raw = hv + hvt[rr];
+        const T rv = rcp(fmax(var_raw, a.eps));
+        const T dsq = c > (T)0 ? g * rv : (T)0;
+        if (f0 == 0) {
+          const T h = PEN ? tile[NPL - 1][e] : (T)0;
+          dv += var_raw > a.eps ? (T)0.5 * fma(a.beta, h, -(g * c)) * rv : (T)0;
+        }
+        T yo[kBfChunk];
+        bf_row<T, kBfChunk, true>(yt + rr * YP, kBfChunk, yo);
+#pragma unroll
+        for (int k = 0; k < kBfChunk; ++k) acc[k] = fma(dsq, xo[k] - yo[k], acc[k]);
+      }
+    }
+    if (lane_in) {
+      T* out = (rows ? a.dX + (size_t)b * N * F : a.dY + (size_t)b * M * F) + (size_t)own * F + f0;
+#pragma unroll
+      for (int k = 0; k < kBfChunk; ++k)
+        if (k < fc) out[k] = (T)2 * acc[k];
+    }
+  }
+  T* dvp = rows ? a.dVX : a.dVY;
+  if (dvp && lane_in) {
+    // the gradient of a standard deviation s is 2 s d/dv
+    const T v = vown[own];
+    dvp[(size_t)b * n_own + own] = a.sigma ? (T)2 * v * dv : dv;
+  }
+}
+
+template <typename T>
+BandFeat<T> bf_args(const UdtwArgs<T>& u, const T* X, const T* Y, int F) {
+  BandFeat<T> f = {};
+  f.X = X;
+  f.Y = Y;
+  f.VX = u.VX;
+  f.VY = u.VY;
+  f.N = u.N;
+  f.M = u.M;
+  f.F = F;
+  f.w = (int)u.band;
+  const int S = band_slots(f.w);
+  f.NS = (f.w + 1 + S - 1) / S * S;
+  f.D = u.N + u.M - 1;
+  f.hv1 = u.hv1;
+  f.hv0 = u.hv0;
+  f.eps = u.eps;
+  f.beta = u.beta;
+  f.beta_ln2 = u.beta_ln2;
+  f.sigma = u.sigma;
+  return f;
+}
+
+constexpr int kMaxGridZ = 65535;
+
+template <typename T>
+void bf_build(const BandFeat<T>& f, bool pen, int B, hipStream_t s) {
+  // rows as 16-byte loads: F a multiple of 16 bytes and 16-byte aligned bases
+  const bool v16 = (f.F * sizeof(T)) % 16 == 0 && ((uintptr_t)f.X & 15) == 0 &&
+                   ((uintptr_t)f.Y & 15) == 0;
+  const int fm = f.F <= 16 ? 16 : (f.F <= 32 ? 32 : (f.F <= 64 && sizeof(T) == 4 ? 64 : 0));
+  for (int b0 = 0; b0 < B; b0 += kMaxGridZ) {
+    const int nb = B - b0 < kMaxGridZ ? B - b0 : kMaxGridZ;
+    const dim3 grid((unsigned)((f.NS + 63) / 64), (unsigned)((f.D + kBfDiags - 1) / kBfDiags),
+                    (unsigned)nb);
+#define TW_BFB(PEN_, FM_)                                                                       \
+  do {                                                                                          \
+    if (v16)                                                                                    \
+      hipLaunchKernelGGL((band_feat_build<T, PEN_, FM_, true>), grid, dim3(64), 0, s, f, b0);   \
+    else                                                                                        \
+      hipLaunchKernelGGL((band_feat_build<T, PEN_, FM_, false>), grid, dim3(64), 0, s, f, b0);  \
+  } while (0)
+#define TW_BFB_FM(PEN_)                                                                         \
+  do {                                                                                          \
+    if (fm == 16)                                                                               \
+      TW_BFB(PEN_, 16);                                                                         \
+    else if (fm == 32)                                                                          \
+      TW_BFB(PEN_, 32);                                                                         \
+    else if constexpr (sizeof(T) == 4) {                                                        \
+      if (fm == 64) TW_BFB(PEN_, 64);                                                           \
+    }                                                                                           \
+    if (fm == 0)                                                                                \
+      hipLaunchKernelGGL((band_feat_build_any<T, PEN_>), grid, dim3(64), 0, s, f, b0);          \
+  } while (0)
+    if (pen)
+      TW_BFB_FM(true);
+    else
+      TW_BFB_FM(false);
+#undef TW_BFB_FM
+#undef TW_BFB
+  }
+}
+
+}  // namespace
+
+size_t band_feat_plane_elems(int N, int M, double band) {
+  const int w = (int)band;
+  const int S = band_slots(w);
+  if (S == 0) return 0;
+  return (size_t)(N + M - 1) * (size_t)((w + 1 + S - 1) / S * S);
+}
+
+bool band_feat_path(int N, int M, int F, double band) {
+  if (F < 2 || !band_path(N, M, band)) return false;
+  // a pair's feature rows are addressed with 32-bit byte offsets
+  if ((long long)(N > M ? N : M) * F * 8 >= (1LL << 31)) return false;
+  // the backward keeps three planes (C rebuilt when the forward's are not
+  // given, dC, dQ) in the N M elements per pair of its workspace
+  return 3 * band_feat_plane_elems(N, M, band) <= (size_t)N * M;
+}
+
+template <typename T>
+int band_feat_fwd(const UdtwArgs<T>& u, const T* X, const T* Y, int F, int B, T* ws,
+                  hipStream_t s, const char* what) {
+  if (B == 0) return TW_OK;
+  if (((uintptr_t)ws & 15) != 0)
+    return fail(TW_EINVAL, "%s: the workspace must be 16-byte aligned", what);
+  const bool pen = u.beta != (T)0;
+  BandFeat<T> f = bf_args(u, X, Y, F);
+  const size_t pl = (size_t)B * f.D * f.NS;
+  f.Cb = ws;
+  f.Qb = pen ? ws + pl : nullptr;
+  bf_build<T>(f, pen, B, s);
+  if (int e = check_launch(what)) return e;
+  UdtwArgs<T> a = u;
+  a.C = f.Cb;
+  a.Q = f.Qb;
+  return band_sweep<T>(false, a, B, s, what, true);
+}
+
+template <typename T>
+int band_feat_bwd(const UdtwArgs<T>& u, const T* X, const T* Y, int F, int B, const T* ws_fwd,
+                  T* ws, T* dX, T* dY, hipStream_t s, const char* what) {
+  if (B == 0) return TW_OK;
+  if (((uintptr_t)ws & 15) != 0)
+    return fail(TW_EINVAL, "%s: the workspace must be 16-byte aligned", what);
+  const bool pen = u.beta != (T)0;
+  BandFeat<T> f = bf_args(u, X, Y, F);
+  const size_t pl = (size_t)B * f.D * f.NS;
+  // the cost plane: the forward's, or rebuilt at the workspace's start
+  T* dst = ws;
+  if (ws_fwd) {
+    f.Cb = const_cast<T*>(ws_fwd);
+  } else {
+    f.Cb = ws;
+    f.Qb = nullptr;
+    bf_build<T>(f, false, B, s);
+    if (int e = check_launch(what)) return e;
+    dst = ws + pl;
+  }
+  f.dCb = dst;
+  f.dQb = pen ? dst + pl : nullptr;
+  UdtwArgs<T> a = u;
+  a.dC = dst;
+  a.dQ = pen ? dst + pl : nullptr;
+  if (int e = band_sweep<T>(true, a, B, s, what, true)) return e;
+  f.dX = dX;
+  f.dY = dY;
+  f.dVX = u.dVX;
+  f.dVY = u.dVY;
+  const int nrb = (f.N + 63) / 64, ncb = (f.M + 63) / 64;
+  for (int b0 = 0; b0 < B; b0 += kMaxGridZ) {
+    const int nb = B - b0 < kMaxGridZ ? B - b0 : kMaxGridZ;
+    const dim3 grid((unsigned)(nrb + ncb), (unsigned)nb);
+    if (pen)
+      hipLaunchKernelGGL((band_feat_grad<T, true>), grid, dim3(64), 0, s, f, nrb, b0);
+    else
+      hipLaunchKernelGGL((band_feat_grad<T, false>), grid, dim3(64), 0, s, f, nrb, b0);
+  }
+  return check_launch(what);
+}
+
+template int band_feat_fwd<float>(const UdtwArgs<float>&, const float*, const float*, int, int,
+                                  float*, hipStream_t, const char*);
+template int band_feat_fwd<double>(const UdtwArgs<double>&, const double*, const double*, int,
+                                   int, double*, hipStream_t, const char*);
+template int band_feat_bwd<float>(const UdtwArgs<float>&, const float*, const float*, int, int,
+                                  const float*, float*, float*, float*, hipStream_t, const char*);
+template int band_feat_bwd<double>(const UdtwArgs<double>&, const double*, const double*, int,
+                                   int, const double*, double*, double*, double*, hipStream_t,
+                                   const char*);
 
 }  // namespace tw

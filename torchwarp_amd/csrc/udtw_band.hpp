@@ -13,9 +13,28 @@ int band_mode();
 // 256 slots across, whose band-compressed planes fit in the N M elements of
 // the caller's R / P.
 bool band_path(int N, int M, double band);
-// The banded forward (bwd false) or backward on the cost path; R / P hold the
-// band-compressed planes.
+// The banded forward (bwd false) or backward; R / P hold the band-compressed
+// planes. C / Q (forward) and dC / dQ (backward) are [B, N, M], or with
+// band_io in the band layout [B][N + M - 1][NS]; the penalty is on when Q is
+// given, or with band_io when a.beta != 0.
 template <typename T>
-int band_sweep(bool bwd, const UdtwArgs<T>& a, int B, hipStream_t s, const char* what);
+int band_sweep(bool bwd, const UdtwArgs<T>& a, int B, hipStream_t s, const char* what,
+               bool band_io = false);
+// Elements of one pair's band-layout plane (N + M - 1 diagonals of NS slots).
+size_t band_feat_plane_elems(int N, int M, double band);
+// True when the feature path with F > 1 features runs banded: the banded
+// sweep serves the problem and three band-layout planes fit in N M elements.
+bool band_feat_path(int N, int M, int F, double band);
+// The banded feature path: the band's cost and penalty built from X, Y and
+// the variances of `a` into the band layout at `ws` (the forward's
+// workspace, which the backward reads back), then the banded sweep. The
+// backward rebuilds the cost plane when ws_fwd is null, takes dC / dQ from
+// the banded sweep into `ws` and reduces them to dX, dY and a.dVX / a.dVY.
+template <typename T>
+int band_feat_fwd(const UdtwArgs<T>& a, const T* X, const T* Y, int F, int B, T* ws,
+                  hipStream_t s, const char* what);
+template <typename T>
+int band_feat_bwd(const UdtwArgs<T>& a, const T* X, const T* Y, int F, int B, const T* ws_fwd,
+                  T* ws, T* dX, T* dY, hipStream_t s, const char* what);
 
 }  // namespace tw

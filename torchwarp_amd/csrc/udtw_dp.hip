@@ -252,6 +252,7 @@ static int feat_fwd(const T* X, const T* Y, const T* vx, const T* vy, int B, int
   const size_t need = (size_t)B * N * M * sizeof(T);
   if (!ws || ws_bytes < need)
     return fail(TW_ESIZE, "%s: workspace of %zu bytes needed", what, need);
+  if (band_feat_path(N, M, D, band)) return band_feat_fwd<T>(a, X, Y, D, B, ws, s, what);
   if (int e = sqdist_raw<T>(X, Y, B, N, M, D, ws, s, what)) return e;
   a.C = ws;
   return launch_pen<T, SRC_SQ>(pen, false, a, B, s, what);
@@ -302,6 +303,10 @@ static int feat_bwd(const T* X, const T* Y, const T* vx, const T* vy, const T* R
     a.dY = dY;
     return launch_pen<T, SRC_FEAT1>(pen, true, a, B, s, what);
   }
+  // a band narrower than the grid: the forward left the band's cost and
+  // penalty in its workspace and R / P band-compressed
+  if (band_feat_path(N, M, D, band))
+    return band_feat_bwd<T>(a, X, Y, D, B, ws_fwd, ws, dX, dY, s, what);
   // the raw squared distances: the forward's, or recomputed into the
   // workspace; the sweep writes their adjoint into the workspace (in place
   // when they are there: each cell is read and written by the same thread)
