@@ -746,6 +746,23 @@ __device__ __forceinline__ T bf_hvar(const BandFeat<T>& a, T v) {
 
 constexpr int kBfDiags = 32;   // diagonals per workgroup of the builder
 
+// XCD-aware placement. Workgroup ids go round-robin over the device's kXcds
+// XCDs (MI355X: 8), each with its own L2; pair b's W workgroups take the ids
+// congruent to b modulo kXcds, so a pair's features and band planes are
+// read through one L2. Launch ceil(B / kXcds) kXcds W workgroups; returns
+// false for the ids past the last pair. (On another XCD count the mapping
+// stays exact and only the locality changes.)
+constexpr int kXcds = 8;
+__device__ __forceinline__ bool xcd_place(int W, int B, int& b, int& local) {
+  const int id = (int)blockIdx.x, x = id % kXcds, r = id / kXcds;
+  b = x + kXcds * (r / W);
+  local = r % W;
+  return b < B;
+}
+static unsigned xcd_grid(int W, int B) {
+  return (unsigned)((B + kXcds - 1) / kXcds) * kXcds * (unsigned)W;
+}
+
 // A row of F <= FM features into registers: 16-byte loads where the rows
 // are 16-byte aligned (V16), else one element at a time.
 template <typename T, int FM, bool V16>
@@ -780,9 +797,11 @@ __device__ __forceinline__ void bf_row(const T* p, int F, T (&r)[FM]) {
 // a wavefront load consecutive rows and store consecutive elements.
 // F <= FM; the squared distance sums the features in order with fma.
 template <typename T, bool PEN, int FM, bool V16>
-__global__ void __launch_bounds__(64) band_feat_build(BandFeat<T> a, int b0) {
-  const int m = blockIdx.x * 64 + threadIdx.x;
-  const int b = b0 + (int)blockIdx.z;
+__global__ void __launch_bounds__(64) band_feat_build(BandFeat<T> a, int B, int ngx) {
+  int b, local;
+  if (!xcd_place(ngx * ((a.D + kBfDiags - 1) / kBfDiags), B, b, local)) return;
+  const int gx = local % ngx, gy = local / ngx;
+  const int m = gx * 64 + threadIdx.x;
   if (m >= a.NS) return;
   const int N = a.N, M = a.M, F = a.F, w = a.w, NS = a.NS;
   const T* X = a.X + (size_t)b * N * F;
@@ -790,7 +809,7 @@ __global__ void __launch_bounds__(64) band_feat_build(BandFeat<T> a, int b0) {
   const T* VX = a.VX + (size_t)b * N;
   const T* VY = a.VY + (size_t)b * M;
   const size_t pb = (size_t)b * a.D * NS;
-  const int d0 = blockIdx.y * kBfDiags;
+  const int d0 = gy * kBfDiags;
   const int d1 = d0 + kBfDiags < a.D ? d0 + kBfDiags : a.D;
   // the slot's cell at d0 (2i, 2j), and the rows it holds (clamped to the grid)
   int i2 = d0 + 2 * m + ((d0 + w) & 1) - w;
@@ -837,15 +856,17 @@ __global__ void __launch_bounds__(64) band_feat_build(BandFeat<T> a, int b0) {
 // Any F (features summed in order with fma, as above): both rows loaded per
 // cell.
 template <typename T, bool PEN>
-__global__ void __launch_bounds__(64) band_feat_build_any(BandFeat<T> a, int b0) {
-  const int m = blockIdx.x * 64 + threadIdx.x;
-  const int b = b0 + (int)blockIdx.z;
+__global__ void __launch_bounds__(64) band_feat_build_any(BandFeat<T> a, int B, int ngx) {
+  int b, local;
+  if (!xcd_place(ngx * ((a.D + kBfDiags - 1) / kBfDiags), B, b, local)) return;
+  const int gx = local % ngx, gy = local / ngx;
+  const int m = gx * 64 + threadIdx.x;
   if (m >= a.NS) return;
   const int N = a.N, M = a.M, F = a.F, w = a.w, NS = a.NS;
   const T* X = a.X + (size_t)b * N * F;
   const T* Y = a.Y + (size_t)b * M * F;
   const size_t pb = (size_t)b * a.D * NS;
-  const int d0 = blockIdx.y * kBfDiags;
+  const int d0 = gy * kBfDiags;
   const int d1 = d0 + kBfDiags < a.D ? d0 + kBfDiags : a.D;
   for (int d = d0; d < d1; ++d) {
     const int l = 2 * m + ((d + w) & 1);
@@ -893,7 +914,7 @@ constexpr int kBfChunk = 16;            // features per pass
 // general sweep's backward: dS = dC / var where S > 0, and
 // dvar = (beta dQ - dC C) / var, half of it to each side's half variance.
 template <typename T, bool PEN>
-__global__ void __launch_bounds__(64) band_feat_grad(BandFeat<T> a, int nrb, int b0) {
+__global__ void __launch_bounds__(64) band_feat_grad(BandFeat<T> a, int B, int nrb, int ncb) {
   constexpr int NPL = PEN ? 3 : 2;
   // feature rows padded by 16 bytes: the 16-byte reads of consecutive rows
   // by consecutive lanes fall on distinct banks
@@ -901,10 +922,11 @@ __global__ void __launch_bounds__(64) band_feat_grad(BandFeat<T> a, int nrb, int
   __shared__ T tile[NPL][kBgTD * kBgTS];
   __shared__ __align__(16) T yt[kBgTR * YP];
   __shared__ T hvt[kBgTR];
-  const int b = b0 + (int)blockIdx.y;
-  const bool rows = (int)blockIdx.x < nrb;
+  int b, g;
+  if (!xcd_place(nrb + ncb, B, b, g)) return;
+  const bool rows = g < nrb;
   const int lane = threadIdx.x;
-  const int o0 = ((int)blockIdx.x - (rows ? 0 : nrb)) * 64;
+  const int o0 = (g - (rows ? 0 : nrb)) * 64;
   const int own = o0 + lane;
   const int N = a.N, M = a.M, F = a.F, w = a.w, NS = a.NS, D = a.D;
   const int n_own = rows ? N : M, n_oth = rows ? M : N;
@@ -1043,24 +1065,22 @@ BandFeat<T> bf_args(const UdtwArgs<T>& u, const T* X, const T* Y, int F) {
   return f;
 }
 
-constexpr int kMaxGridZ = 65535;
-
 template <typename T>
 void bf_build(const BandFeat<T>& f, bool pen, int B, hipStream_t s) {
   // rows as 16-byte loads: F a multiple of 16 bytes and 16-byte aligned bases
   const bool v16 = (f.F * sizeof(T)) % 16 == 0 && ((uintptr_t)f.X & 15) == 0 &&
                    ((uintptr_t)f.Y & 15) == 0;
   const int fm = f.F <= 16 ? 16 : (f.F <= 32 ? 32 : (f.F <= 64 && sizeof(T) == 4 ? 64 : 0));
-  for (int b0 = 0; b0 < B; b0 += kMaxGridZ) {
-    const int nb = B - b0 < kMaxGridZ ? B - b0 : kMaxGridZ;
-    const dim3 grid((unsigned)((f.NS + 63) / 64), (unsigned)((f.D + kBfDiags - 1) / kBfDiags),
-                    (unsigned)nb);
-#define TW_BFB(PEN_, FM_)                                                                       \
-  do {                                                                                          \
-    if (v16)                                                                                    \
-      hipLaunchKernelGGL((band_feat_build<T, PEN_, FM_, true>), grid, dim3(64), 0, s, f, b0);   \
-    else                                                                                        \
-      hipLaunchKernelGGL((band_feat_build<T, PEN_, FM_, false>), grid, dim3(64), 0, s, f, b0);  \
+  {
+    const int ngx = (f.NS + 63) / 64;
+    const dim3 grid(xcd_grid(ngx * ((f.D + kBfDiags - 1) / kBfDiags), B));
+#define TW_BFB(PEN_, FM_)                                                                        \
+  do {                                                                                           \
+    if (v16)                                                                                     \
+      hipLaunchKernelGGL((band_feat_build<T, PEN_, FM_, true>), grid, dim3(64), 0, s, f, B, ngx); \
+    else                                                                                         \
+      hipLaunchKernelGGL((band_feat_build<T, PEN_, FM_, false>), grid, dim3(64), 0, s, f, B,      \
+                         ngx);                                                                   \
   } while (0)
 #define TW_BFB_FM(PEN_)                                                                         \
   do {                                                                                          \
@@ -1072,7 +1092,7 @@ void bf_build(const BandFeat<T>& f, bool pen, int B, hipStream_t s) {
       if (fm == 64) TW_BFB(PEN_, 64);                                                           \
     }                                                                                           \
     if (fm == 0)                                                                                \
-      hipLaunchKernelGGL((band_feat_build_any<T, PEN_>), grid, dim3(64), 0, s, f, b0);          \
+      hipLaunchKernelGGL((band_feat_build_any<T, PEN_>), grid, dim3(64), 0, s, f, B, ngx);      \
   } while (0)
     if (pen)
       TW_BFB_FM(true);
@@ -1151,14 +1171,11 @@ int band_feat_bwd(const UdtwArgs<T>& u, const T* X, const T* Y, int F, int B, co
   f.dVX = u.dVX;
   f.dVY = u.dVY;
   const int nrb = (f.N + 63) / 64, ncb = (f.M + 63) / 64;
-  for (int b0 = 0; b0 < B; b0 += kMaxGridZ) {
-    const int nb = B - b0 < kMaxGridZ ? B - b0 : kMaxGridZ;
-    const dim3 grid((unsigned)(nrb + ncb), (unsigned)nb);
-    if (pen)
-      hipLaunchKernelGGL((band_feat_grad<T, true>), grid, dim3(64), 0, s, f, nrb, b0);
-    else
-      hipLaunchKernelGGL((band_feat_grad<T, false>), grid, dim3(64), 0, s, f, nrb, b0);
-  }
+  const dim3 grid(xcd_grid(nrb + ncb, B));
+  if (pen)
+    hipLaunchKernelGGL((band_feat_grad<T, true>), grid, dim3(64), 0, s, f, B, nrb, ncb);
+  else
+    hipLaunchKernelGGL((band_feat_grad<T, false>), grid, dim3(64), 0, s, f, B, nrb, ncb);
   return check_launch(what);
 }
 
