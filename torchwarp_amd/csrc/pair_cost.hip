@@ -18,9 +18,9 @@
 // pair's dS fits in LDS and C <= 64, one fused kernel per pair streams A and B
 // once (threads along D, dB partial sums in registers); otherwise two tiled
 // passes that each read dS once (dA by row blocks, dB by column blocks), on
-// the matrix cores in fp32 (D > 64 in 64-feature slices) and on FMAs in fp64
-// (D > 32 in 32-feature slices); FMA kernels only past 31-bit offsets in
-// fp32.
+// the matrix cores in both precisions (D > 64 in 64-feature slices in fp32,
+// D > 32 in 32-feature slices in fp64); FMA kernels only past 31-bit
+// offsets.
 //
 // The uDTW feature path (sqdist_raw / sqdist_raw_bwd) keeps S and dS by
 // anti-diagonals (plane_index), the layout in which the sweeps' per-diagonal
