@@ -352,7 +352,8 @@ struct alignas(2 * sizeof(T)) FG {
   T f, g;   // F = Rh - Ch and G = Rbar of a cell
 };
 
-// PS: dC in aligned pairs of row neighbours (as jeanie3p_bwd_kernel's PS).
+// PS: dC in aligned pairs of row neighbours: the pair of steps v - 1 and v
+// at step v (half 0: v odd, half 1: v even, v >= 2).
 template <typename T, int SMAX, int UC, int KS, bool PS>
 __global__ void __launch_bounds__(64) jeanie3_bwd_kernel(JeanieArgs<T> a) {
   constexpr int SPR = UC + 1;
@@ -603,10 +604,12 @@ __global__ void __launch_bounds__(64) jeanie3p_fwd_kernel(JeanieArgs<T> a) {
   if (h == hl && lane % 32 == 0) a.out[b] = (m - lg2(s)) * a.inv_k;
 }
 
-// PS: rows of exactly UC columns (U = UC), not transposed, dC's element
-// index even at offset 0: each lane stores its cells in aligned pairs of row
-// neighbours, the pair of steps v - 1 and v at step v (half 0: v odd, half 1:
-// v even, v >= 2), so a store instruction covers half the cache lines.
+// PS: rows of exactly UC columns (U = UC), not transposed, dC 16-byte
+// aligned: each lane keeps its row's dC in registers through the row pair
+// and stores the whole row at its end in 16-byte pieces. The halves' rows
+// 2r and 2r + 1 are adjacent, so a store instruction writes whole cache
+// lines (scattered single or pair stores, each a few bytes of a line, had
+// cost about 30% more HBM writes than dC's bytes).
 template <typename T, int UC, int P, bool PS>
 __global__ void __launch_bounds__(64) jeanie3p_bwd_kernel(JeanieArgs<T> a) {
   constexpr int SPR = UC + 1;
@@ -647,6 +650,7 @@ __global__ void __launch_bounds__(64) jeanie3p_bwd_kernel(JeanieArgs<T> a) {
     }
   }
   FG<T> left = none, pup = none, xch = none, lup = none;
+  T drow[SPR];   // PS: the row pair's dC, by step
   for (int r = 0; r < nrp; ++r) {
     const int vb = g.base(r), vbn = g.base(r + 1);
 #pragma unroll
@@ -675,11 +679,7 @@ __global__ void __launch_bounds__(64) jeanie3p_bwd_kernel(JeanieArgs<T> a) {
       if (has_gr) rbar += rg[v];
       const FG<T> cur = {valid ? rh - ch : -INF, rbar};
       if constexpr (PS) {
-        // step v's cell is column UC - 1 + h - v: the lower address of the
-        // pair it forms with step v - 1 (one column to its right) when that
-        // column is even
-        const bool pair = ((h + v) & 1) && v >= 1 + h;
-        st_pair<T>(bD, (valid && pair) ? g.at(vb, v) : kOob, rbar, left.g);
+        drow[v] = rbar;
       } else {
         bD.st(rbar, valid ? g.at(vb, v) : kOob, 0);
       }
@@ -691,6 +691,41 @@ __global__ void __launch_bounds__(64) jeanie3p_bwd_kernel(JeanieArgs<T> a) {
       rr[v] = bR.ld<T>(o, 0);
       rc[v] = bC.ld<T>(o, 0);
       rg[v] = bG.ld<T>(o, 0);
+    }
+    if constexpr (PS) {
+      // the lane's whole row (column u was step UC - 1 + h - u), from
+      // column 0 up in 16-byte stores: the two halves' rows 2r and 2r + 1
+      // are adjacent, so each store instruction writes whole cache lines
+      constexpr int EV = 16 / (int)sizeof(T);
+      typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+      const int o0 = vb == kOob ? kOob : g.at(vb, UC - 1 + h);
+#pragma unroll
+      for (int q = 0; q < UC / EV; ++q) {
+        T x[EV];
+#pragma unroll
+        for (int e = 0; e < EV; ++e) {
+          // (the empty asm keeps the select a select: folded into an index
+          // h + const, it became a run-time index into drow, one compare
+          // and select per element)
+          const int u = q * EV + e;
+          T x0 = drow[UC - 1 - u], x1 = drow[UC - u];
+          asm volatile("" : "+v"(x0), "+v"(x1));
+          x[e] = h ? x1 : x0;
+        }
+        u4 w;
+        if constexpr (sizeof(T) == 4) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = __float_as_uint(x[e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const unsigned long long z = (unsigned long long)__double_as_longlong(x[e]);
+            w[2 * e] = (unsigned)z;
+            w[2 * e + 1] = (unsigned)(z >> 32);
+          }
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(w, bD.r, o0 == kOob ? kOob : o0 + 16 * q, 0, 0);
+      }
     }
   }
 }
@@ -939,8 +974,8 @@ static void j3_launch_ks(bool bwd, int uc, const JeanieArgs<T>& a, int B, hipStr
 
 template <typename T, int P>
 static void j3p_launch_uc(bool bwd, int uc, const JeanieArgs<T>& a, int B, hipStream_t s) {
-  // pair stores of dC: full rows, not transposed, even element index at dC
-  const bool ps = a.Un == uc && !a.swap && (((size_t)a.dC / sizeof(T)) & 1) == 0;
+  // whole-row stores of dC: full rows, not transposed, dC 16-byte aligned
+  const bool ps = a.Un == uc && !a.swap && ((size_t)a.dC & 15) == 0;
 #define TW_J3P(UC_)                                                                              \
   do {                                                                                           \
     if (bwd && ps)                                                                               \
