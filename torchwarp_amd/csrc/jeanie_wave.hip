@@ -542,7 +542,41 @@ __device__ __forceinline__ int pview(int n, int P, int K1, int K2, bool* ok) {
   return *ok ? n1 * K2 + n2 : 0;
 }
 
-template <typename T, int UC, int P>
+// A lane's row of UC elements at byte offset o (kOob: zeros) into registers,
+// in column order, by 16-byte loads.
+template <typename T, int UC>
+__device__ __forceinline__ void j3_ld_row(const Buf& b, int o, T (&x)[UC]) {
+  constexpr int EV = 16 / (int)sizeof(T);
+  typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int q = 0; q < UC / EV; ++q) {
+    const u4 w = __builtin_amdgcn_raw_buffer_load_b128(b.r, o == kOob ? kOob : o + 16 * q, 0, 0);
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[q * 4 + e] = __uint_as_float(w[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        x[q * 2 + e] =
+            __longlong_as_double((long long)(((unsigned long long)w[2 * e + 1] << 32) | w[2 * e]));
+    }
+  }
+}
+
+// x0 on half 0's lanes, x1 on half 1's, as a select (the empty asm keeps a
+// select of two register-array entries whose indices differ by the half
+// from being folded into a run-time index into the array).
+template <typename T>
+__device__ __forceinline__ T j3_by_half(int h, T x0, T x1) {
+  asm volatile("" : "+v"(x0), "+v"(x1));
+  return h ? x1 : x0;
+}
+
+// RS: rows of exactly UC columns (U = UC), not transposed, R 16-byte
+// aligned: each lane keeps its row of R through the row pair and stores it
+// whole at the end in 16-byte pieces (a quarter of the store instructions;
+// the halves' adjacent rows fill whole cache lines).
+template <typename T, int UC, int P, bool RS>
 __global__ void __launch_bounds__(64) jeanie3p_fwd_kernel(JeanieArgs<T> a) {
   constexpr int SPR = UC + 1;
   const int b = blockIdx.x;
@@ -564,15 +598,29 @@ __global__ void __launch_bounds__(64) jeanie3p_fwd_kernel(JeanieArgs<T> a) {
   T ub[SPR];
 #pragma unroll
   for (int v = 0; v < SPR; ++v) ub[v] = BIG;
-  T cr[SPR];
-  {
+  // cost of the row pair by step: RS loads the next row pair's rows whole
+  // (column u is step u + h) at the start of each row pair, else one
+  // element per step
+  T cr[SPR], cnext[UC];
+  auto c_steps = [&](const T (&row)[UC]) {
+#pragma unroll
+    for (int v = 0; v < SPR; ++v)
+      cr[v] = j3_by_half(h, row[v < UC ? v : 0], row[v > 0 ? v - 1 : 0]);
+  };
+  if constexpr (RS) {
+    const int vb = g.base(0);
+    j3_ld_row<T, UC>(bC, vb == kOob ? kOob : g.at(vb, h), cnext);
+    c_steps(cnext);
+  } else {
     const int vb = g.base(0);
 #pragma unroll
     for (int v = 0; v < SPR; ++v) cr[v] = bC.ld<T>(g.at(vb, v), 0);
   }
   T left = BIG, pup = BIG, xch = BIG, lup = BIG, rlast = BIG;
+  T rrow[SPR];   // RS: the row pair's R, by step
   for (int r = 0; r < nrp; ++r) {
     const int vb = g.base(r), vbn = g.base(r + 1);
+    if constexpr (RS) j3_ld_row<T, UC>(bC, vbn == kOob ? kOob : g.at(vbn, h), cnext);
 #pragma unroll
     for (int v = 0; v < SPR; ++v) {
       const bool valid = vb != kOob && g.col_ok(v);
@@ -586,13 +634,49 @@ __global__ void __launch_bounds__(64) jeanie3p_fwd_kernel(JeanieArgs<T> a) {
       // take lane 32's value into its window, and axis 1 reads lane 31)
       const T s2h = w2 ? (valid ? pwin<1>(rh) : BIG) : rh;
       const T rw = w1 ? pwin<P>(s2h) : s2h;
-      bR.st(rh * a.inv_k, valid ? g.at(vb, v) : kOob, 0);
+      if constexpr (RS)
+        rrow[v] = rh * a.inv_k;
+      else
+        bR.st(rh * a.inv_k, valid ? g.at(vb, v) : kOob, 0);
       if (r == nrp - 1 && v == Un - 1 + hl) rlast = rh;
       left = rw;
       pup = up;
       xch = swap_halves(rw);
       if (v >= 1) ub[v - 1] = xch;
-      cr[v] = bC.ld<T>(g.at(vbn, v), 0);
+      if constexpr (!RS) cr[v] = bC.ld<T>(g.at(vbn, v), 0);
+    }
+    if constexpr (RS) {
+      c_steps(cnext);
+      // column u was step u + h
+      constexpr int EV = 16 / (int)sizeof(T);
+      typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+      const int o0 = vb == kOob ? kOob : g.at(vb, h);
+#pragma unroll
+      for (int q = 0; q < UC / EV; ++q) {
+        T x[EV];
+#pragma unroll
+        for (int e = 0; e < EV; ++e) {
+          // (kept a select: folded into an index h + const it would become a
+          // run-time index into rrow)
+          const int u = q * EV + e;
+          T x0 = rrow[u], x1 = rrow[u + 1];
+          asm volatile("" : "+v"(x0), "+v"(x1));
+          x[e] = h ? x1 : x0;
+        }
+        u4 w;
+        if constexpr (sizeof(T) == 4) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = __float_as_uint(x[e]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const unsigned long long z = (unsigned long long)__double_as_longlong(x[e]);
+            w[2 * e] = (unsigned)z;
+            w[2 * e + 1] = (unsigned)(z >> 32);
+          }
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(w, bR.r, o0 == kOob ? kOob : o0 + 16 * q, 0, 0);
+      }
     }
   }
   T m = vn ? rlast : INF;
@@ -638,8 +722,32 @@ __global__ void __launch_bounds__(64) jeanie3p_bwd_kernel(JeanieArgs<T> a) {
   FG<T> ub[SPR];
 #pragma unroll
   for (int v = 0; v < SPR; ++v) ub[v] = none;
-  T rr[SPR], rc[SPR], rg[SPR];
-  {
+  // R, C (and grad_R) of the row pair by step: PS loads the next row pair's
+  // rows whole (column u is step UC - 1 + h - u) at the start of each row
+  // pair, else one element per step
+  T rr[SPR], rc[SPR], rg[SPR], nR[UC], nC[UC], nG[UC];
+  auto to_steps = [&](const T (&row)[UC], T (&st)[SPR]) {
+#pragma unroll
+    for (int v = 0; v < SPR; ++v)
+      st[v] = j3_by_half(h, row[v < UC ? UC - 1 - v : 0], row[v > 0 ? UC - v : 0]);
+  };
+  auto ld_rows = [&](int vbr) {
+    const int o = vbr == kOob ? kOob : g.at(vbr, UC - 1 + h);
+    j3_ld_row<T, UC>(bR, o, nR);
+    j3_ld_row<T, UC>(bC, o, nC);
+    if (has_gr) j3_ld_row<T, UC>(bG, o, nG);
+  };
+  auto rows_to_steps = [&]() {
+    to_steps(nR, rr);
+    to_steps(nC, rc);
+    if (has_gr) to_steps(nG, rg);
+  };
+  if constexpr (PS) {
+#pragma unroll
+    for (int v = 0; v < SPR; ++v) rg[v] = (T)0;
+    ld_rows(g.base(0));
+    rows_to_steps();
+  } else {
     const int vb = g.base(0);
 #pragma unroll
     for (int v = 0; v < SPR; ++v) {
@@ -653,6 +761,7 @@ __global__ void __launch_bounds__(64) jeanie3p_bwd_kernel(JeanieArgs<T> a) {
   T drow[SPR];   // PS: the row pair's dC, by step
   for (int r = 0; r < nrp; ++r) {
     const int vb = g.base(r), vbn = g.base(r + 1);
+    if constexpr (PS) ld_rows(vbn);
 #pragma unroll
     for (int v = 0; v < SPR; ++v) {
       const bool valid = vb != kOob && g.col_ok(v);
@@ -687,12 +796,15 @@ __global__ void __launch_bounds__(64) jeanie3p_bwd_kernel(JeanieArgs<T> a) {
       pup = up;
       xch = {swap_halves(cur.f), swap_halves(cur.g)};
       if (v >= 1) ub[v - 1] = xch;
-      const int o = g.at(vbn, v);
-      rr[v] = bR.ld<T>(o, 0);
-      rc[v] = bC.ld<T>(o, 0);
-      rg[v] = bG.ld<T>(o, 0);
+      if constexpr (!PS) {
+        const int o = g.at(vbn, v);
+        rr[v] = bR.ld<T>(o, 0);
+        rc[v] = bC.ld<T>(o, 0);
+        rg[v] = bG.ld<T>(o, 0);
+      }
     }
     if constexpr (PS) {
+      rows_to_steps();
       // the lane's whole row (column u was step UC - 1 + h - u), from
       // column 0 up in 16-byte stores: the two halves' rows 2r and 2r + 1
       // are adjacent, so each store instruction writes whole cache lines
@@ -974,16 +1086,21 @@ static void j3_launch_ks(bool bwd, int uc, const JeanieArgs<T>& a, int B, hipStr
 
 template <typename T, int P>
 static void j3p_launch_uc(bool bwd, int uc, const JeanieArgs<T>& a, int B, hipStream_t s) {
-  // whole-row stores of dC: full rows, not transposed, dC 16-byte aligned
-  const bool ps = a.Un == uc && !a.swap && ((size_t)a.dC & 15) == 0;
+  // whole-row loads and stores: full rows, not transposed, 16-byte aligned
+  auto al16 = [](const void* p) { return ((size_t)p & 15) == 0; };
+  const bool rows = a.Un == uc && !a.swap;
+  const bool ps = rows && al16(a.dC) && al16(a.C) && al16(a.R) && al16(a.gR);
+  const bool rs = rows && al16(a.Rw) && al16(a.C);
 #define TW_J3P(UC_)                                                                              \
   do {                                                                                           \
     if (bwd && ps)                                                                               \
       hipLaunchKernelGGL((jeanie3p_bwd_kernel<T, UC_, P, true>), dim3(B), dim3(64), 0, s, a);    \
     else if (bwd)                                                                                \
       hipLaunchKernelGGL((jeanie3p_bwd_kernel<T, UC_, P, false>), dim3(B), dim3(64), 0, s, a);   \
+    else if (rs)                                                                                 \
+      hipLaunchKernelGGL((jeanie3p_fwd_kernel<T, UC_, P, true>), dim3(B), dim3(64), 0, s, a);    \
     else                                                                                         \
-      hipLaunchKernelGGL((jeanie3p_fwd_kernel<T, UC_, P>), dim3(B), dim3(64), 0, s, a);          \
+      hipLaunchKernelGGL((jeanie3p_fwd_kernel<T, UC_, P, false>), dim3(B), dim3(64), 0, s, a);   \
   } while (0)
   switch (uc) {
     case 8: TW_J3P(8); break;
