@@ -563,6 +563,30 @@ __device__ __forceinline__ void j3_ld_row(const Buf& b, int o, T (&x)[UC]) {
   }
 }
 
+// A lane's row of UC elements (column order) stored at byte offset o (kOob:
+// dropped) by 16-byte stores.
+template <typename T, int UC>
+__device__ __forceinline__ void j3_st_row(const Buf& b, int o, const T (&x)[UC]) {
+  constexpr int EV = 16 / (int)sizeof(T);
+  typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int q = 0; q < UC / EV; ++q) {
+    u4 w;
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[e] = __float_as_uint(x[q * 4 + e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const unsigned long long z = (unsigned long long)__double_as_longlong(x[q * 2 + e]);
+        w[2 * e] = (unsigned)z;
+        w[2 * e + 1] = (unsigned)(z >> 32);
+      }
+    }
+    __builtin_amdgcn_raw_buffer_store_b128(w, b.r, o == kOob ? kOob : o + 16 * q, 0, 0);
+  }
+}
+
 // x0 on half 0's lanes, x1 on half 1's, as a select (the empty asm keeps a
 // select of two register-array entries whose indices differ by the half
 // from being folded into a run-time index into the array).
@@ -864,7 +888,8 @@ __device__ __forceinline__ void j3_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <typename T, int UC, int P>
+// RS: whole-row loads of C and stores of R (as jeanie3p_fwd_kernel).
+template <typename T, int UC, int P, bool RS>
 __global__ void __launch_bounds__(64 * kJ3mWaves) jeanie3m_fwd_kernel(JeanieArgs<T> a) {
   constexpr int SPR = UC + 1, L = kJ3mLag;
   extern __shared__ __align__(16) unsigned char j3m_lds[];
@@ -894,8 +919,17 @@ __global__ void __launch_bounds__(64 * kJ3mWaves) jeanie3m_fwd_kernel(JeanieArgs
   bC.init(a.C + (size_t)b * K * plane, (long long)K * plane);
   bR.init(a.Rw + (size_t)b * K * plane, (long long)K * plane);
 
-  T cr[SPR];
-  {
+  T cr[SPR], cnext[UC], rrow[SPR];
+  auto c_steps = [&](const T (&row)[UC]) {
+#pragma unroll
+    for (int v = 0; v < SPR; ++v)
+      cr[v] = j3_by_half(h, row[v < UC ? v : 0], row[v > 0 ? v - 1 : 0]);
+  };
+  if constexpr (RS) {
+    const int vb = g.base(wave);
+    j3_ld_row<T, UC>(bC, vb == kOob ? kOob : g.at(vb, h), cnext);
+    c_steps(cnext);
+  } else {
     const int vb = g.base(wave);
 #pragma unroll
     for (int v = 0; v < SPR; ++v) cr[v] = bC.ld<T>(g.at(vb, v), 0);
@@ -905,6 +939,7 @@ __global__ void __launch_bounds__(64 * kJ3mWaves) jeanie3m_fwd_kernel(JeanieArgs
   for (int k = 0; k < KR; ++k) {
     const int r = wave + k * W;
     const int vb = g.base(r), vbn = g.base(r + W);
+    if constexpr (RS) j3_ld_row<T, UC>(bC, vbn == kOob ? kOob : g.at(vbn, h), cnext);
     T left = BIG, pup = BIG, xch = BIG;
 #pragma unroll
     for (int v = 0; v < SPR; ++v) {
@@ -918,15 +953,25 @@ __global__ void __launch_bounds__(64 * kJ3mWaves) jeanie3m_fwd_kernel(JeanieArgs
       rh = valid ? rh : BIG;
       const T s2h = w2 ? (valid ? pwin<1>(rh) : BIG) : rh;
       const T rw = w1 ? pwin<P>(s2h) : s2h;
-      bR.st(rh * a.inv_k, valid ? g.at(vb, v) : kOob, 0);
+      if constexpr (RS)
+        rrow[v] = rh * a.inv_k;
+      else
+        bR.st(rh * a.inv_k, valid ? g.at(vb, v) : kOob, 0);
       if (r == nrp - 1 && v == Un - 1 + hl) rlast = rh;
       left = rw;
       pup = up;
       xch = swap_halves(rw);
       // half 1: column v - 1 of its row, for the next row pair's half 0
       if (v >= 1) *(h ? out_slot + (v - 1) * 32 : out_slot) = rw;
-      cr[v] = bC.ld<T>(g.at(vbn, v), 0);
+      if constexpr (!RS) cr[v] = bC.ld<T>(g.at(vbn, v), 0);
       j3_barrier();
+    }
+    if constexpr (RS) {
+      c_steps(cnext);
+      T row[UC];   // column u was step u + h
+#pragma unroll
+      for (int u = 0; u < UC; ++u) row[u] = j3_by_half(h, rrow[u], rrow[u + 1]);
+      j3_st_row<T, UC>(bR, vb == kOob ? kOob : g.at(vb, h), row);
     }
     for (int i = SPR; i < PER; ++i) j3_barrier();
   }
@@ -975,8 +1020,29 @@ __global__ void __launch_bounds__(64 * kJ3mWaves) jeanie3m_bwd_kernel(JeanieArgs
   bD.init(a.dC + pb, (long long)K * plane);
 
   const FG<T> none = {-INF, (T)0};
-  T rr[SPR], rc[SPR], rg[SPR];
-  {
+  T rr[SPR], rc[SPR], rg[SPR], nR[UC], nC[UC], nG[UC], drow[SPR];
+  auto to_steps = [&](const T (&row)[UC], T (&st)[SPR]) {
+#pragma unroll
+    for (int v = 0; v < SPR; ++v)
+      st[v] = j3_by_half(h, row[v < UC ? UC - 1 - v : 0], row[v > 0 ? UC - v : 0]);
+  };
+  auto ld_rows = [&](int vbr) {
+    const int o = vbr == kOob ? kOob : g.at(vbr, UC - 1 + h);
+    j3_ld_row<T, UC>(bR, o, nR);
+    j3_ld_row<T, UC>(bC, o, nC);
+    if (has_gr) j3_ld_row<T, UC>(bG, o, nG);
+  };
+  auto rows_to_steps = [&]() {
+    to_steps(nR, rr);
+    to_steps(nC, rc);
+    if (has_gr) to_steps(nG, rg);
+  };
+  if constexpr (PS) {
+#pragma unroll
+    for (int v = 0; v < SPR; ++v) rg[v] = (T)0;
+    ld_rows(g.base(wave));
+    rows_to_steps();
+  } else {
     const int vb = g.base(wave);
 #pragma unroll
     for (int v = 0; v < SPR; ++v) {
@@ -990,6 +1056,7 @@ __global__ void __launch_bounds__(64 * kJ3mWaves) jeanie3m_bwd_kernel(JeanieArgs
   for (int k = 0; k < KR; ++k) {
     const int r = wave + k * W;
     const int vb = g.base(r), vbn = g.base(r + W);
+    if constexpr (PS) ld_rows(vbn);
     FG<T> left = none, pup = none, xch = none;
 #pragma unroll
     for (int v = 0; v < SPR; ++v) {
@@ -1019,21 +1086,28 @@ __global__ void __launch_bounds__(64 * kJ3mWaves) jeanie3m_bwd_kernel(JeanieArgs
       }
       if (has_gr) rbar += rg[v];
       const FG<T> cur = {valid ? rh - ch : -INF, rbar};
-      if constexpr (PS) {
-        const bool pair = ((h + v) & 1) && v >= 1 + h;
-        st_pair<T>(bD, (valid && pair) ? g.at(vb, v) : kOob, rbar, left.g);
-      } else {
+      if constexpr (PS)
+        drow[v] = rbar;
+      else
         bD.st(rbar, valid ? g.at(vb, v) : kOob, 0);
-      }
       left = cur;
       pup = up;
       xch = {swap_halves(cur.f), swap_halves(cur.g)};
       if (v >= 1) *(h ? out_slot + (v - 1) * 32 : out_slot) = cur;
-      const int o = g.at(vbn, v);
-      rr[v] = bR.ld<T>(o, 0);
-      rc[v] = bC.ld<T>(o, 0);
-      rg[v] = bG.ld<T>(o, 0);
+      if constexpr (!PS) {
+        const int o = g.at(vbn, v);
+        rr[v] = bR.ld<T>(o, 0);
+        rc[v] = bC.ld<T>(o, 0);
+        rg[v] = bG.ld<T>(o, 0);
+      }
       j3_barrier();
+    }
+    if constexpr (PS) {
+      rows_to_steps();
+      T row[UC];   // column u was step UC - 1 + h - u
+#pragma unroll
+      for (int u = 0; u < UC; ++u) row[u] = j3_by_half(h, drow[UC - 1 - u], drow[UC - u]);
+      j3_st_row<T, UC>(bD, vb == kOob ? kOob : g.at(vb, UC - 1 + h), row);
     }
     for (int i = SPR; i < PER; ++i) j3_barrier();
   }
@@ -1115,7 +1189,13 @@ static void j3p_launch_uc(bool bwd, int uc, const JeanieArgs<T>& a, int B, hipSt
 // Several wavefronts per pair (W of them, 2 <= W <= kJ3mWaves).
 template <typename T, int P>
 static void j3m_launch_uc(bool bwd, int uc, int W, const JeanieArgs<T>& a, int B, hipStream_t s) {
-  const bool ps = a.Un == uc && !a.swap && (((size_t)a.dC / sizeof(T)) & 1) == 0;
+  // whole-row loads and stores: full rows, not transposed, 16-byte aligned,
+  // of at most 64 bytes (longer rows' registers would spill under the
+  // 512-thread launch bound)
+  auto al16 = [](const void* p) { return ((size_t)p & 15) == 0; };
+  const bool rows = a.Un == uc && !a.swap && uc * sizeof(T) <= 64;
+  const bool ps = rows && al16(a.dC) && al16(a.C) && al16(a.R) && al16(a.gR);
+  const bool rs = rows && al16(a.Rw) && al16(a.C);
   const size_t elem = bwd ? 2 * sizeof(T) : sizeof(T);
   const size_t lds = ((size_t)W * (uc + 1) * 32 + 64) * elem;
   const dim3 grid((unsigned)B), block((unsigned)(64 * W));
@@ -1125,8 +1205,10 @@ static void j3m_launch_uc(bool bwd, int uc, int W, const JeanieArgs<T>& a, int B
       hipLaunchKernelGGL((jeanie3m_bwd_kernel<T, UC_, P, true>), grid, block, lds, s, a);        \
     else if (bwd)                                                                                \
       hipLaunchKernelGGL((jeanie3m_bwd_kernel<T, UC_, P, false>), grid, block, lds, s, a);       \
+    else if (rs)                                                                                 \
+      hipLaunchKernelGGL((jeanie3m_fwd_kernel<T, UC_, P, true>), grid, block, lds, s, a);        \
     else                                                                                         \
-      hipLaunchKernelGGL((jeanie3m_fwd_kernel<T, UC_, P>), grid, block, lds, s, a);              \
+      hipLaunchKernelGGL((jeanie3m_fwd_kernel<T, UC_, P, false>), grid, block, lds, s, a);       \
   } while (0)
   switch (uc) {
     case 8: TW_J3M(8); break;
