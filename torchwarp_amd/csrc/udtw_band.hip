@@ -655,9 +655,9 @@ int band_run(bool bwd, bool bio, const UdtwArgs<T>& u, int B, hipStream_t s, con
   a.k = u.k;
   a.inv_k = u.inv_k;
   a.inv_gamma = u.inv_gamma;
-  // the penalty: given as Q on the cost path; from features (band_io) it is
-  // built when beta != 0, and the backward reads no Q
-  const bool pen = bio ? u.beta != (T)0 : u.Q != nullptr;
+  // the penalty: on when Q is given; from features (band_io, beta != 0) the
+  // backward has no Q to give
+  const bool pen = u.Q != nullptr || (bio && u.beta != (T)0);
 #define TW_BAND(S_)                                                             \
   (bio ? (pen ? band_launch<T, RT, S_, true, true>(bwd, a, B, s)                \
               : band_launch<T, RT, S_, false, true>(bwd, a, B, s))              \
@@ -1188,5 +1188,106 @@ template int band_feat_bwd<float>(const UdtwArgs<float>&, const float*, const fl
 template int band_feat_bwd<double>(const UdtwArgs<double>&, const double*, const double*, int,
                                    int, const double*, double*, double*, double*, hipStream_t,
                                    const char*);
+
+// ------------------------------------------------ cost path, band layout
+//
+// The cost path's forward reads C and Q at the band's cells of the [B, N, M]
+// planes, one cache line per lane and slot at every step of its chain. When
+// the caller's R buffer has room behind the band planes, a gather pass first
+// copies the band's cells of C and Q into the band layout there (an LDS
+// transpose of 32-row tiles, XCD-aware placement), and the sweep then reads
+// them coalesced (as from features).
+
+namespace {
+
+constexpr int kGatherRows = 32;   // rows of the [N, M] planes per gather workgroup
+
+// One workgroup per 32 rows of a pair: each plane's band segments of those
+// rows (columns i - w .. i + w) are read row by row into LDS, contiguous in
+// memory, and written out diagonal by diagonal, where the tile's cells of a
+// diagonal are consecutive slots. Slots no row of the grid fills are left
+// as they are: the sweep masks the cells off the grid.
+template <typename T, bool PEN>
+__global__ void __launch_bounds__(256) band_gather(const T* __restrict__ C,
+                                                   const T* __restrict__ Q, T* Cb, T* Qb, int B,
+                                                   int N, int M, int w, int NS, int D, int ntile) {
+  extern __shared__ __align__(16) unsigned char gather_lds[];
+  T* tile = reinterpret_cast<T*>(gather_lds);
+  int b, tl;
+  if (!xcd_place(ntile, B, b, tl)) return;
+  const int i0 = tl * kGatherRows;
+  const int RW = 2 * w + 1;   // row-local columns: c = j - (i - w)
+  const int rows = N - i0 < kGatherRows ? N - i0 : kGatherRows;
+  const size_t nm = (size_t)N * M;
+  for (int q = 0; q < (PEN ? 2 : 1); ++q) {
+    const T* src = (q ? Q : C) + b * nm;
+    T* dst = (q ? Qb : Cb) + (size_t)b * D * NS;
+    if (q) __syncthreads();
+    // (a thread's column c of all 32 rows loaded before any is stored, so
+    // the rows' loads are in flight together; 8 diagonals x 32 rows per
+    // pass of the threads on the way out)
+    for (int c = threadIdx.x; c < RW; c += blockDim.x) {
+      T v[kGatherRows];
+#pragma unroll
+      for (int r = 0; r < kGatherRows; ++r) {
+        const int i = i0 + r, j = i - w + c;
+        v[r] = (r < rows && j >= 0 && j < M) ? src[(size_t)i * M + j] : (T)0;
+      }
+#pragma unroll
+      for (int r = 0; r < kGatherRows; ++r)
+        if (r < rows) tile[r * RW + c] = v[r];
+    }
+    __syncthreads();
+    // diagonals 2 i0 - w .. 2 (i0 + rows - 1) + w, rows r of each
+    const int dlo = 2 * i0 - w, nd = 2 * (rows - 1) + RW;
+    const int r = threadIdx.x & (kGatherRows - 1);
+    for (int dd = threadIdx.x / kGatherRows; dd < nd; dd += blockDim.x / kGatherRows) {
+      const int d = dlo + dd, i = i0 + r, j = d - i;
+      const int l = i - j + w;
+      if (r >= rows || d < 0 || d >= D || j < 0 || j >= M || l < 0 || l > 2 * w) continue;
+      dst[(size_t)d * NS + (l >> 1)] = tile[r * RW + (j - i + w)];
+    }
+  }
+}
+
+}  // namespace
+
+template <typename T>
+int band_cost_fwd(const UdtwArgs<T>& u, int B, hipStream_t s, const char* what) {
+  if (B == 0) return TW_OK;
+  const int w = (int)u.band;
+  const int S = band_slots(w);
+  const int NS = (w + 1 + S - 1) / S * S, D = u.N + u.M - 1;
+  const bool pen = u.Q != nullptr;
+  // R's elements per pair hold the band planes (2 D NS of RT) first; the
+  // gathered C, Q go behind all pairs' planes
+  const size_t rs = u.rd ? 8 : sizeof(T);
+  const size_t planes = (size_t)B * 2 * D * NS * rs;
+  const size_t room = (size_t)B * u.N * u.M * rs;
+  const size_t need = (size_t)B * D * NS * sizeof(T) * (pen ? 2 : 1);
+  char* tail = reinterpret_cast<char*>(u.R) + planes;
+  if (planes + need > room || ((uintptr_t)tail & 15) != 0 ||
+      (long long)u.N * u.M * (long long)rs >= (1LL << 31))
+    return band_sweep<T>(false, u, B, s, what);   // (which also reports the size limit)
+  T* Cb = reinterpret_cast<T*>(tail);
+  T* Qb = pen ? Cb + (size_t)B * D * NS : nullptr;
+  const int ntile = (u.N + kGatherRows - 1) / kGatherRows;
+  const dim3 grid(xcd_grid(ntile, B));
+  const size_t lds = (size_t)kGatherRows * (2 * w + 1) * sizeof(T);
+  if (pen)
+    hipLaunchKernelGGL((band_gather<T, true>), grid, dim3(256), lds, s, u.C, u.Q, Cb, Qb, B, u.N,
+                       u.M, w, NS, D, ntile);
+  else
+    hipLaunchKernelGGL((band_gather<T, false>), grid, dim3(256), lds, s, u.C, u.Q, Cb, Qb, B,
+                       u.N, u.M, w, NS, D, ntile);
+  if (int e = check_launch(what)) return e;
+  UdtwArgs<T> a = u;
+  a.C = Cb;
+  a.Q = Qb;
+  return band_sweep<T>(false, a, B, s, what, true);
+}
+
+template int band_cost_fwd<float>(const UdtwArgs<float>&, int, hipStream_t, const char*);
+template int band_cost_fwd<double>(const UdtwArgs<double>&, int, hipStream_t, const char*);
 
 }  // namespace tw

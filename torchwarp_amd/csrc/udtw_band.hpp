@@ -20,6 +20,11 @@ bool band_path(int N, int M, double band);
 template <typename T>
 int band_sweep(bool bwd, const UdtwArgs<T>& a, int B, hipStream_t s, const char* what,
                bool band_io = false);
+// The banded forward on the cost path: the band's cells of C and Q first
+// gathered into the band layout behind the band planes in R's buffer when
+// it has the room (else the sweep reads the [B, N, M] planes).
+template <typename T>
+int band_cost_fwd(const UdtwArgs<T>& a, int B, hipStream_t s, const char* what);
 // Elements of one pair's band-layout plane (N + M - 1 diagonals of NS slots).
 size_t band_feat_plane_elems(int N, int M, double band);
 // True when the feature path with F > 1 features runs banded: the banded

@@ -96,7 +96,7 @@ static int cost_fwd(const T* C, const T* Q, int B, int N, int M, double gamma, d
   a.M = M;
   a.rd = allow_rd && carry_double<T>(N, M, gamma);
   set_hyper(a, gamma, 0.0, 1.0, band);
-  if (band_path(N, M, band)) return band_sweep<T>(false, a, B, s, what);
+  if (band_path(N, M, band)) return band_cost_fwd<T>(a, B, s, what);
   return launch_pen<T, SRC_COST>(Q != nullptr, false, a, B, s, what);
 }
 
