@@ -207,7 +207,7 @@ def _hip_call_times(name, inputs, iters):
         R = C.new_empty(B, _hip.carry_cols(N, M, 1.0, C.dtype))
         P = C.new_empty(B, N * M)
         o1, o2 = C.new_empty(B), C.new_empty(B)
-        nws = _hip.udtw_cost_workspace_elems(B, N, M, C.dtype)
+        nws = _hip.udtw_cost_workspace_elems(B, N, M, C.dtype, band)
         ws = C.new_empty(nws) if nws else None
         wsb = 0 if ws is None else nws * 4
         g = torch.full((B,), 1.0 / B, device=dev)

@@ -100,6 +100,13 @@ size_t tw_udtw_carry_bytes(int B, int N, int M, double gamma, int elem_size);
  * through it. There is no length limit beyond the 2 GiB of one pair's N*M
  * planes (32-bit offsets within a pair). */
 size_t tw_udtw_cost_workspace_bytes(int B, int N, int M, int elem_size);
+/* The workspace with which a banded backward (a Sakoe-Chiba band narrower
+ * than the grid) first keeps d_cost / d_pen in the band layout of its sweep
+ * and then scatters them into [B,N,M], instead of writing them there one
+ * cache line per lane (no counterpart in the reference, which only masks);
+ * at least tw_udtw_cost_workspace_bytes. A smaller workspace keeps the
+ * direct writes. */
+size_t tw_udtw_cost_band_workspace_bytes(int B, int N, int M, double bandwidth, int elem_size);
 int tw_udtw_cost_fwd_f32(const float* cost, const float* pen, int B, int N, int M, float gamma,
                          float bandwidth, float* R, float* P, float* out_dist, float* out_pen,
                          hipStream_t stream);

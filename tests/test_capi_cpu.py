@@ -25,7 +25,7 @@ def _declared():
 def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(_hip.LIB_PATH))
     names = _declared()
-    assert len(names) == 44
+    assert len(names) == 45
     for name in names:
         assert hasattr(lib, name), name
     assert lib.tw_version() == 1
@@ -34,7 +34,8 @@ def test_library_exports_every_declared_symbol():
 def test_binding_covers_every_entry_point():
     bound = {"tw_version", "tw_last_error", "tw_udtw_feat_workspace_bytes", "tw_async_status",
              "tw_test_set_wait", "tw_udtw_carry_bytes",
-             "tw_udtw_cost_workspace_bytes", "tw_test_set_mw", "tw_fvm_workspace_bytes",
+             "tw_udtw_cost_workspace_bytes", "tw_udtw_cost_band_workspace_bytes",
+             "tw_test_set_mw", "tw_fvm_workspace_bytes",
              "tw_noalloc_scratch_bytes", "tw_udtw_tangent_workspace_bytes"}
     for base in _hip.SIGNATURES:
         bound |= {base + "_f32", base + "_f64"}

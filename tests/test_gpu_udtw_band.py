@@ -82,14 +82,18 @@ def test_banded_sweep_matches_oracle(case):
     assert float(c.grad[:, out].abs().max()) == 0.0
 
 
-@pytest.mark.parametrize("band", [20.0, 0.0], ids=["banded", "general"])
+@pytest.mark.parametrize("band,band_ws", [(20.0, False), (20.0, True), (0.0, False)],
+                         ids=["banded", "banded-scatter", "general"])
 @pytest.mark.parametrize("dtype", [torch.float32, f64], ids=["f32", "f64"])
-def test_backward_with_gradients_at_odd_offsets(dtype, band):
+def test_backward_with_gradients_at_odd_offsets(dtype, band, band_ws):
     """The cost-path backwards (the banded sweep, and the general sweep
     without a band) store the gradients in aligned pairs of row neighbours,
-    chosen by the parity of each cell's address. Here d_cost starts at an odd
-    element offset and d_pen at an even one, with N M odd (the pairs' parity
-    alternates between batch entries), through the C ABI; against the oracle."""
+    chosen by the parity of each cell's address; with the band workspace the
+    banded sweep keeps them in its band layout and a scatter pass writes them
+    (the sweep's other workgroups zeroing the rest). Here d_cost starts at an
+    odd element offset and d_pen at an even one, with N M odd (the pairs'
+    parity alternates between batch entries), through the C ABI; against the
+    oracle, and nothing outside the planes is written."""
     from torchwarp_amd import _hip
     B, N, M, gamma = 3, 151, 163, 0.5
     g = torch.Generator().manual_seed(7)
@@ -112,7 +116,9 @@ def test_backward_with_gradients_at_odd_offsets(dtype, band):
     buf_c = torch.full((n + 3,), 7.0, device="cuda", dtype=dtype)
     buf_q = torch.full((n + 4,), 7.0, device="cuda", dtype=dtype)
     dc, dq = buf_c[1:1 + n], buf_q[2:2 + n]
-    ws_n = _hip.udtw_cost_workspace_elems(B, N, M, dtype)
+    ws_n = _hip.udtw_cost_workspace_elems(B, N, M, dtype, band if band_ws else 0.0)
+    if band_ws:
+        assert ws_n > _hip.udtw_cost_workspace_elems(B, N, M, dtype)
     ws = torch.empty(max(ws_n, 1), device="cuda", dtype=dtype)
     _hip.call("tw_udtw_cost_bwd", dtype, c, q, R, P, dev(wr), dev(wp), B, N, M, gamma, band, 1,
               dc, dq, ws if ws_n else None, ws_n * ws.element_size())

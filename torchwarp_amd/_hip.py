@@ -75,6 +75,9 @@ def _load():
     lib.tw_fvm_workspace_bytes.argtypes = [ctypes.c_int] * 5
     lib.tw_udtw_cost_workspace_bytes.restype = ctypes.c_size_t
     lib.tw_udtw_cost_workspace_bytes.argtypes = [ctypes.c_int] * 4
+    lib.tw_udtw_cost_band_workspace_bytes.restype = ctypes.c_size_t
+    lib.tw_udtw_cost_band_workspace_bytes.argtypes = [ctypes.c_int] * 3 + [ctypes.c_double,
+                                                                           ctypes.c_int]
     lib.tw_udtw_tangent_workspace_bytes.restype = ctypes.c_size_t
     lib.tw_udtw_tangent_workspace_bytes.argtypes = [ctypes.c_int] * 5
     lib.tw_udtw_carry_bytes.restype = ctypes.c_size_t
@@ -212,11 +215,15 @@ def udtw_workspace_elems(B, N, M, D, dtype=torch.float32):
     return -(-library().tw_udtw_feat_workspace_bytes(B, N, M, D, es) // es)
 
 
-def udtw_cost_workspace_elems(B, N, M, dtype=torch.float32):
-    """Elements (of ``dtype``) of the workspace a cost-path uDTW backward needs
-    (the hand-off records between workgroups of long sequences; 0 otherwise)."""
+def udtw_cost_workspace_elems(B, N, M, dtype=torch.float32, bandwidth=0.0):
+    """Elements (of ``dtype``) of the workspace a cost-path uDTW backward uses:
+    the hand-off records between workgroups of long sequences, and with a band
+    narrower than the grid the gradients in the banded sweep's layout (0 when
+    neither applies)."""
     es = 4 if dtype == torch.float32 else 8
-    return -(-library().tw_udtw_cost_workspace_bytes(B, N, M, es) // es)
+    lib = library()
+    n = lib.tw_udtw_cost_band_workspace_bytes(B, N, M, float(bandwidth or 0.0), es)
+    return -(-n // es)
 
 
 def udtw_tangent_workspace_elems(B, N, M, has_penalty, dtype=torch.float32):

@@ -65,7 +65,8 @@ struct BandArgs {
   T *out_r, *out_p;    // forward [B]
   const T *gr, *gp;    // backward [B], element stride gstride
   int gstride;
-  T *dC, *dQ;          // backward [B,N,M] (inside the band)
+  T *dC, *dQ;          // backward [B,N,M] (inside the band), or the band layout
+  T *zC, *zQ;          // backward: the [B,N,M] planes zeroed outside the band
   int N, M, w, NS, D;
   int B, nzero;        // pairs; backward: workgroups past B zero outside the band
   T k, inv_k, inv_gamma;
@@ -394,8 +395,7 @@ __device__ void band_zero_rows(T* dC, T* dQ, int B, int N, int M, int w, int z, 
 template <typename T, typename RT, int S, bool PEN, int WP, bool BIO>
 __global__ void __launch_bounds__(64) udtw_band_bwd(BandArgs<T, RT> a) {
   if ((int)blockIdx.x >= a.B) {
-    if constexpr (!BIO)
-      band_zero_rows<T>(a.dC, a.dQ, a.B, a.N, a.M, a.w, (int)blockIdx.x - a.B, a.nzero);
+    band_zero_rows<T>(a.zC, a.zQ, a.B, a.N, a.M, a.w, (int)blockIdx.x - a.B, a.nzero);
     return;
   }
   // prefetch distance (steps, even): as deep as the memory counter (63
@@ -627,7 +627,8 @@ int band_launch(bool bwd, const BandArgs<T, RT>& a, int B, hipStream_t s) {
 }
 
 template <typename T, typename RT>
-int band_run(bool bwd, bool bio, const UdtwArgs<T>& u, int B, hipStream_t s, const char* what) {
+int band_run(bool bwd, bool bio, const UdtwArgs<T>& u, int B, hipStream_t s, const char* what,
+             T* zero_c, T* zero_q) {
   BandArgs<T, RT> a;
   a.C = u.C;
   a.Q = u.Q;
@@ -640,6 +641,10 @@ int band_run(bool bwd, bool bio, const UdtwArgs<T>& u, int B, hipStream_t s, con
   a.gstride = u.gstride;
   a.dC = u.dC;
   a.dQ = u.dQ;
+  // the zeros outside the band: into dC / dQ themselves, or with the band
+  // layout into the given [B, N, M] planes (none given: no zeroing)
+  a.zC = bio ? zero_c : u.dC;
+  a.zQ = bio ? zero_q : u.dQ;
   a.N = u.N;
   a.M = u.M;
   a.w = (int)u.band;
@@ -651,7 +656,7 @@ int band_run(bool bwd, bool bio, const UdtwArgs<T>& u, int B, hipStream_t s, con
   a.B = B;
   // zeroing workgroups: at least 4 rows each, at most 1024
   const long long rows = (long long)B * u.N;
-  a.nzero = bwd && !bio ? (int)((rows + 3) / 4 < 1024 ? (rows + 3) / 4 : 1024) : 0;
+  a.nzero = bwd && a.zC ? (int)((rows + 3) / 4 < 1024 ? (rows + 3) / 4 : 1024) : 0;
   a.k = u.k;
   a.inv_k = u.inv_k;
   a.inv_gamma = u.inv_gamma;
@@ -701,7 +706,7 @@ bool band_path(int N, int M, double band) {
 
 template <typename T>
 int band_sweep(bool bwd, const UdtwArgs<T>& a, int B, hipStream_t s, const char* what,
-               bool band_io) {
+               bool band_io, T* zero_c, T* zero_q) {
   if (B == 0) return TW_OK;
   // planes are addressed with 32-bit byte offsets within a pair
   const long long rbytes = a.rd ? 8 : (long long)sizeof(T);
@@ -709,13 +714,15 @@ int band_sweep(bool bwd, const UdtwArgs<T>& a, int B, hipStream_t s, const char*
     return fail(TW_ESIZE, "%s: one pair's N*M matrix (%d x %d) must stay below 2 GiB", what,
                 a.N, a.M);
   }
-  if (sizeof(T) == 4 && a.rd) return band_run<T, double>(bwd, band_io, a, B, s, what);
-  return band_run<T, T>(bwd, band_io, a, B, s, what);
+  if (sizeof(T) == 4 && a.rd)
+    return band_run<T, double>(bwd, band_io, a, B, s, what, zero_c, zero_q);
+  return band_run<T, T>(bwd, band_io, a, B, s, what, zero_c, zero_q);
 }
 
-template int band_sweep<float>(bool, const UdtwArgs<float>&, int, hipStream_t, const char*, bool);
+template int band_sweep<float>(bool, const UdtwArgs<float>&, int, hipStream_t, const char*, bool,
+                               float*, float*);
 template int band_sweep<double>(bool, const UdtwArgs<double>&, int, hipStream_t, const char*,
-                                bool);
+                                bool, double*, double*);
 
 // ----------------------------------------------------- from features (F > 1)
 //
@@ -1289,5 +1296,103 @@ int band_cost_fwd(const UdtwArgs<T>& u, int B, hipStream_t s, const char* what) 
 
 template int band_cost_fwd<float>(const UdtwArgs<float>&, int, hipStream_t, const char*);
 template int band_cost_fwd<double>(const UdtwArgs<double>&, int, hipStream_t, const char*);
+
+namespace {
+
+// The reverse of band_gather: the band-layout dC (and dQ) of 32 rows read
+// diagonal by diagonal into LDS (a diagonal's cells of the tile are
+// consecutive slots; eight diagonals' loads of a lane in flight together),
+// then written into the [N, M] planes row by row, each row's band segment
+// contiguous. Cells outside the band are not written (zeroed elsewhere).
+template <typename T, bool PEN>
+__global__ void __launch_bounds__(256) band_scatter(const T* __restrict__ dCb,
+                                                    const T* __restrict__ dQb, T* dC, T* dQ,
+                                                    int B, int N, int M, int w, int NS, int D,
+                                                    int ntile) {
+  extern __shared__ __align__(16) unsigned char scatter_lds[];
+  T* tile = reinterpret_cast<T*>(scatter_lds);
+  int b, tl;
+  if (!xcd_place(ntile, B, b, tl)) return;
+  const int i0 = tl * kGatherRows;
+  const int RW = 2 * w + 1;
+  const int rows = N - i0 < kGatherRows ? N - i0 : kGatherRows;
+  const size_t nm = (size_t)N * M;
+  const int dlo = 2 * i0 - w, nd = 2 * (rows - 1) + RW;
+  const int r = threadIdx.x & (kGatherRows - 1);
+  constexpr int DPASS = 256 / kGatherRows, UN = 8;
+  for (int q = 0; q < (PEN ? 2 : 1); ++q) {
+    const T* src = (q ? dQb : dCb) + (size_t)b * D * NS;
+    T* dst = (q ? dQ : dC) + b * nm;
+    if (q) __syncthreads();
+    for (int dd0 = threadIdx.x / kGatherRows; dd0 < nd; dd0 += DPASS * UN) {
+      T v[UN];
+      int e[UN];
+#pragma unroll
+      for (int k = 0; k < UN; ++k) {
+        const int dd = dd0 + DPASS * k;
+        const int d = dlo + dd, i = i0 + r, j = d - i;
+        const int l = i - j + w;
+        const bool in = dd < nd && r < rows && d >= 0 && d < D && j >= 0 && j < M && l >= 0 &&
+                        l <= 2 * w;
+        v[k] = in ? src[(size_t)d * NS + (l >> 1)] : (T)0;
+        e[k] = in ? r * RW + (j - i + w) : -1;
+      }
+#pragma unroll
+      for (int k = 0; k < UN; ++k)
+        if (e[k] >= 0) tile[e[k]] = v[k];
+    }
+    __syncthreads();
+    for (int rr = 0; rr < rows; ++rr) {
+      const int i = i0 + rr;
+      for (int c = threadIdx.x; c < RW; c += blockDim.x) {
+        const int j = i - w + c;
+        if (j >= 0 && j < M) dst[(size_t)i * M + j] = tile[rr * RW + c];
+      }
+    }
+  }
+}
+
+}  // namespace
+
+size_t band_cost_workspace_elems(int B, int N, int M, double band) {
+  if (B <= 0 || N <= 0 || M <= 0 || N > M || !band_path(N, M, band)) return 0;
+  // dC and dQ in the band layout, and 16 bytes of slack for the alignment
+  return (size_t)2 * B * band_feat_plane_elems(N, M, band) + 2;
+}
+
+template <typename T>
+int band_cost_bwd(const UdtwArgs<T>& u, int B, hipStream_t s, const char* what, T* ws,
+                  size_t ws_bytes) {
+  if (B == 0) return TW_OK;
+  const size_t pl = (size_t)B * band_feat_plane_elems(u.N, u.M, u.band);
+  const bool pen = u.Q != nullptr;
+  // the band layout's planes, 16-byte aligned within the workspace
+  T* base = ws ? reinterpret_cast<T*>(((uintptr_t)ws + 15) & ~(uintptr_t)15) : nullptr;
+  const size_t skip = ws ? (size_t)(reinterpret_cast<char*>(base) - reinterpret_cast<char*>(ws)) : 0;
+  if (!ws || ws_bytes < skip + (pen ? 2 : 1) * pl * sizeof(T))
+    return band_sweep<T>(true, u, B, s, what);   // gradients straight into [B, N, M]
+  UdtwArgs<T> a = u;
+  a.dC = base;
+  a.dQ = pen ? base + pl : nullptr;
+  if (int e = band_sweep<T>(true, a, B, s, what, true, u.dC, pen ? u.dQ : nullptr)) return e;
+  const int w = (int)u.band;
+  const int S = band_slots(w);
+  const int NS = (w + 1 + S - 1) / S * S, D = u.N + u.M - 1;
+  const int ntile = (u.N + kGatherRows - 1) / kGatherRows;
+  const dim3 grid(xcd_grid(ntile, B));
+  const size_t lds = (size_t)kGatherRows * (2 * w + 1) * sizeof(T);
+  if (pen)
+    hipLaunchKernelGGL((band_scatter<T, true>), grid, dim3(256), lds, s, a.dC, a.dQ, u.dC, u.dQ,
+                       B, u.N, u.M, w, NS, D, ntile);
+  else
+    hipLaunchKernelGGL((band_scatter<T, false>), grid, dim3(256), lds, s, a.dC, a.dQ, u.dC,
+                       u.dQ, B, u.N, u.M, w, NS, D, ntile);
+  return check_launch(what);
+}
+
+template int band_cost_bwd<float>(const UdtwArgs<float>&, int, hipStream_t, const char*, float*,
+                                  size_t);
+template int band_cost_bwd<double>(const UdtwArgs<double>&, int, hipStream_t, const char*,
+                                   double*, size_t);
 
 }  // namespace tw

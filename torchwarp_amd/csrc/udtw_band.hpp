@@ -17,9 +17,19 @@ bool band_path(int N, int M, double band);
 // planes. C / Q (forward) and dC / dQ (backward) are [B, N, M], or with
 // band_io in the band layout [B][N + M - 1][NS]; the penalty is on when Q is
 // given, or with band_io when a.beta != 0.
+// With band_io, the backward zeroes zero_c / zero_q ([B, N, M]) outside the
+// band alongside the sweep (null: no zeroing).
 template <typename T>
 int band_sweep(bool bwd, const UdtwArgs<T>& a, int B, hipStream_t s, const char* what,
-               bool band_io = false);
+               bool band_io = false, T* zero_c = nullptr, T* zero_q = nullptr);
+// The banded backward on the cost path: with a workspace of
+// band_cost_workspace_elems elements, dC / dQ first in the band layout there
+// (the sweep's other workgroups zeroing a.dC / a.dQ outside the band), then
+// scattered into a.dC / a.dQ; with less, straight into a.dC / a.dQ.
+size_t band_cost_workspace_elems(int B, int N, int M, double band);
+template <typename T>
+int band_cost_bwd(const UdtwArgs<T>& a, int B, hipStream_t s, const char* what, T* ws,
+                  size_t ws_bytes);
 // The banded forward on the cost path: the band's cells of C and Q first
 // gathered into the band layout behind the band planes in R's buffer when
 // it has the room (else the sweep reads the [B, N, M] planes).

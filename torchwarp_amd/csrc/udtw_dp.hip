@@ -129,7 +129,7 @@ static int cost_bwd(const T* C, const T* Q, const T* R, const T* P, const T* gr,
     return fail(TW_ESIZE, "%s: workspace of %zu bytes needed", what, need);
   a.hand = need ? reinterpret_cast<unsigned long long*>(ws) : nullptr;
   set_hyper(a, gamma, 0.0, 1.0, band);
-  if (band_path(N, M, band)) return band_sweep<T>(true, a, B, s, what);
+  if (band_path(N, M, band)) return band_cost_bwd<T>(a, B, s, what, ws, ws_bytes);
   return launch_pen<T, SRC_COST>(pen, true, a, B, s, what);
 }
 
@@ -341,6 +341,14 @@ size_t tw_udtw_cost_workspace_bytes(int B, int N, int M, int elem_size) {
   if (B <= 0 || N <= 0 || M <= 0 || (elem_size != 4 && elem_size != 8)) return 0;
   const int n = N < M ? N : M, m = N < M ? M : N;
   return elem_size == 4 ? mw_hand_bytes<float>(B, n, m) : mw_hand_bytes<double>(B, n, m);
+}
+
+size_t tw_udtw_cost_band_workspace_bytes(int B, int N, int M, double bandwidth, int elem_size) {
+  if (B <= 0 || N <= 0 || M <= 0 || (elem_size != 4 && elem_size != 8)) return 0;
+  const int n = N < M ? N : M, m = N < M ? M : N;
+  const size_t band = band_cost_workspace_elems(B, n, m, bandwidth) * (size_t)elem_size;
+  const size_t hand = tw_udtw_cost_workspace_bytes(B, N, M, elem_size);
+  return band > hand ? band : hand;
 }
 
 int tw_udtw_feat_fwd_f32(const float* X, const float* Y, const float* vx, const float* vy, int B,

@@ -69,7 +69,7 @@ def dp_backward(cost: Tensor, penalty: Tensor, R: Tensor, P: Tensor, grad_r: Ten
     d_pen = torch.empty_like(c) if pen else c.new_empty(0)
     grads, gs = _hip.per_pair(*((grad_r.to(c.dtype), grad_p.to(c.dtype)) if pen
                                 else (grad_r.to(c.dtype),)))
-    nws = _hip.udtw_cost_workspace_elems(B, N, M, c.dtype)
+    nws = _hip.udtw_cost_workspace_elems(B, N, M, c.dtype, bandwidth)
     ws = c.new_empty(nws) if nws else c.new_empty(0)
     _hip.call("tw_udtw_cost_bwd", c.dtype, c, q, R, P, grads[0], grads[1] if pen else None,
               B, N, M, gamma, bandwidth, gs, d_cost, d_pen, *_ws_args(ws))
