@@ -902,18 +902,25 @@ __global__ void __launch_bounds__(64) band_feat_build_any(BandFeat<T> a, int B, 
 // The reducer walks, per lane, the cells of its row (or column) "own" in
 // order: step t in [0, 2w] is the cell with the other index own - w + t, on
 // diagonal 2 own - w + t, in slot (2w - t) / 2 (rows) or t / 2 (columns).
-// The 64 lanes of a workgroup take 64 consecutive rows (columns) and kBgT
-// steps at a time. Their cells lie in a tile of 127 + kBgT diagonals by
-// kBgT / 2 + 1 slots of the band planes, and their other indices in 63 +
-// kBgT consecutive rows of the other side's features: the workgroup loads
-// both into LDS with contiguous reads (a lane's own cells are spread one per
-// diagonal, one cache line each), and the steps read only LDS.
-constexpr int kBgT = 32;
-constexpr int kBgTD = 127 + kBgT;       // diagonals of a tile
-constexpr int kBgTS = kBgT / 2 + 1;     // slots of a tile (odd: LDS rows 2 apart
-                                        // start on different banks)
-constexpr int kBgTR = 63 + kBgT;        // other-side rows of a tile
-constexpr int kBfChunk = 16;            // features per pass
+// The 64 lanes of a workgroup take 64 consecutive rows (columns) and kT
+// steps at a time, those whose cells lie in one aligned block of kT / 2
+// slots (64 bytes). Their cells lie in a tile of 127 + kT diagonals by those
+// slots of the band planes, and their other indices in 63 + kT consecutive
+// rows of the other side's features: the workgroup loads both into LDS with
+// contiguous reads, one 64-byte sector per diagonal and plane (a lane's own
+// cells are spread one per diagonal, one cache line each), and the steps
+// read only LDS. A whole tile's loads are held in registers, which float
+// affords at 32 steps per tile and double at 16.
+template <typename T>
+struct BgTile {
+  static constexpr int kT = sizeof(T) == 4 ? 32 : 16;
+  static constexpr int kTD = 127 + kT;   // diagonals of a tile
+  static constexpr int kSL = kT / 2;     // slots of a tile: 64 bytes
+  static constexpr int kTS = kSL + 1;    // LDS row of a diagonal (odd: rows 2
+                                         // apart start on different banks)
+  static constexpr int kTR = 63 + kT;    // other-side rows of a tile
+};
+constexpr int kBfChunk = 16;             // features per pass
 
 // Workgroups [0, nrb) take rows i, the others columns j: the lane of row i
 // sums its band cells (i, j) for j ascending, the lane of column j its cells
@@ -923,6 +930,8 @@ constexpr int kBfChunk = 16;            // features per pass
 template <typename T, bool PEN>
 __global__ void __launch_bounds__(64) band_feat_grad(BandFeat<T> a, int B, int nrb, int ncb) {
   constexpr int NPL = PEN ? 3 : 2;
+  constexpr int kBgT = BgTile<T>::kT, kBgTD = BgTile<T>::kTD, kSL = BgTile<T>::kSL,
+                kBgTS = BgTile<T>::kTS, kBgTR = BgTile<T>::kTR;
   // feature rows padded by 16 bytes: the 16-byte reads of consecutive rows
   // by consecutive lanes fall on distinct banks
   constexpr int YP = kBfChunk + 16 / (int)sizeof(T);
@@ -949,6 +958,8 @@ __global__ void __launch_bounds__(64) band_feat_grad(BandFeat<T> a, int B, int n
   bpl[1].init(a.dCb + pb, (long long)D * NS);
   if (PEN) bpl[NPL - 1].init(a.dQb + pb, (long long)D * NS);
   bo.init(oth, (long long)n_oth * F);
+  Buf bv;
+  bv.init(voth, (long long)n_oth);
   constexpr int es = (int)sizeof(T);
   const T hv = bf_hvar(a, vown[ownc]);
   T dv = (T)0;
@@ -960,66 +971,84 @@ __global__ void __launch_bounds__(64) band_feat_grad(BandFeat<T> a, int B, int n
       acc[k] = (T)0;
       xo[k] = k < fc ? xown[f0 + k] : (T)0;
     }
-    for (int t0 = 0; t0 <= 2 * w; t0 += kBgT) {
-      // the tile: diagonals from 2 o0 - w + t0, slots from ms, other-side
-      // rows from ub
-      const int dbase = 2 * o0 - w + t0;
-      const int ms = rows ? (2 * w - t0 - kBgT + 1) >> 1 : t0 >> 1;
-      const int ub = o0 - w + t0;
-      __syncthreads();
-      // batches of loads in flight before their LDS stores; cells off the
-      // planes (and rows off the grid) load 0 by the buffer's range check
-      constexpr int TE = kBgTD * kBgTS, TB = 11;
-      for (int e0 = 0; e0 < TE; e0 += 64 * TB) {
-        T v[NPL][TB];
+    // Tile kt holds the steps whose cells lie in slots [kSL kt, kSL kt + kSL)
+    // (one 64-byte sector of each diagonal): steps from tA = 2w - kT kt -
+    // kT + 1 (rows) or kT kt (columns), on diagonals from 2 o0 - w + tA,
+    // with other-side rows from o0 - w + tA. Rows take the tiles in
+    // descending kt, columns ascending, so a lane adds its cells in
+    // ascending step order. All of a tile's global loads are issued at once,
+    // a tile ahead, into registers (the LDS allows one wavefront per SIMD,
+    // so registers are free), and are in flight while the tile before is
+    // reduced; cells off the planes and rows off the grid load 0 by the
+    // buffer's range check.
+    constexpr int TE = kBgTD * kSL, TB = (TE + 63) / 64;
+    constexpr int YE = kBgTR * kBfChunk, YB = (YE + 63) / 64;
+    constexpr int HB = (kBgTR + 63) / 64;
+    const int KT = 2 * w / kBgT + 1;
+    auto tile_kt = [&](int i) { return rows ? KT - 1 - i : i; };
+    auto tile_t0 = [&](int kt) { return rows ? 2 * w - kBgT * kt - kBgT + 1 : kBgT * kt; };
+    T v[NPL][TB], vy[YB], vh[HB];
+    auto fetch = [&](int kt) {
+      const int tA = tile_t0(kt);
+      const int dbase = 2 * o0 - w + tA, ms = kSL * kt, ub = o0 - w + tA;
 #pragma unroll
-        for (int k = 0; k < TB; ++k) {
-          const int e = e0 + 64 * k + lane;
-          const int dd = e / kBgTS, ss = e - dd * kBgTS;
-          const int d = dbase + dd, m = ms + ss;
-          const int o = (e < TE && d >= 0 && d < D && m >= 0 && m < NS) ? (d * NS + m) * es : kOob;
+      for (int k = 0; k < TB; ++k) {
+        const int e = 64 * k + lane;
+        const int dd = e / kSL, ss = e % kSL;
+        const int d = dbase + dd, m = ms + ss;
+        const int o = (e < TE && d >= 0 && d < D && m < NS) ? (d * NS + m) * es : kOob;
 #pragma unroll
-          for (int q = 0; q < NPL; ++q) v[q][k] = bpl[q].template ld<T>(o, 0);
-        }
-#pragma unroll
-        for (int k = 0; k < TB; ++k) {
-          const int e = e0 + 64 * k + lane;
-          if (e < TE) {
-#pragma unroll
-            for (int q = 0; q < NPL; ++q) tile[q][e] = v[q][k];
-          }
-        }
+        for (int q = 0; q < NPL; ++q) v[q][k] = bpl[q].template ld<T>(o, 0);
       }
-      constexpr int YE = kBgTR * kBfChunk, YB = (YE + 63) / 64;
-      {
-        T v[YB];
 #pragma unroll
-        for (int k = 0; k < YB; ++k) {
-          const int e = 64 * k + lane;
-          const int rr = e / kBfChunk, kk = e - rr * kBfChunk;
-          const int u = ub + rr;
-          const int o = (e < YE && u >= 0 && u < n_oth && kk < fc) ? (u * F + f0 + kk) * es : kOob;
-          v[k] = bo.ld<T>(o, 0);
-        }
-#pragma unroll
-        for (int k = 0; k < YB; ++k) {
-          const int e = 64 * k + lane;
-          const int rr = e / kBfChunk, kk = e - rr * kBfChunk;
-          if (e < YE) yt[rr * YP + kk] = v[k];
-        }
-      }
-      for (int rr = lane; rr < kBgTR; rr += 64) {
+      for (int k = 0; k < YB; ++k) {
+        const int e = 64 * k + lane;
+        const int rr = e / kBfChunk, kk = e - rr * kBfChunk;
         const int u = ub + rr;
-        hvt[rr] = (u >= 0 && u < n_oth) ? bf_hvar(a, voth[u]) : (T)0;
+        const int o = (e < YE && u >= 0 && u < n_oth && kk < fc) ? (u * F + f0 + kk) * es : kOob;
+        vy[k] = bo.template ld<T>(o, 0);
+      }
+#pragma unroll
+      for (int k = 0; k < HB; ++k) {
+        const int u = ub + 64 * k + lane;
+        vh[k] = bv.template ld<T>(u >= 0 && u < n_oth ? u * es : kOob, 0);
+      }
+    };
+    fetch(tile_kt(0));
+    for (int i = 0; i < KT; ++i) {
+      const int kt = tile_kt(i), tA = tile_t0(kt), ms = kSL * kt;
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < TB; ++k) {
+        const int e = 64 * k + lane;
+        if (e < TE) {
+          const int dd = e / kSL, ss = e % kSL;
+#pragma unroll
+          for (int q = 0; q < NPL; ++q) tile[q][dd * kBgTS + ss] = v[q][k];
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < YB; ++k) {
+        const int e = 64 * k + lane;
+        const int rr = e / kBfChunk, kk = e - rr * kBfChunk;
+        if (e < YE) yt[rr * YP + kk] = vy[k];
+      }
+#pragma unroll
+      for (int k = 0; k < HB; ++k) {
+        const int rr = 64 * k + lane;
+        // a row off the grid loaded 0, whose half variance is 0
+        if (rr < kBgTR) hvt[rr] = bf_hvar(a, vh[k]);
       }
       __syncthreads();
-      const int t1 = t0 + kBgT < 2 * w + 1 ? t0 + kBgT : 2 * w + 1;
+      if (i + 1 < KT) fetch(tile_kt(i + 1));
+      const int t0 = tA > 0 ? tA : 0;
+      const int t1 = tA + kBgT < 2 * w + 1 ? tA + kBgT : 2 * w + 1;
       for (int t = t0; t < t1; ++t) {
         const int u = own - w + t;   // the other index
         if (!lane_in || u < 0 || u >= n_oth) continue;
         const int m = rows ? (2 * w - t) >> 1 : t >> 1;
-        const int e = (2 * lane + t - t0) * kBgTS + (m - ms);
-        const int rr = lane + t - t0;
+        const int e = (2 * lane + t - tA) * kBgTS + (m - ms);
+        const int rr = lane + t - tA;
         const T c = tile[0][e], g = tile[1][e];
         const T var_raw = hv + hvt[rr];
         const T rv = rcp(fmax(var_raw, a.eps));
