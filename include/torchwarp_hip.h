@@ -184,6 +184,15 @@ int tw_udtw_cost_tangent_f64(const double* cost, const double* pen, const double
  * workspace. The backward writes their adjoint into workspace; fwd_workspace
  * is only read, unless it is workspace itself. */
 size_t tw_udtw_feat_workspace_bytes(int B, int N, int M, int D, int elem_size);
+
+/* Workspace of tw_udtw_feat_fwd / tw_udtw_feat_bwd for a given bandwidth (the
+ * band of udtw_cuda.cu:126-130). A Sakoe-Chiba band narrower than the grid
+ * runs the banded feature path, D = 1 included: cost, penalty, R and P in a
+ * band layout built in a workspace of B*N*M elements, which both directions
+ * then need; otherwise this equals tw_udtw_feat_workspace_bytes. No
+ * counterpart in the reference, whose band only masks cells. */
+size_t tw_udtw_feat_band_workspace_bytes(int B, int N, int M, int D, double bandwidth,
+                                         int elem_size);
 int tw_udtw_feat_fwd_f32(const float* X, const float* Y, const float* vx, const float* vy, int B,
                          int N, int M, int D, float gamma, float beta, float eps,
                          float bandwidth, int sigma, float* R, float* P, float* out_dist,

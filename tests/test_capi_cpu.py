@@ -25,7 +25,7 @@ def _declared():
 def test_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(str(_hip.LIB_PATH))
     names = _declared()
-    assert len(names) == 45
+    assert len(names) == 46
     for name in names:
         assert hasattr(lib, name), name
     assert lib.tw_version() == 1
@@ -35,6 +35,7 @@ def test_binding_covers_every_entry_point():
     bound = {"tw_version", "tw_last_error", "tw_udtw_feat_workspace_bytes", "tw_async_status",
              "tw_test_set_wait", "tw_udtw_carry_bytes",
              "tw_udtw_cost_workspace_bytes", "tw_udtw_cost_band_workspace_bytes",
+             "tw_udtw_feat_band_workspace_bytes",
              "tw_test_set_mw", "tw_fvm_workspace_bytes",
              "tw_noalloc_scratch_bytes", "tw_udtw_tangent_workspace_bytes"}
     for base in _hip.SIGNATURES:
@@ -62,6 +63,14 @@ def test_workspace_query_is_host_only():
     assert lib.tw_udtw_feat_workspace_bytes(2, 2000, 2100, 5, 4) == \
         2 * 2000 * 2100 * 4 + 2 * 7 * 2100 * 4 * 8
     assert lib.tw_udtw_feat_workspace_bytes(1, 600, 700, 1, 8) == 2 * 700 * 6 * 8
+    # a band narrower than the grid: the banded feature path's plane of
+    # B*N*M elements, D = 1 included; otherwise the unbanded size
+    assert lib.tw_udtw_feat_band_workspace_bytes(2, 300, 310, 1, 30.0, 4) == 2 * 300 * 310 * 4
+    assert lib.tw_udtw_feat_band_workspace_bytes(2, 300, 310, 5, 30.0, 8) == 2 * 300 * 310 * 8
+    plain = lib.tw_udtw_feat_workspace_bytes(2, 300, 310, 1, 4)
+    assert lib.tw_udtw_feat_band_workspace_bytes(2, 300, 310, 1, 0.0, 4) == plain
+    assert lib.tw_udtw_feat_band_workspace_bytes(2, 300, 310, 1, 299.0, 4) == plain
+    assert lib.tw_udtw_feat_band_workspace_bytes(1, 2000, 2100, 1, 0.0, 4) == 7 * 2100 * 4 * 8
     assert lib.tw_udtw_cost_workspace_bytes(3, 1025, 1100, 4) == 3 * 4 * 1100 * 4 * 8
     assert lib.tw_udtw_cost_workspace_bytes(3, 1100, 1025, 4) == 3 * 4 * 1100 * 4 * 8
     # up to 1024 rows, pairs split over workgroups only when the batch has

@@ -1,4 +1,4 @@
-"""The banded feature path (csrc/udtw_band.hip) for sequences of F > 1 features.
+"""The banded feature path (csrc/udtw_band.hip) for sequences of F >= 1 features.
 
 With a Sakoe-Chiba band narrower than the grid, the cost max(S, 0) / var and
 the penalty beta ln var are built only for the band's cells, in the band
@@ -8,7 +8,8 @@ and the standard deviations are summed from it row by row and column by
 column. Against the float64 oracle (its dense masked DP, udtw_cuda.cu:126-130):
 distances, penalties and all four gradients, over one, two and four band
 slots per lane, F below, at and above the reducer's 16-feature pass, F not a
-multiple of 4, fractional widths, the swapped orientation, soft-DTW (no
+multiple of 4, a single feature (D = 1, whose unbanded path builds the cost
+in the sweep), fractional widths, the swapped orientation, soft-DTW (no
 penalty) and float32 with R in double. Through the C ABI: the backward with
 the forward's planes and with NULL (rebuilt) gives the same bits, and
 variance inputs (sigma = 0) agree with standard deviations.
@@ -41,6 +42,10 @@ CASES = [  # (B, N, M, F, gamma, beta, bandwidth, dtype)
     (1, 1000, 1000, 8, 1.0, 1.0, 130.0, f64),    # four slots per lane
     (2, 300, 310, 16, 0.5, 1.0, 30.0, f32),
     (1, 1024, 1024, 16, 0.1, 1.0, 102.0, f32),   # long and sharp: R in double
+    (2, 300, 310, 1, 0.5, 1.0, 30.0, f64),       # D = 1
+    (2, 290, 270, 1, 1.0, 1.0, 40.0, f64),       # D = 1, swapped
+    (2, 250, 260, 1, 0.5, 0.0, 25.5, f64),       # D = 1 soft-DTW
+    (1, 1024, 1024, 1, 0.1, 1.0, 102.0, f32),    # D = 1, R in double
 ]
 
 
@@ -80,7 +85,7 @@ def _feat_fwd(X, Y, vx, vy, gamma, beta, band, sigma):
     R = X.new_empty(B, _hip.carry_cols(N, M, gamma, dtype))
     P = X.new_empty(B, N * M)
     o1, o2 = X.new_empty(B), X.new_empty(B)
-    nws = _hip.udtw_workspace_elems(B, N, M, F, dtype)
+    nws = _hip.udtw_workspace_elems(B, N, M, F, dtype, band)
     ws = X.new_empty(nws)
     _hip.call("tw_udtw_feat_fwd", dtype, X, Y, vx, vy, B, N, M, F, gamma, beta, 1e-8, band,
               sigma, R, P, o1, o2, ws, nws * X.element_size())
@@ -91,7 +96,7 @@ def _feat_bwd(X, Y, vx, vy, R, P, gr, gp, gamma, beta, band, sigma, fwd_ws):
     dtype = X.dtype
     B, N, F = X.shape
     M = Y.shape[1]
-    nws = _hip.udtw_workspace_elems(B, N, M, F, dtype)
+    nws = _hip.udtw_workspace_elems(B, N, M, F, dtype, band)
     grads = [torch.empty_like(t) for t in (X, Y, vx, vy)]
     _hip.call("tw_udtw_feat_bwd", dtype, X, Y, vx, vy, R, P, gr, gp, B, N, M, F, gamma, beta,
               1e-8, band, sigma, 1, *grads, fwd_ws, X.new_empty(nws), nws * X.element_size())
@@ -134,3 +139,28 @@ def test_variance_inputs_match_standard_deviations():
     assert _maxnorm(gv[0], gs[0]) < 1e-12 and _maxnorm(gv[1], gs[1]) < 1e-12
     assert _maxnorm(gv[2], gs[2] / (2 * sx)) < 1e-12
     assert _maxnorm(gv[3], gs[3] / (2 * sy)) < 1e-12
+
+
+def test_single_feature_band_takes_the_banded_path():
+    """D = 1 with a band narrower than the grid runs banded: the forward needs
+    the B*N*M-element plane (and the size query reports it), and its
+    distances and gradients equal, to rounding, those of a D = 2 input whose
+    second feature is zero (the builder and the reducer at F = 1 and 2)."""
+    B, N, M, gamma, beta, band = 2, 300, 310, 0.5, 1.0, 30.0
+    X, Y, sx, sy, gr, gp = _inputs(B, N, M, 1, f64, 14)
+    assert _hip.udtw_workspace_elems(B, N, M, 1, f64, band) == B * N * M
+    assert _hip.udtw_feat_plane(B, N, M, 1, f64, band)
+    assert not _hip.udtw_feat_plane(B, N, M, 1, f64, 0.0)
+    R = X.new_empty(B, _hip.carry_cols(N, M, gamma, f64))
+    with pytest.raises(RuntimeError, match="workspace"):
+        _hip.call("tw_udtw_feat_fwd", f64, X, Y, sx, sy, B, N, M, 1, gamma, beta, 1e-8, band, 1,
+                  R, X.new_empty(B, N * M), X.new_empty(B), X.new_empty(B), None, 0)
+    X2, Y2 = (torch.cat([t, torch.zeros_like(t)], dim=2) for t in (X, Y))
+    outs = []
+    for x, y in ((X, Y), (X2, Y2)):
+        R, P, o1, o2, ws = _feat_fwd(x, y, sx, sy, gamma, beta, band, 1)
+        g = _feat_bwd(x, y, sx, sy, R, P, gr, gp, gamma, beta, band, 1, ws)
+        outs.append([o1, o2, g[0][..., :1], g[1][..., :1], g[2], g[3]])
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert _maxnorm(a, b) < 1e-12

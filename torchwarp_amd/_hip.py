@@ -75,6 +75,9 @@ def _load():
     lib.tw_fvm_workspace_bytes.argtypes = [ctypes.c_int] * 5
     lib.tw_udtw_cost_workspace_bytes.restype = ctypes.c_size_t
     lib.tw_udtw_cost_workspace_bytes.argtypes = [ctypes.c_int] * 4
+    lib.tw_udtw_feat_band_workspace_bytes.restype = ctypes.c_size_t
+    lib.tw_udtw_feat_band_workspace_bytes.argtypes = [ctypes.c_int] * 4 + [ctypes.c_double,
+                                                                           ctypes.c_int]
     lib.tw_udtw_cost_band_workspace_bytes.restype = ctypes.c_size_t
     lib.tw_udtw_cost_band_workspace_bytes.argtypes = [ctypes.c_int] * 3 + [ctypes.c_double,
                                                                            ctypes.c_int]
@@ -207,12 +210,22 @@ def check_udtw_plane(N, M, gamma, dtype):
             "downsample the sequences.".format(N, M, nbytes))
 
 
-def udtw_workspace_elems(B, N, M, D, dtype=torch.float32):
+def udtw_workspace_elems(B, N, M, D, dtype=torch.float32, bandwidth=0.0):
     """Elements (of ``dtype``) of the workspace a feature-path uDTW backward
     needs: the squared-distance plane for D > 1 and, for sequences longer
-    than one workgroup holds, the hand-off records between workgroups."""
+    than one workgroup holds, the hand-off records between workgroups; with
+    a band narrower than the grid, the B*N*M-element plane of the banded
+    feature path (D = 1 included)."""
     es = 4 if dtype == torch.float32 else 8
-    return -(-library().tw_udtw_feat_workspace_bytes(B, N, M, D, es) // es)
+    n = library().tw_udtw_feat_band_workspace_bytes(B, N, M, D, float(bandwidth or 0.0), es)
+    return -(-n // es)
+
+
+def udtw_feat_plane(B, N, M, D, dtype=torch.float32, bandwidth=0.0):
+    """Whether a feature-path uDTW forward needs its B*N*M-element workspace
+    plane: the squared distances (D > 1), or the banded path's cost and
+    penalty (D = 1 with a band narrower than the grid)."""
+    return D > 1 or udtw_workspace_elems(B, N, M, D, dtype, bandwidth) >= B * N * M
 
 
 def udtw_cost_workspace_elems(B, N, M, dtype=torch.float32, bandwidth=0.0):

@@ -79,7 +79,7 @@ def udtw_fused(X: Tensor, Y: Tensor, vx: Tensor, vy: Tensor, gamma: float, beta:
 def _(X, Y, vx, vy, gamma, beta, eps, bandwidth, backend):
     B, N, M = X.shape[0], X.shape[1], Y.shape[1]
     P = X.new_empty(B, N * M) if beta != 0.0 else X.new_empty(0)
-    S = X.new_empty(B, N * M) if X.shape[2] > 1 else X.new_empty(0)
+    S = _uops._feat_ws(X, N, M, bandwidth)
     R = X.new_empty(B, _hip.carry_cols(N, M, gamma, X.dtype))
     return X.new_empty(B), X.new_empty(B), R, P, S, X.new_empty(0), X.new_empty(0)
 

@@ -1149,7 +1149,7 @@ size_t band_feat_plane_elems(int N, int M, double band) {
 }
 
 bool band_feat_path(int N, int M, int F, double band) {
-  if (F < 2 || !band_path(N, M, band)) return false;
+  if (F < 1 || !band_path(N, M, band)) return false;
   // a pair's feature rows are addressed with 32-bit byte offsets
   if ((long long)(N > M ? N : M) * F * 8 >= (1LL << 31)) return false;
   // the backward keeps three planes (C rebuilt when the forward's are not

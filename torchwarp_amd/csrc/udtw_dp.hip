@@ -244,7 +244,10 @@ static int feat_fwd(const T* X, const T* Y, const T* vx, const T* vy, int B, int
   a.rd = carry_double<T>(N, M, gamma);
   set_hyper(a, gamma, beta, eps, band);
   set_sigma(a, sigma);
-  if (D == 1) {
+  // a band narrower than the grid: cost, penalty, R and P in the band layout
+  // (D = 1 too), built in the workspace
+  const bool banded = band_feat_path(N, M, D, band);
+  if (D == 1 && !banded) {
     a.X = X;
     a.Y = Y;
     return launch_pen<T, SRC_FEAT1>(pen, false, a, B, s, what);
@@ -252,7 +255,7 @@ static int feat_fwd(const T* X, const T* Y, const T* vx, const T* vy, int B, int
   const size_t need = (size_t)B * N * M * sizeof(T);
   if (!ws || ws_bytes < need)
     return fail(TW_ESIZE, "%s: workspace of %zu bytes needed", what, need);
-  if (band_feat_path(N, M, D, band)) return band_feat_fwd<T>(a, X, Y, D, B, ws, s, what);
+  if (banded) return band_feat_fwd<T>(a, X, Y, D, B, ws, s, what);
   if (int e = sqdist_raw<T>(X, Y, B, N, M, D, ws, s, what)) return e;
   a.C = ws;
   return launch_pen<T, SRC_SQ>(pen, false, a, B, s, what);
@@ -289,6 +292,15 @@ static int feat_bwd(const T* X, const T* Y, const T* vx, const T* vy, const T* R
   a.rd = carry_double<T>(N, M, gamma);
   set_hyper(a, gamma, beta, eps, band);
   set_sigma(a, sigma);
+  // a band narrower than the grid: the forward left the band's cost and
+  // penalty in its workspace and R / P band-compressed (D = 1 too); the
+  // workspace takes dC, dQ (and C, rebuilt when the forward's is not given)
+  if (band_feat_path(N, M, D, band)) {
+    const size_t need = (size_t)B * N * M * sizeof(T);
+    if (!ws || ws_bytes < need)
+      return fail(TW_ESIZE, "%s: workspace of %zu bytes needed", what, need);
+    return band_feat_bwd<T>(a, X, Y, D, B, ws_fwd, ws, dX, dY, s, what);
+  }
   // workspace: the S / dS plane (D > 1), then the MW hand-off records
   const size_t sp = splane_bytes<T>(B, N, M, D), hb = mw_hand_bytes<T>(B, N, M);
   const size_t need = hb ? align8(sp) + hb : sp;
@@ -303,10 +315,6 @@ static int feat_bwd(const T* X, const T* Y, const T* vx, const T* vy, const T* R
     a.dY = dY;
     return launch_pen<T, SRC_FEAT1>(pen, true, a, B, s, what);
   }
-  // a band narrower than the grid: the forward left the band's cost and
-  // penalty in its workspace and R / P band-compressed
-  if (band_feat_path(N, M, D, band))
-    return band_feat_bwd<T>(a, X, Y, D, B, ws_fwd, ws, dX, dY, s, what);
   // the raw squared distances: the forward's, or recomputed into the
   // workspace; the sweep writes their adjoint into the workspace (in place
   // when they are there: each cell is read and written by the same thread)
@@ -335,6 +343,14 @@ size_t tw_udtw_feat_workspace_bytes(int B, int N, int M, int D, int elem_size) {
   const size_t sp = D > 1 ? (size_t)B * N * M * (size_t)elem_size : 0;
   const size_t hb = elem_size == 4 ? mw_hand_bytes<float>(B, n, m) : mw_hand_bytes<double>(B, n, m);
   return hb ? align8(sp) + hb : sp;
+}
+
+size_t tw_udtw_feat_band_workspace_bytes(int B, int N, int M, int D, double bandwidth,
+                                         int elem_size) {
+  if (B <= 0 || N <= 0 || M <= 0 || D <= 0 || (elem_size != 4 && elem_size != 8)) return 0;
+  const int n = N < M ? N : M, m = N < M ? M : N;
+  if (band_feat_path(n, m, D, bandwidth)) return (size_t)B * N * M * (size_t)elem_size;
+  return tw_udtw_feat_workspace_bytes(B, N, M, D, elem_size);
 }
 
 size_t tw_udtw_cost_workspace_bytes(int B, int N, int M, int elem_size) {

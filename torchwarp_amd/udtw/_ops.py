@@ -90,15 +90,20 @@ register_autocast(dp_backward)
 # --------------------------------------------------------- from features
 
 
-def _feat_ws(X, N, M):
-    """The squared-distance plane [B, N*M] of D > 1 (empty for D == 1)."""
-    return X.new_empty(X.shape[0], N * M) if X.shape[2] > 1 else X.new_empty(0)
+def _feat_ws(X, N, M, bandwidth):
+    """The forward's plane [B, N*M]: the squared distances (D > 1) or, with a
+    band narrower than the grid, the banded path's cost and penalty (D = 1
+    too); empty when the forward needs none."""
+    B, D = X.shape[0], X.shape[2]
+    return (X.new_empty(B, N * M) if _hip.udtw_feat_plane(B, N, M, D, X.dtype, bandwidth)
+            else X.new_empty(0))
 
 
-def _feat_bwd_ws(X, N, M):
-    """The backward's workspace: the squared-distance plane (D > 1), then the
-    hand-off records of long sequences (empty when neither is needed)."""
-    n = _hip.udtw_workspace_elems(X.shape[0], N, M, X.shape[2], X.dtype)
+def _feat_bwd_ws(X, N, M, bandwidth):
+    """The backward's workspace: the squared-distance plane (D > 1) or the
+    banded path's gradient planes, then the hand-off records of long
+    sequences (empty when none is needed)."""
+    n = _hip.udtw_workspace_elems(X.shape[0], N, M, X.shape[2], X.dtype, bandwidth)
     return X.new_empty(n) if n else X.new_empty(0)
 
 
@@ -124,7 +129,7 @@ def fused(X: Tensor, Y: Tensor, vx: Tensor, vy: Tensor, gamma: float, beta: floa
     R = X.new_empty(B, _hip.carry_cols(N, M, gamma, X.dtype))
     P = X.new_empty(B, N * M) if pen else X.new_empty(0)
     out_r, out_p = X.new_empty(B), X.new_empty(B)
-    S = _feat_ws(X, N, M)
+    S = _feat_ws(X, N, M, bandwidth)
     _hip.call("tw_udtw_feat_fwd", X.dtype, X, Y, vx, vy, B, N, M, D, gamma, beta, eps, bandwidth,
               int(sigma), R, P, out_r, out_p, *_ws_args(S))
     return out_r, out_p, R, P, S
@@ -134,7 +139,7 @@ def fused(X: Tensor, Y: Tensor, vx: Tensor, vy: Tensor, gamma: float, beta: floa
 def _(X, Y, vx, vy, gamma, beta, eps, bandwidth, backend, sigma):
     B, N, M = X.shape[0], X.shape[1], Y.shape[1]
     P = X.new_empty(B, N * M) if beta != 0.0 else X.new_empty(0)
-    S = X.new_empty(B, N * M) if X.shape[2] > 1 else X.new_empty(0)
+    S = _feat_ws(X, N, M, bandwidth)
     R = X.new_empty(B, _hip.carry_cols(N, M, gamma, X.dtype))
     return X.new_empty(B), X.new_empty(B), R, P, S
 
@@ -151,9 +156,8 @@ def fused_backward(X: Tensor, Y: Tensor, vx: Tensor, vy: Tensor, R: Tensor, P: T
     pen = beta != 0.0
     dX, dY = torch.empty_like(X), torch.empty_like(Y)
     dvx, dvy = torch.empty_like(vx), torch.empty_like(vy)
-    ws = _feat_bwd_ws(X, N, M)
-    S = S if (D > 1 and S.shape == (B, N * M) and S.dtype == X.dtype
-              and S.is_contiguous()) else None
+    ws = _feat_bwd_ws(X, N, M, bandwidth)
+    S = S if (S.shape == (B, N * M) and S.dtype == X.dtype and S.is_contiguous()) else None
     grads, gs = _hip.per_pair(*(_hip.dense(X.dtype, grad_r, grad_p, contiguous=False) if pen
                                 else _hip.dense(X.dtype, grad_r, contiguous=False)))
     _hip.call("tw_udtw_feat_bwd", X.dtype, X, Y, vx, vy, R, P if pen else None, grads[0],
