@@ -1255,34 +1255,38 @@ __global__ void __launch_bounds__(256) band_gather(const T* __restrict__ C,
   const int RW = 2 * w + 1;   // row-local columns: c = j - (i - w)
   const int rows = N - i0 < kGatherRows ? N - i0 : kGatherRows;
   const size_t nm = (size_t)N * M;
-  for (int q = 0; q < (PEN ? 2 : 1); ++q) {
-    const T* src = (q ? Q : C) + b * nm;
-    T* dst = (q ? Qb : Cb) + (size_t)b * D * NS;
-    if (q) __syncthreads();
-    // (a thread's column c of all 32 rows loaded before any is stored, so
-    // the rows' loads are in flight together; 8 diagonals x 32 rows per
-    // pass of the threads on the way out)
-    for (int c = threadIdx.x; c < RW; c += blockDim.x) {
-      T v[kGatherRows];
+  constexpr int NP = PEN ? 2 : 1;
+  const T* src[2] = {C + b * nm, PEN ? Q + b * nm : nullptr};
+  T* dst[2] = {Cb + (size_t)b * D * NS, PEN ? Qb + (size_t)b * D * NS : nullptr};
+  // (a thread's column c of all 32 rows, of both planes, loaded before any is
+  // stored, so the loads are in flight together; 8 diagonals x 32 rows per
+  // pass of the threads on the way out)
+  for (int c = threadIdx.x; c < RW; c += blockDim.x) {
+    T v[NP][kGatherRows];
 #pragma unroll
-      for (int r = 0; r < kGatherRows; ++r) {
-        const int i = i0 + r, j = i - w + c;
-        v[r] = (r < rows && j >= 0 && j < M) ? src[(size_t)i * M + j] : (T)0;
-      }
+    for (int r = 0; r < kGatherRows; ++r) {
+      const int i = i0 + r, j = i - w + c;
+      const bool in = r < rows && j >= 0 && j < M;
+#pragma unroll
+      for (int q = 0; q < NP; ++q) v[q][r] = in ? src[q][(size_t)i * M + j] : (T)0;
+    }
+#pragma unroll
+    for (int q = 0; q < NP; ++q)
 #pragma unroll
       for (int r = 0; r < kGatherRows; ++r)
-        if (r < rows) tile[r * RW + c] = v[r];
-    }
-    __syncthreads();
-    // diagonals 2 i0 - w .. 2 (i0 + rows - 1) + w, rows r of each
-    const int dlo = 2 * i0 - w, nd = 2 * (rows - 1) + RW;
-    const int r = threadIdx.x & (kGatherRows - 1);
-    for (int dd = threadIdx.x / kGatherRows; dd < nd; dd += blockDim.x / kGatherRows) {
-      const int d = dlo + dd, i = i0 + r, j = d - i;
-      const int l = i - j + w;
-      if (r >= rows || d < 0 || d >= D || j < 0 || j >= M || l < 0 || l > 2 * w) continue;
-      dst[(size_t)d * NS + (l >> 1)] = tile[r * RW + (j - i + w)];
-    }
+        if (r < rows) tile[(q * kGatherRows + r) * RW + c] = v[q][r];
+  }
+  __syncthreads();
+  // diagonals 2 i0 - w .. 2 (i0 + rows - 1) + w, rows r of each
+  const int dlo = 2 * i0 - w, nd = 2 * (rows - 1) + RW;
+  const int r = threadIdx.x & (kGatherRows - 1);
+  for (int dd = threadIdx.x / kGatherRows; dd < nd; dd += blockDim.x / kGatherRows) {
+    const int d = dlo + dd, i = i0 + r, j = d - i;
+    const int l = i - j + w;
+    if (r >= rows || d < 0 || d >= D || j < 0 || j >= M || l < 0 || l > 2 * w) continue;
+#pragma unroll
+    for (int q = 0; q < NP; ++q)
+      dst[q][(size_t)d * NS + (l >> 1)] = tile[(q * kGatherRows + r) * RW + (j - i + w)];
   }
 }
 
@@ -1302,14 +1306,15 @@ int band_cost_fwd(const UdtwArgs<T>& u, int B, hipStream_t s, const char* what) 
   const size_t room = (size_t)B * u.N * u.M * rs;
   const size_t need = (size_t)B * D * NS * sizeof(T) * (pen ? 2 : 1);
   char* tail = reinterpret_cast<char*>(u.R) + planes;
-  if (planes + need > room || ((uintptr_t)tail & 15) != 0 ||
+  // the gather's tile: 32 rows of 2 w + 1 columns of each plane
+  const size_t lds = (size_t)(pen ? 2 : 1) * kGatherRows * (2 * w + 1) * sizeof(T);
+  if (planes + need > room || ((uintptr_t)tail & 15) != 0 || lds > (size_t)max_lds_bytes() ||
       (long long)u.N * u.M * (long long)rs >= (1LL << 31))
     return band_sweep<T>(false, u, B, s, what);   // (which also reports the size limit)
   T* Cb = reinterpret_cast<T*>(tail);
   T* Qb = pen ? Cb + (size_t)B * D * NS : nullptr;
   const int ntile = (u.N + kGatherRows - 1) / kGatherRows;
   const dim3 grid(xcd_grid(ntile, B));
-  const size_t lds = (size_t)kGatherRows * (2 * w + 1) * sizeof(T);
   if (pen)
     hipLaunchKernelGGL((band_gather<T, true>), grid, dim3(256), lds, s, u.C, u.Q, Cb, Qb, B, u.N,
                        u.M, w, NS, D, ntile);
