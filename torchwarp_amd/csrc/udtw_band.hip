@@ -1354,33 +1354,40 @@ __global__ void __launch_bounds__(256) band_scatter(const T* __restrict__ dCb,
   const int dlo = 2 * i0 - w, nd = 2 * (rows - 1) + RW;
   const int r = threadIdx.x & (kGatherRows - 1);
   constexpr int DPASS = 256 / kGatherRows, UN = 8;
-  for (int q = 0; q < (PEN ? 2 : 1); ++q) {
-    const T* src = (q ? dQb : dCb) + (size_t)b * D * NS;
-    T* dst = (q ? dQ : dC) + b * nm;
-    if (q) __syncthreads();
-    for (int dd0 = threadIdx.x / kGatherRows; dd0 < nd; dd0 += DPASS * UN) {
-      T v[UN];
-      int e[UN];
+  constexpr int NP = PEN ? 2 : 1;
+  const T* src[2] = {dCb + (size_t)b * D * NS, PEN ? dQb + (size_t)b * D * NS : nullptr};
+  T* dst[2] = {dC + b * nm, PEN ? dQ + b * nm : nullptr};
+  // both planes' diagonal runs in flight together (UN per plane and lane)
+  for (int dd0 = threadIdx.x / kGatherRows; dd0 < nd; dd0 += DPASS * UN) {
+    T v[NP][UN];
+    int e[UN];
 #pragma unroll
-      for (int k = 0; k < UN; ++k) {
-        const int dd = dd0 + DPASS * k;
-        const int d = dlo + dd, i = i0 + r, j = d - i;
-        const int l = i - j + w;
-        const bool in = dd < nd && r < rows && d >= 0 && d < D && j >= 0 && j < M && l >= 0 &&
-                        l <= 2 * w;
-        v[k] = in ? src[(size_t)d * NS + (l >> 1)] : (T)0;
-        e[k] = in ? r * RW + (j - i + w) : -1;
-      }
+    for (int k = 0; k < UN; ++k) {
+      const int dd = dd0 + DPASS * k;
+      const int d = dlo + dd, i = i0 + r, j = d - i;
+      const int l = i - j + w;
+      const bool in = dd < nd && r < rows && d >= 0 && d < D && j >= 0 && j < M && l >= 0 &&
+                      l <= 2 * w;
 #pragma unroll
-      for (int k = 0; k < UN; ++k)
-        if (e[k] >= 0) tile[e[k]] = v[k];
+      for (int q = 0; q < NP; ++q) v[q][k] = in ? src[q][(size_t)d * NS + (l >> 1)] : (T)0;
+      e[k] = in ? r * RW + (j - i + w) : -1;
     }
-    __syncthreads();
-    for (int rr = 0; rr < rows; ++rr) {
-      const int i = i0 + rr;
-      for (int c = threadIdx.x; c < RW; c += blockDim.x) {
-        const int j = i - w + c;
-        if (j >= 0 && j < M) dst[(size_t)i * M + j] = tile[rr * RW + c];
+#pragma unroll
+    for (int k = 0; k < UN; ++k)
+      if (e[k] >= 0) {
+#pragma unroll
+        for (int q = 0; q < NP; ++q) tile[q * kGatherRows * RW + e[k]] = v[q][k];
+      }
+  }
+  __syncthreads();
+  for (int rr = 0; rr < rows; ++rr) {
+    const int i = i0 + rr;
+    for (int c = threadIdx.x; c < RW; c += blockDim.x) {
+      const int j = i - w + c;
+      if (j >= 0 && j < M) {
+#pragma unroll
+        for (int q = 0; q < NP; ++q)
+          dst[q][(size_t)i * M + j] = tile[(q * kGatherRows + rr) * RW + c];
       }
     }
   }
@@ -1403,18 +1410,19 @@ int band_cost_bwd(const UdtwArgs<T>& u, int B, hipStream_t s, const char* what, 
   // the band layout's planes, 16-byte aligned within the workspace
   T* base = ws ? reinterpret_cast<T*>(((uintptr_t)ws + 15) & ~(uintptr_t)15) : nullptr;
   const size_t skip = ws ? (size_t)(reinterpret_cast<char*>(base) - reinterpret_cast<char*>(ws)) : 0;
-  if (!ws || ws_bytes < skip + (pen ? 2 : 1) * pl * sizeof(T))
+  const int w = (int)u.band;
+  // the scatter's tile: 32 rows of 2 w + 1 columns of each plane
+  const size_t lds = (size_t)(pen ? 2 : 1) * kGatherRows * (2 * w + 1) * sizeof(T);
+  if (!ws || ws_bytes < skip + (pen ? 2 : 1) * pl * sizeof(T) || lds > (size_t)max_lds_bytes())
     return band_sweep<T>(true, u, B, s, what);   // gradients straight into [B, N, M]
   UdtwArgs<T> a = u;
   a.dC = base;
   a.dQ = pen ? base + pl : nullptr;
   if (int e = band_sweep<T>(true, a, B, s, what, true, u.dC, pen ? u.dQ : nullptr)) return e;
-  const int w = (int)u.band;
   const int S = band_slots(w);
   const int NS = (w + 1 + S - 1) / S * S, D = u.N + u.M - 1;
   const int ntile = (u.N + kGatherRows - 1) / kGatherRows;
   const dim3 grid(xcd_grid(ntile, B));
-  const size_t lds = (size_t)kGatherRows * (2 * w + 1) * sizeof(T);
   if (pen)
     hipLaunchKernelGGL((band_scatter<T, true>), grid, dim3(256), lds, s, a.dC, a.dQ, u.dC, u.dQ,
                        B, u.N, u.M, w, NS, D, ntile);
