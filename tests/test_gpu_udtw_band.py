@@ -32,6 +32,9 @@ CASES = [  # (B, N, M, gamma, bandwidth, penalty, dtype)
     (2, 300, 300, 0.7, 37.0, True, f64),       # odd width
     (2, 400, 380, 0.5, 100.0, True, f64),      # two slots per lane, N > M
     (1, 600, 640, 1.0, 200.0, True, f64),      # four slots per lane
+    (1, 1200, 1200, 1.0, 200.0, True, f64),    # banded, but 32 rows of 2w + 1
+                                               # columns of both planes exceed
+                                               # the LDS: no gather / scatter
     (2, 250, 260, 0.3, 12.5, True, f64),       # fractional width
     (2, 300, 320, 0.5, 24.0, False, f64),      # soft-DTW
     (2, 150, 170, 0.5, 20.0, True, f64),       # |N - M| = width
