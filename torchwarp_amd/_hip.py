@@ -225,7 +225,12 @@ def udtw_feat_plane(B, N, M, D, dtype=torch.float32, bandwidth=0.0):
     """Whether a feature-path uDTW forward needs its B*N*M-element workspace
     plane: the squared distances (D > 1), or the banded path's cost and
     penalty (D = 1 with a band narrower than the grid)."""
-    return D > 1 or udtw_workspace_elems(B, N, M, D, dtype, bandwidth) >= B * N * M
+    if D > 1:
+        return True
+    if not bandwidth or bandwidth <= 0:
+        return False
+    B, N, M, D = int(B), int(N), int(M), int(D)   # concrete sizes for the C query
+    return udtw_workspace_elems(B, N, M, D, dtype, bandwidth) >= B * N * M
 
 
 def udtw_cost_workspace_elems(B, N, M, dtype=torch.float32, bandwidth=0.0):
